@@ -1,0 +1,215 @@
+/*
+ * sox_abi.h - kernel argument blocks of the gfx950 code objects (one definition, shared by the
+ * kernels, the host backend and any other host that launches them through sox_launch).
+ *
+ * Each kernel takes exactly one of these structs by value, so its kernarg segment IS the struct:
+ * a host fills it and passes its bytes to sox_launch (hipModuleLaunchKernel with
+ * HIP_LAUNCH_PARAM_BUFFER_POINTER). Field order is device pointers first, then the parameter
+ * block, mirroring the reference's binding order + push-constant struct for the matching shader
+ * (e.g. Backends/Vulkan/Shaders/conv_cm.comp:86-91 and its ND(...) call, Backends/Vulkan/VkGraph.cs:664-674).
+ *
+ * Storage types: "act" tensors are fp16 on fp16 graphs and fp32 on fp32 graphs; bias, norm and
+ * SE parameters are always fp32 (ConstKind.F32, Engine/Extensions.cs:145).
+ */
+#ifndef SOX_ABI_H
+#define SOX_ABI_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ActivationKind (Engine/ExecPlan.cs:42). */
+enum sox_act { SOX_ACT_NONE = 0, SOX_ACT_RELU = 1, SOX_ACT_SIGMOID = 2, SOX_ACT_GELU = 3, SOX_ACT_HARDSWISH = 4, SOX_ACT_SWISH = 5 };
+
+/* Epilogue flag bits, conv_cm's layout (VkGraph.cs:667-669): bias=1, residual=2, reflect=4, act<<4. */
+#define SOX_F_BIAS 1
+#define SOX_F_RESIDUAL 2
+#define SOX_F_REFLECT 4
+#define SOX_F_ACT_SHIFT 4
+#define SOX_F_ACT_MASK 0xF0
+#define SOX_F_DENSE_A 0x100 /* A is a plain row-major [M][lda] matrix (Gemm), not an NHWC image */
+
+/*
+ * Implicit-GEMM convolution / Gemm with fused epilogue (conv_cm.comp, gemm.comp).
+ *   M = n*oh*ow output pixels (or Gemm rows), N = oc, K = kh*kw*ic (tap-major, channel fastest).
+ *   w is [N][kpad] (k fastest: ConstKind.ConvWT / GemmNK, Engine/Extensions.cs:150-153).
+ *   y[m*ldy + n] = act(sum_k A[m,k] w[n,k] (+ bias[n]) (+ add[m*ldy + n]))
+ * Grid: (ceil(M/BM), ceil(N/BN)); 256 threads.
+ */
+typedef struct sox_igemm_args {
+    const void* x;
+    const void* w;
+    const float* bias;
+    const void* add;
+    void* y;
+    int32_t m, n, k, kpad;
+    int32_t ih, iw, ic, oh, ow;
+    int32_t kh, kw, sh, sw, pt, pl;
+    int32_t flags;
+    float pad_value;
+    int32_t ldy;  /* output / residual row stride in elements (n, or a concat channel total) */
+    int32_t lda;  /* SOX_F_DENSE_A: A row stride in elements */
+    int32_t tiles_n; /* ceil(N/BN): tile-order remap of the 1-D grid */
+} sox_igemm_args;
+
+/*
+ * Depthwise k x k conv, NHWC (depthwise.comp; Kernels/Nhwc.cs:496-631).
+ *   w is [tap][c] (ConstKind.DwW). acc = bias[c] + sum_tap x * w; act.
+ * Grid: 1-D over n*oh*ow*(c/cvec) work items.
+ */
+typedef struct sox_dw_args {
+    const void* x;
+    const void* w;
+    const float* bias;
+    const void* add;
+    void* y;
+    int32_t n, c, ih, iw, oh, ow;
+    int32_t kh, kw, sh, sw, pt, pl;
+    int32_t flags;
+    float pad_value;
+} sox_dw_args;
+
+/*
+ * ConvTranspose with stride == kernel, no pad, group 1 (convt.comp; Kernels/Nhwc.Det.cs:51-131).
+ *   w is [tap][ic][oc] (ConstKind.ConvTW). out[(y*kh+dy), (x*kw+dx), o] = act(b[o] + sum_c x[y,x,c] w[tap][c][o]).
+ */
+typedef struct sox_convt_args {
+    const void* x;
+    const void* w;
+    const float* bias;
+    void* y;
+    int32_t n, ih, iw, ic, oc, kh, kw;
+    int32_t flags;
+} sox_convt_args;
+
+/* Per-channel mean partials over pixel chunks (gap_part.comp): part[n][chunk][c] (fp32). */
+typedef struct sox_gap_args {
+    const void* x;
+    float* part;
+    int32_t n, hw, c, chunks;
+} sox_gap_args;
+
+/*
+ * Squeeze-excitation gate (se_gate.comp; Kernels/Nhwc.Det.cs:287-314), one workgroup per image:
+ *   mean = sum(part)/hw; hid = act1(b1 + W1 mean); z = b2 + W2 hid; s = gate(z) + offset  (out [n][c]).
+ */
+typedef struct sox_se_args {
+    const float* part;
+    const float* w1;
+    const float* b1;
+    const float* w2;
+    const float* b2;
+    void* s; /* [n][c] in the graph's storage type */
+    int32_t c, r, chunks, hw;
+    int32_t flags; /* bit0 b1, bit1 b2, bit2 act1 relu, bit3 hard */
+    float alpha, beta, offset;
+} sox_se_args;
+
+/* out[p, c] = act(x[p, c] op v[img(p), c]): NHWC per-channel broadcast (ew2 / ChannelBroadcast). */
+typedef struct sox_chan_args {
+    const void* x;
+    const void* v; /* [n][c], storage type */
+    void* y;
+    int64_t rows;  /* n*h*w */
+    int32_t c, hw;
+    int32_t op;    /* EwOp: 0 add, 1 sub, 2 mul, 3 div */
+    int32_t flags; /* bit0 reversed operands, act<<4 */
+} sox_chan_args;
+
+/* Same-shape elementwise binary op + act (ew2v.comp). */
+typedef struct sox_ew_args {
+    const void* a;
+    const void* b;
+    void* y;
+    int64_t count;
+    int32_t op;
+    int32_t flags; /* act<<4 */
+} sox_ew_args;
+
+/* Unary activation / affine (unary.comp, unary2.comp, hsig.comp): y = act(alpha*x + beta) or hard-sigmoid. */
+typedef struct sox_unary_args {
+    const void* x;
+    void* y;
+    int64_t count;
+    int32_t mode;  /* 0 act, 1 affine alpha*x+beta, 2 hard-sigmoid clamp(alpha*x+beta,0,1), 3 copy */
+    int32_t act;
+    float alpha, beta;
+} sox_unary_args;
+
+/* Nearest resize (asymmetric, floor) + optional [relu] addend (nearest.comp; Nhwc.Det.cs:167-204). */
+typedef struct sox_nearest_args {
+    const void* x;
+    const void* add;
+    void* y;
+    int32_t n, ih, iw, c, oh, ow;
+    float sy, sx;
+    int32_t flags; /* bit0 addend, bit1 relu on addend */
+    int32_t ldy, y_off; /* output pixel stride and channel offset (writes a concat slice) */
+} sox_nearest_args;
+
+/* Channel-slice copy: y[p*ldy + y_off + c] = x[p*c_in + c] (concat_ax.comp, NHWC channel concat). */
+typedef struct sox_slice_copy_args {
+    const void* x;
+    void* y;
+    int64_t rows;
+    int32_t c, ldy, y_off;
+} sox_slice_copy_args;
+
+/* fp32 <-> fp16 staging conversion (f32to16.comp / f16to32.comp). */
+typedef struct sox_cvt_args {
+    const void* x;
+    void* y;
+    int64_t count;
+} sox_cvt_args;
+
+/* LayerNorm over the innermost dim, one wave per row (layernorm.comp; Kernels/Ops.cs:544-574). */
+typedef struct sox_ln_args {
+    const void* x;
+    const float* gamma;
+    const float* beta;
+    void* y;
+    int64_t rows;
+    int32_t len;
+    float eps;
+} sox_ln_args;
+
+/* Row softmax over the innermost dim (softmax.comp; Kernels/Ops.Seq.cs:28-72). */
+typedef struct sox_softmax_args {
+    const void* x;
+    void* y;
+    int64_t rows;
+    int32_t len;
+    int32_t pad;
+} sox_softmax_args;
+
+/*
+ * Fused attention (attn.comp): out[b,h,t,:] = sum_s softmax_s(scale q.k) v over strided views.
+ * Element (b, h, t, d) of operand i lives at base_i + b*sb_i + h*sh_i + t*st_i + d (d contiguous).
+ */
+typedef struct sox_attn_args {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    int32_t batch, heads, t, s, d;
+    float scale;
+    int64_t q_sb, q_sh, q_st;
+    int64_t k_sb, k_sh, k_st;
+    int64_t v_sb, v_sh, v_st;
+    int64_t o_sb, o_sh, o_st;
+} sox_attn_args;
+
+/* 2x2/2 max pool (+relu) of an NHWC tensor (the ConvP.Pool epilogue when it runs as its own pass). */
+typedef struct sox_pool_args {
+    const void* x;
+    void* y;
+    int32_t n, ih, iw, c, oh, ow;
+    int32_t kh, kw, sh, sw, pt, pl;
+    int32_t flags; /* bit0 relu */
+} sox_pool_args;
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,164 @@
+/*
+ * sox_backend.h - the HIP backend behind SimdOnnx's backend surface, as a C ABI.
+ *
+ * It mirrors the reference's three-class GPU backend surface and its extension hook:
+ *   HipBackend          <- VkBackend (Backends/Vulkan/VkBackend.cs:11-267): device, Default /
+ *                          TryGetDefault, IsLost, graph building
+ *   HipGraphModel       <- VkGraphModel (Backends/Vulkan/VkGraph.cs:44-1233): const packing and
+ *                          upload, one Emit per ExecNode producing dispatch records
+ *   HipInferenceSession <- VkInferenceSession (Backends/Vulkan/VkSession.cs:63-571): one arena
+ *                          slab, mapped fp32 staging, Run / Submit / Wait, DebugProfile
+ *   ext emit hook       <- ExtOp.EmitVulkan + VkGraphModel.Dispatch (Engine/Extensions.cs:41-50,
+ *                          VkGraph.cs:1117-1123)
+ * The plan a caller hands over is the reference's ExecPlan (Engine/ExecPlan.cs:235-317) as the
+ * unchanged GraphCompiler produced it for PlanTarget.Hip: values (shape, physical layout, arena
+ * buffer or const data), nodes (ExecOp + value ids + the op's parameter record) and the arena plan.
+ * All status codes are those of sox_hip.h.
+ */
+#ifndef SOX_BACKEND_H
+#define SOX_BACKEND_H
+#include <stddef.h>
+#include <stdint.h>
+
+#include "sox_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct sox_plan sox_plan;
+typedef struct sox_backend sox_backend;
+typedef struct sox_graph sox_graph;
+typedef struct sox_session sox_session;
+
+/* ExecOp, numbered as Engine/ExecPlan.cs:4-40. */
+enum sox_exec_op {
+    SOX_OP_CONV = 0, SOX_OP_MAXPOOL = 1, SOX_OP_ELEMENTWISE = 2, SOX_OP_RELU = 3, SOX_OP_SIGMOID = 4,
+    SOX_OP_ERF = 5, SOX_OP_GELU = 6, SOX_OP_LAYERNORM = 7, SOX_OP_GEMM = 8, SOX_OP_RESIZE_BILINEAR = 9,
+    SOX_OP_PAD = 10, SOX_OP_TRANSPOSE = 11, SOX_OP_SLICE = 12, SOX_OP_CONCAT = 13, SOX_OP_COPY = 14,
+    SOX_OP_HARD_SIGMOID = 15, SOX_OP_GLOBAL_AVG_POOL = 16, SOX_OP_CONV_TRANSPOSE = 17, SOX_OP_RESIZE_NEAREST = 18,
+    SOX_OP_MATMUL = 19, SOX_OP_SOFTMAX = 20, SOX_OP_REDUCE_MEAN = 21, SOX_OP_SQRT = 22, SOX_OP_AVGPOOL = 23,
+    SOX_OP_HARDSWISH = 24, SOX_OP_SWISH = 25, SOX_OP_EXT = 26, SOX_OP_CHANNEL_GATE = 27, SOX_OP_ATTENTION = 28,
+    SOX_OP_LEAKY_RELU = 29, SOX_OP_TANH = 30, SOX_OP_CLIP = 31, SOX_OP_DEPTH_TO_SPACE = 32, SOX_OP_SPACE_TO_DEPTH = 33
+};
+
+/* Parameter records (Engine/ExecPlan.cs:50-199), value ids -1 = none. */
+typedef struct sox_conv_p {          /* ConvP :50-65 */
+    int32_t pads[4];                 /* top, left, bottom, right */
+    int32_t strides[2], dilations[2], kernel[2];
+    int32_t group, act, pad_mode;    /* pad_mode: 0 constant, 1 reflect */
+    float pad_value;
+    int32_t bias_value, add_value;
+    int32_t has_pool;                /* ConvP.Pool: fused 2x2/2 max pool, Out[0] is the pooled tensor */
+    int32_t pool_kernel[2], pool_strides[2], pool_pads[4];
+    int32_t pool_relu;
+} sox_conv_p;
+
+typedef struct sox_pool_p {          /* PoolP :67-74 */
+    int32_t kernel[2], strides[2], pads[4];
+    int32_t fuse_relu, count_include_pad;
+} sox_pool_p;
+
+typedef struct sox_ew_p { int32_t op, act; } sox_ew_p;                      /* EwP :76-80 */
+typedef struct sox_ln_p { float eps; } sox_ln_p;                            /* LnP :82-85 */
+typedef struct sox_gemm_p { int32_t trans_b, bias_value, act; } sox_gemm_p; /* GemmP :87-93 */
+typedef struct sox_hard_sigmoid_p { float alpha, beta; } sox_hard_sigmoid_p; /* :103-106 */
+typedef struct sox_convt_p { int32_t kernel[2]; int32_t bias_value, act; } sox_convt_p; /* ConvTP :108-114 */
+typedef struct sox_resize_nearest_p { float scales[4]; int32_t add_relu; } sox_resize_nearest_p; /* :116-121 */
+typedef struct sox_concat_p { int32_t axis; } sox_concat_p;                 /* ConcatP :196-199 */
+typedef struct sox_channel_gate_p {                                          /* ChannelGateP :151-158 */
+    int32_t b1, b2, act1, hard;
+    float alpha, beta, offset;
+} sox_channel_gate_p;
+typedef struct sox_attention_p {                                             /* AttentionP :166-174 */
+    float scale;
+    int32_t dims[3][4];              /* per operand: logical axes holding (n, h, t|s, d), -1 = size 1 */
+    int32_t fix_axis[3], fix_index[3];
+    int32_t out_layout[4];           /* physical order of the [n,h,t,d] output; all -1 = identity */
+} sox_attention_p;
+
+/* ---- plan (ExecPlan) ---- */
+int sox_plan_create(sox_plan** plan);
+void sox_plan_destroy(sox_plan* plan);
+/* CValue (ExecPlan.cs:202-220). shape = logical dims; layout = physical order (layout[i] = the
+ * logical dim stored at physical position i; NULL = identity); buf >= 0: activation buffer id,
+ * else a const whose nfloats floats are copied. */
+int sox_plan_add_value(sox_plan* plan, const int32_t* shape, int32_t rank, const int32_t* layout, int32_t buf,
+                       const float* floats, int64_t nfloats, const char* name, int32_t* id);
+/* ExecNode (ExecPlan.cs:235-276); params is the op's record above (bytes copied). Ext nodes pass
+ * the extension op's registered name as `ext_name` and an opaque params blob. */
+int sox_plan_add_node(sox_plan* plan, int32_t op, const int32_t* in, int32_t nin, const int32_t* out, int32_t nout,
+                      const void* params, size_t params_bytes, const char* ext_name, int32_t* id);
+/* ExecPlan.BufOffset / ArenaFloats (ExecPlan.cs:283-285): offsets in elements. */
+int sox_plan_set_arena(sox_plan* plan, const int64_t* buf_offset, int32_t nbuf, int64_t arena_floats);
+int sox_plan_set_io(sox_plan* plan, const int32_t* inputs, int32_t ninputs, int32_t output);
+
+/* ---- backend (VkBackend) ---- */
+int sox_backend_default(sox_backend** backend);   /* Default: device 0, re-created after a device loss */
+int sox_backend_info(sox_backend* backend, sox_device_info* info);
+int sox_backend_is_lost(sox_backend* backend);
+/* Loads an extension's code object (an embedded resource of its owner, ShaderResources.Open). */
+int sox_backend_load_module(sox_backend* backend, const void* image, size_t bytes, void** module);
+
+/* ---- extension ops (ExtOp.EmitVulkan analogue) ---- */
+typedef struct sox_bind { int32_t slot; int32_t pad_; uint64_t offset, size; } sox_bind; /* VkBind, VkGraph.cs:12-21 */
+enum { SOX_SLOT_ARENA = 0, SOX_SLOT_CONSTS = 1, SOX_SLOT_DUMMY = 2 };
+/* ConstKind (Engine/Extensions.cs:144-159) as an id. */
+enum { SOX_CK_RAW = 0, SOX_CK_F32 = 1, SOX_CK_CONVWT = 2, SOX_CK_GEMMNK = 3, SOX_CK_DWW = 4, SOX_CK_CONVTW = 5 };
+typedef int (*sox_ext_emit_fn)(void* user, sox_graph* graph, int32_t node);
+typedef int (*sox_ext_consts_fn)(void* user, const sox_plan* plan, int32_t node, int32_t* values, int32_t* kinds,
+                                 int32_t cap); /* GpuConsts: returns the count written */
+int sox_backend_register_ext(sox_backend* backend, const char* name, sox_ext_emit_fn emit, sox_ext_consts_fn consts,
+                             void* user);
+/* Inside an emit callback: Bind(valueId, kind) and Dispatch(n, kernel, binds, params, grid). The
+ * kernarg block is the binds' device addresses (8 bytes each, in order) followed by params. */
+int sox_graph_bind(sox_graph* graph, int32_t value, int32_t const_kind, sox_bind* out);
+int sox_graph_scratch(sox_graph* graph, uint64_t bytes, sox_bind* out);
+int sox_graph_dispatch(sox_graph* graph, int32_t node, void* module, const char* kernel, const sox_bind* binds,
+                       int32_t nbinds, const void* params, size_t params_bytes, const uint32_t grid[3],
+                       const uint32_t block[3], uint32_t lds_bytes);
+int sox_graph_node_info(sox_graph* graph, int32_t node, int32_t* op, const void** params, size_t* params_bytes);
+int sox_graph_value_shape(sox_graph* graph, int32_t value, int32_t* phys_shape, int32_t cap, int32_t* rank);
+int sox_graph_is_f16(sox_graph* graph);
+
+/* ---- graph model (VkGraphModel) ---- */
+/* Builds the dispatch list of a plan: f16 = fp16 activation/weight storage with fp32 math (the
+ * reference GPU contract, Backends/Vulkan/VkGraph.cs:33-43), else fp32 storage. */
+int sox_graph_create(sox_backend* backend, const sox_plan* plan, int32_t f16, sox_graph** graph);
+void sox_graph_release(sox_graph* graph);
+int sox_graph_dispatch_count(sox_graph* graph);
+int sox_graph_dispatch_info(sox_graph* graph, int32_t index, char* name, size_t name_cap, uint32_t grid[3],
+                            int32_t* node);
+uint64_t sox_graph_arena_bytes(sox_graph* graph);
+uint64_t sox_graph_const_bytes(sox_graph* graph);
+/* Last build error text (NotSupportedException message analogue). */
+const char* sox_last_error(void);
+
+/* ---- session (VkInferenceSession); not thread-safe: one per thread ---- */
+int sox_session_create(sox_graph* graph, sox_session** session);
+void sox_session_destroy(sox_session* session);
+/* Mapped fp32 staging of graph input `index` / the output, in the plan's physical layout. */
+int sox_session_input(sox_session* session, int32_t index, float** host, int64_t* count);
+int sox_session_output(sox_session* session, float** host, int64_t* count);
+/* Run = Submit + Wait. */
+int sox_session_run(sox_session* session);
+int sox_session_submit(sox_session* session);
+int sox_session_wait(sox_session* session);
+/* Replay the dispatch sequence from a captured HIP graph (1) or launch it node by node (0). */
+int sox_session_set_replay(sox_session* session, int32_t on);
+/* Device-side timing with HIP events on the session stream: `iters` back-to-back enqueues of the
+ * dispatch list (flags bit0: include the staging copies/conversions), total ms. */
+enum { SOX_RUN_STAGING = 1, SOX_RUN_DISPATCHES = 2 };
+int sox_session_time(sox_session* session, int32_t iters, int32_t flags, float* total_ms);
+/* DebugProfile (VkSession.cs:413-490): per-dispatch device ms, min over `reps` runs. */
+int sox_session_profile(sox_session* session, int32_t reps, float* ms, int32_t cap);
+/* Debug read of any arena value as fp32 (node-by-node bisecting, VkDebugTests analogue). */
+int sox_session_read_value(sox_session* session, int32_t value, float* host, int64_t count);
+/* Device address of an arena value (advanced callers / tests). */
+int sox_session_value_ptr(sox_session* session, int32_t value, void** dev);
+void* sox_session_stream(sox_session* session);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

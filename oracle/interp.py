@@ -1,0 +1,110 @@
+"""Runs an ExecPlan on the CPU oracle: the restatement of InferenceSession.ExecNhwc
+(Engine/Session.cs:322-427) over the oracle kernels. Test infrastructure only.
+
+Values are kept as fp32 numpy arrays in their physical layout; zero-copy views (CValue.AliasOf)
+are reshapes of the same data. Fused GPU-plan ops are computed with the CPU formulas they fuse:
+HardSwish as a conv epilogue (Nhwc.Act8), Attention as MatMul -> scale -> Softmax -> MatMul
+(Ops.Seq.cs:28-116), ChannelGate as Nhwc.ChannelGate.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+import oracle as O
+
+
+def _phys(plan, vid, arr):
+    return np.ascontiguousarray(arr, dtype=np.float32).reshape(plan.values[vid].phys)
+
+
+def run_plan(plan, inputs, keep=False):
+    """Returns the output (physical layout); with keep=True also the dict of every value."""
+    env = {}
+    vals = plan.values
+
+    def get(vid):
+        v = vals[vid]
+        if v.is_const:
+            return v.data
+        if vid in env:
+            return env[vid]
+        if v.alias_of >= 0:
+            return get(v.alias_of).reshape(v.phys)
+        raise KeyError(f"value {vid} ({v.name}) read before written")
+
+    for vid, x in zip(plan.inputs, inputs):
+        env[vid] = _phys(plan, vid, x)
+    for node in plan.nodes:
+        p = node.p
+        out = node.outs[0]
+        oshape = vals[out].phys
+        if node.op == "Conv":
+            x = get(node.ins[0])
+            w = get(node.ins[1])
+            bias = get(p.bias) if p.bias >= 0 else None
+            add = get(p.add) if p.add >= 0 else None
+            pool_relu = p.pool[3] if p.pool is not None else False
+            y = O.conv(x, w, bias, add, stride=p.strides, pads=p.pads, group=p.group, act=p.act,
+                       pad_mode=p.pad_mode, pad_value=p.pad_value, pool=p.pool is not None, pool_relu=pool_relu)
+        elif node.op == "Gemm":
+            a = get(node.ins[0])
+            bias = get(p.bias) if p.bias >= 0 else None
+            y = O.gemm(a.reshape(-1, a.shape[-1]), get(node.ins[1]), bias, trans_b=p.trans_b, act=p.act)
+        elif node.op == "ConvTranspose":
+            y = O.conv_transpose(get(node.ins[0]), get(node.ins[1]), get(p.bias) if p.bias >= 0 else None, act=p.act)
+        elif node.op == "ChannelGate":
+            x = get(node.ins[0])
+            w1, w2 = get(node.ins[1]), get(node.ins[2])
+            r, c = w1.shape[0], w2.shape[0]
+            y = O.channel_gate(x, w1.reshape(r, c), get(p.b1) if p.b1 >= 0 else None, w2.reshape(c, r),
+                               get(p.b2) if p.b2 >= 0 else None, act1_relu=p.act1 == "relu", hard=p.hard,
+                               alpha=p.alpha, beta=p.beta, offset=p.offset)
+        elif node.op == "Elementwise":
+            a, b = get(node.ins[0]), get(node.ins[1])
+            act = 1 if p.act == "relu" else 0
+            if a.size == b.size:
+                y = O.ew2(a.reshape(-1), b.reshape(-1), op=p.op, act=act)
+            elif b.size == 1 or a.size == 1:
+                f = np.float32
+                s = (b if b.size == 1 else a).reshape(-1)[0]
+                x = a if b.size == 1 else b
+                rev = a.size == 1
+                y = {0: lambda: x + f(s), 1: lambda: (f(s) - x) if rev else (x - f(s)), 2: lambda: x * f(s),
+                     3: lambda: (f(s) / x) if rev else (x / f(s))}[p.op]()
+            else:
+                # NHWC per-channel broadcast [N,H,W,C] op [N,C]
+                full, vec, rev = (a, b, False) if a.size > b.size else (b, a, True)
+                nb = full.shape[0]
+                c = full.shape[-1]
+                vec = vec.reshape(nb, c)
+                y = np.concatenate([O.channel_broadcast(full[i].reshape(-1, c), vec[i], op=p.op, rev=rev, act=act)
+                                    .reshape(1, -1) for i in range(nb)])
+        elif node.op in ("Relu", "Sigmoid", "Gelu", "HardSwish", "Swish"):
+            y = O.activation(get(node.ins[0]), node.op.lower())
+        elif node.op == "HardSigmoid":
+            y = O.hard_sigmoid(get(node.ins[0]), p.alpha, p.beta)
+        elif node.op == "Copy":
+            y = get(node.ins[0]).copy()
+        elif node.op == "ResizeNearest":
+            x = get(node.ins[0])
+            add = get(node.ins[1]) if len(node.ins) > 1 else None
+            y = O.resize_nearest(x, p.scales[-2], p.scales[-1], add, p.add_relu)
+        elif node.op == "Concat":
+            y = O.concat_channels([get(v) for v in node.ins])
+        elif node.op == "LayerNorm":
+            y = O.layer_norm(get(node.ins[0]), get(node.ins[1]), get(node.ins[2]), p.eps)
+        elif node.op == "Softmax":
+            y = O.softmax(get(node.ins[0]))
+        elif node.op == "Attention":
+            qkv = get(node.ins[0])  # [N, T, 3, H, D] (identity layout)
+            nb, t, _, h, d = qkv.shape
+            q = np.ascontiguousarray(qkv[:, :, 0].transpose(0, 2, 1, 3)).reshape(nb * h, t, d)
+            k = np.ascontiguousarray(qkv[:, :, 1].transpose(0, 2, 1, 3)).reshape(nb * h, t, d)
+            v = np.ascontiguousarray(qkv[:, :, 2].transpose(0, 2, 1, 3)).reshape(nb * h, t, d)
+            o = O.attention(q, k, v, p.scale).reshape(nb, h, t, d)
+            y = np.ascontiguousarray(o.transpose(0, 2, 1, 3))  # stored [N, T, H, D]
+        else:
+            raise NotImplementedError(f"oracle interpreter: {node.op}")
+        env[out] = np.ascontiguousarray(y, dtype=np.float32).reshape(oshape)
+    res = get(plan.output)
+    return (res, env) if keep else res

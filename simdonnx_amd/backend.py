@@ -1,0 +1,268 @@
+"""Python face of the HIP backend: HipBackend / HipGraphModel / HipInferenceSession.
+
+Thin wrappers over include/sox_backend.h with the reference's member names and semantics
+(Backends/Vulkan/VkBackend.cs:11-267, VkGraph.cs:44-1233, VkSession.cs:63-571). All GPU work is
+done by the native library; nothing here computes anything itself, and there is no fallback: a
+missing library or device raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import numpy as np
+
+from . import native as N
+from .plan import ExecPlan
+
+
+class GpuDeviceInfo:
+    """GpuDeviceInfo (Backends/GpuDeviceInfo.cs:12-20)."""
+
+    def __init__(self, info: N.DeviceInfo):
+        self.name = info.name.decode()
+        self.arch = info.arch.decode()
+        self.compute_units = info.compute_units
+        self.lds_per_cu = info.lds_per_cu
+        self.clock_khz = info.clock_khz
+        self.wave_size = info.warp_size
+        self.vendor_id = info.vendor_id
+        self.hbm_bytes = info.hbm_bytes
+        self.xcds = info.xcds
+
+    def __repr__(self):
+        return (f"GpuDeviceInfo({self.name!r}, {self.arch}, {self.compute_units} CUs, "
+                f"{self.hbm_bytes / 2**30:.0f} GiB, wave{self.wave_size})")
+
+
+class HipBackend:
+    """VkBackend analogue: one per device; ``default()`` re-creates it after a device loss."""
+
+    _default: Optional["HipBackend"] = None
+
+    def __init__(self, handle):
+        self.h = handle
+        info = N.DeviceInfo()
+        N.check(N.backend().sox_backend_info(self.h, ctypes.byref(info)), "sox_backend_info")
+        self.device = GpuDeviceInfo(info)
+        self._ext_keep = []
+
+    @classmethod
+    def default(cls) -> "HipBackend":
+        h = N.c_void_p()
+        N.check(N.backend().sox_backend_default(ctypes.byref(h)), "HipBackend.Default")
+        if cls._default is None or cls._default.h.value != h.value:
+            cls._default = HipBackend(h)
+        return cls._default
+
+    @classmethod
+    def try_default(cls) -> Optional["HipBackend"]:
+        """TryGetDefault (VkBackend.cs:75-86): None when no device can be opened."""
+        try:
+            return cls.default()
+        except (N.SoxError, OSError, RuntimeError):
+            return None
+
+    @property
+    def is_lost(self) -> bool:
+        return bool(N.backend().sox_backend_is_lost(self.h))
+
+    def graph(self, plan: ExecPlan, f16: bool = True) -> "HipGraphModel":
+        return HipGraphModel(self, plan, f16)
+
+    def new_session(self, plan: ExecPlan, f16: bool = True) -> "HipInferenceSession":
+        """NewSession(model, shape, opt) (VkBackend.cs:238-243) for an already compiled plan."""
+        g = self.graph(plan, f16)
+        s = HipInferenceSession(g)
+        g.release()  # the session holds its own reference
+        return s
+
+    def load_module(self, image: bytes):
+        """Loads an extension's code object (sox_backend_load_module)."""
+        buf = ctypes.create_string_buffer(image, len(image))
+        m = N.c_void_p()
+        N.check(N.backend().sox_backend_load_module(self.h, buf, len(image), ctypes.byref(m)), "load_module")
+        self._ext_keep.append(buf)
+        return m
+
+    def register_ext(self, name: str, emit, consts=None):
+        """Registers an extension op's HIP emitter (the ExtOp.EmitHip hook)."""
+        emit_fn = N.EXT_EMIT_FN(lambda user, g, node: emit(HipGraphView(g), node))
+        if consts is None:
+            consts_fn = N.EXT_CONSTS_FN(lambda *a: 0)
+        else:
+            def _c(user, plan, node, vals, kinds, cap):
+                items = consts(node)
+                for i, (v, k) in enumerate(items[:cap]):
+                    vals[i], kinds[i] = v, N.CK[k] if isinstance(k, str) else k
+                return min(len(items), cap)
+            consts_fn = N.EXT_CONSTS_FN(_c)
+        self._ext_keep += [emit_fn, consts_fn]
+        N.check(N.backend().sox_backend_register_ext(self.h, name.encode(), emit_fn, consts_fn, None),
+                "register_ext")
+
+
+class HipGraphView:
+    """The graph handed to an extension emitter: Bind / Scratch / Dispatch (VkGraph.cs:355-400, 1117-1123)."""
+
+    def __init__(self, g):
+        self.h = g
+
+    @property
+    def f16(self) -> bool:
+        return bool(N.backend().sox_graph_is_f16(self.h))
+
+    def bind(self, value: int, kind="raw") -> N.Bind:
+        b = N.Bind()
+        N.check(N.backend().sox_graph_bind(self.h, value, N.CK[kind] if isinstance(kind, str) else kind,
+                                           ctypes.byref(b)), "Bind")
+        return b
+
+    def shape(self, value: int):
+        s = (N.c_int32 * 8)()
+        r = N.c_int32()
+        N.check(N.backend().sox_graph_value_shape(self.h, value, s, 8, ctypes.byref(r)), "shape")
+        return tuple(s[: r.value])
+
+    def dispatch(self, node: int, kernel: str, binds, params: bytes, grid, block=(256, 1, 1), lds=0, module=None):
+        arr = (N.Bind * max(len(binds), 1))(*binds)
+        g3 = (N.c_uint32 * 3)(*grid)
+        b3 = (N.c_uint32 * 3)(*block)
+        pbuf = ctypes.create_string_buffer(params, max(len(params), 1))
+        return N.backend().sox_graph_dispatch(self.h, node, module, kernel.encode(), arr, len(binds), pbuf,
+                                              len(params), g3, b3, lds)
+
+
+class HipGraphModel:
+    """VkGraphModel analogue: packed consts + the dispatch list of one plan."""
+
+    def __init__(self, backend: HipBackend, plan: ExecPlan, f16: bool = True):
+        self.backend = backend
+        self.plan = plan
+        self.f16 = f16
+        ph = plan.to_native()
+        try:
+            h = N.c_void_p()
+            N.check(N.backend().sox_graph_create(backend.h, ph, int(f16), ctypes.byref(h)), "HipGraphModel")
+            self.h = h
+        finally:
+            N.backend().sox_plan_destroy(ph)
+
+    def release(self):
+        if self.h:
+            N.backend().sox_graph_release(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:
+            pass
+
+    @property
+    def dispatches(self):
+        out = []
+        lib = N.backend()
+        for i in range(lib.sox_graph_dispatch_count(self.h)):
+            name = ctypes.create_string_buffer(128)
+            grid = (N.c_uint32 * 3)()
+            node = N.c_int32()
+            lib.sox_graph_dispatch_info(self.h, i, name, 128, grid, ctypes.byref(node))
+            out.append((name.value.decode(), tuple(grid), node.value))
+        return out
+
+    @property
+    def arena_bytes(self) -> int:
+        return int(N.backend().sox_graph_arena_bytes(self.h))
+
+    @property
+    def const_bytes(self) -> int:
+        return int(N.backend().sox_graph_const_bytes(self.h))
+
+
+class HipInferenceSession:
+    """VkInferenceSession analogue: one arena slab, mapped fp32 staging; not thread-safe."""
+
+    def __init__(self, graph: HipGraphModel):
+        self.graph = graph
+        h = N.c_void_p()
+        N.check(N.backend().sox_session_create(graph.h, ctypes.byref(h)), "HipInferenceSession")
+        self.h = h
+        self._inputs = []
+        lib = N.backend()
+        for i in range(len(graph.plan.inputs)):
+            p = ctypes.POINTER(N.c_float)()
+            n = N.c_int64()
+            N.check(lib.sox_session_input(self.h, i, ctypes.byref(p), ctypes.byref(n)), "input")
+            self._inputs.append(np.ctypeslib.as_array(p, shape=(n.value,)))
+        p = ctypes.POINTER(N.c_float)()
+        n = N.c_int64()
+        N.check(lib.sox_session_output(self.h, ctypes.byref(p), ctypes.byref(n)), "output")
+        self._output = np.ctypeslib.as_array(p, shape=(n.value,))
+
+    def close(self):
+        if self.h:
+            N.backend().sox_session_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    @property
+    def input(self) -> np.ndarray:
+        """Mapped fp32 staging of input 0, in the plan's physical layout (flat)."""
+        return self._inputs[0]
+
+    def get_input(self, i: int) -> np.ndarray:
+        return self._inputs[i]
+
+    @property
+    def output(self) -> np.ndarray:
+        return self._output
+
+    def set_input(self, x: np.ndarray, i: int = 0):
+        self._inputs[i][:] = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+
+    def run(self) -> np.ndarray:
+        N.check(N.backend().sox_session_run(self.h), "Run")
+        shape = self.graph.plan.values[self.graph.plan.output].phys
+        return self._output.reshape(shape)
+
+    def submit(self):
+        N.check(N.backend().sox_session_submit(self.h), "Submit")
+
+    def wait(self):
+        N.check(N.backend().sox_session_wait(self.h), "Wait")
+
+    def set_replay(self, on: bool):
+        N.check(N.backend().sox_session_set_replay(self.h, int(on)), "replay")
+
+    def time(self, iters: int, staging: bool = False) -> float:
+        """Device ms for `iters` back-to-back enqueues, measured with HIP events on the session stream."""
+        ms = N.c_float()
+        flags = N.RUN_DISPATCHES | (N.RUN_STAGING if staging else 0)
+        N.check(N.backend().sox_session_time(self.h, iters, flags, ctypes.byref(ms)), "time")
+        return ms.value
+
+    def profile(self, reps: int = 5):
+        """DebugProfile: [(dispatch name, node, min ms)]."""
+        d = self.graph.dispatches
+        ms = (N.c_float * max(len(d), 1))()
+        N.check(N.backend().sox_session_profile(self.h, reps, ms, len(d)), "profile")
+        return [(name, node, ms[i]) for i, (name, grid, node) in enumerate(d)]
+
+    def read_value(self, vid: int) -> np.ndarray:
+        v = self.graph.plan.values[vid]
+        out = np.empty(v.count, np.float32)
+        N.check(N.backend().sox_session_read_value(self.h, vid, out.ctypes.data_as(ctypes.POINTER(N.c_float)),
+                                                   v.count), "read_value")
+        return out.reshape(v.phys)

@@ -1,0 +1,109 @@
+"""Builds the HIP backend in-tree: gfx950 code objects + the two C-ABI shared libraries.
+
+  1. every ``csrc/kernels/*.hip`` -> ``_build/<name>.hsaco`` (``hipcc --genco --offload-arch=gfx950``);
+  2. the code objects are embedded into the backend library with ``.incbin`` (the resource table
+     the backend loads with ``sox_module_load`` = hipModuleLoadData, as the reference embeds its
+     shaders, Sdcb.SimdOnnx.Sources.props:21-31);
+  3. ``lib/libsoxhip.so``      - the thin C ABI over libamdhip64 (include/sox_hip.h);
+     ``lib/libsoxbackend.so``  - HipBackend / HipGraphModel / HipInferenceSession (include/sox_backend.h).
+
+Run ``python -m simdonnx_amd.build`` (or ``__graft_entry__.build()``). Compiles every time it is called.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+KDIR = os.path.join(HERE, "csrc", "kernels")
+HDIR = os.path.join(HERE, "csrc", "host")
+BUILD = os.path.join(HERE, "_build")
+LIB = os.path.join(HERE, "lib")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+ARCH = "gfx950"
+
+# All HIP code is built without packed fp32 ops (v_pk_*_f32).
+HIP_FLAGS = ["-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def _hipcc() -> str:
+    p = shutil.which("hipcc") or os.path.join(ROCM, "bin", "hipcc")
+    if not os.path.exists(p):
+        raise RuntimeError("hipcc not found: the HIP backend cannot be built")
+    return p
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"build step failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    return r
+
+
+def build_code_objects(verbose=False):
+    os.makedirs(BUILD, exist_ok=True)
+    srcs = sorted(f for f in os.listdir(KDIR) if f.endswith(".hip"))
+    hipcc = _hipcc()
+
+    def one(src):
+        name = src[:-4]
+        out = os.path.join(BUILD, name + ".hsaco")
+        _run([hipcc, "--genco", "--no-gpu-bundle-output", f"--offload-arch={ARCH}", *HIP_FLAGS, "-o", out,
+              os.path.join(KDIR, src)])
+        if verbose:
+            print("built", out, os.path.getsize(out), "bytes", flush=True)
+        return name, out
+
+    with ThreadPoolExecutor(max_workers=min(4, len(srcs))) as ex:
+        return list(ex.map(one, srcs))
+
+
+def write_resources(objs):
+    asm = [".section .rodata"]
+    table = ["static const SoxResource sox_resources[] = {"]
+    for name, path in objs:
+        sym = f"sox_res_{name}"
+        asm += [".balign 4096", f".global {sym}_start", f"{sym}_start:", f'.incbin "{path}"',
+                f".global {sym}_end", f"{sym}_end:"]
+        table.insert(0, f'extern "C" const unsigned char {sym}_start[], {sym}_end[];')
+        table.append(f'    {{"{name}", {sym}_start, {sym}_end}},')
+    asm.append('.section .note.GNU-stack,"",@progbits')
+    table.append("    {nullptr, nullptr, nullptr},")
+    table.append("};")
+    with open(os.path.join(BUILD, "resources.S"), "w") as f:
+        f.write("\n".join(asm) + "\n")
+    with open(os.path.join(BUILD, "resources_table.inc"), "w") as f:
+        f.write("\n".join(table) + "\n")
+
+
+def build_libs(verbose=False):
+    os.makedirs(LIB, exist_ok=True)
+    cxx = os.path.join(ROCM, "llvm", "bin", "clang++")
+    if not os.path.exists(cxx):
+        cxx = _hipcc()
+    common = ["-O2", "-fPIC", "-std=c++17", "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", "-Wall",
+              "-Wno-unused-result"]
+    thin = os.path.join(LIB, "libsoxhip.so")
+    _run([cxx, *common, "-shared", "-o", thin, os.path.join(HDIR, "sox_hip.cpp"), f"-L{ROCM}/lib", "-lamdhip64",
+          f"-Wl,-rpath,{ROCM}/lib"])
+    be = os.path.join(LIB, "libsoxbackend.so")
+    _run([cxx, *common, f"-I{BUILD}", "-shared", "-o", be, os.path.join(HDIR, "backend.cpp"),
+          os.path.join(BUILD, "resources.S"), f"-L{LIB}", "-lsoxhip", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{ROCM}/lib"])
+    if verbose:
+        print("built", thin, be, flush=True)
+    return thin, be
+
+
+def build(verbose=False):
+    objs = build_code_objects(verbose)
+    write_resources(objs)
+    return build_libs(verbose)
+
+
+if __name__ == "__main__":
+    build(verbose=True)
+    sys.exit(0)

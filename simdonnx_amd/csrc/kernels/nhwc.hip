@@ -1,0 +1,508 @@
+// Bandwidth-bound NHWC kernels of the detector / recognizer graphs: depthwise conv,
+// stride==kernel ConvTranspose, squeeze-excitation (GAP partials + gate + channel broadcast),
+// nearest upsample + add, channel-slice copies (concat), elementwise, staging conversions,
+// LayerNorm, row softmax and fused attention.
+//
+// They replace depthwise(4).comp, convt.comp, gap_part/se_gate.comp, ew2(v).comp, unary(2).comp,
+// nearest(4).comp, concat_ax.comp, f32to16/f16to32.comp, layernorm.comp, softmax.comp and
+// attn.comp (Backends/Vulkan/Shaders). None of them is GEMM-shaped enough for MFMA: they read
+// each input byte a small constant number of times, so they are written for coalesced 16-byte
+// accesses along the contiguous channel axis and wavefront reductions.
+#include "sox_device.h"
+
+template <typename T> struct V16 {
+    static constexpr int N = 16 / sizeof(T);
+    typedef T Vec __attribute__((ext_vector_type(16 / sizeof(T))));
+};
+
+template <typename T, int CV> struct VecT {
+    typedef T Vec __attribute__((ext_vector_type(CV)));
+};
+
+// ------------------------------------------------------------------------------------------
+// Depthwise k x k (Kernels/Nhwc.cs:496-631): acc = bias[c] + sum over taps (row-major) x*w,
+// + residual, act. One work item = CV channels of one output pixel; taps outside a
+// constant-0 pad are skipped, a nonzero pad value contributes pad * w.
+// ------------------------------------------------------------------------------------------
+template <typename T, int CV>
+__device__ __forceinline__ void dw_body(const sox_dw_args& p) {
+    const int cvn = p.c / CV;
+    const long total = (long)p.n * p.oh * p.ow * cvn;
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const int cv = (int)(idx % cvn);
+    long pix = idx / cvn;
+    const int ox = (int)(pix % p.ow);
+    pix /= p.ow;
+    const int oy = (int)(pix % p.oh);
+    const int b = (int)(pix / p.oh);
+    const int c0 = cv * CV;
+    const bool reflect = (p.flags & SOX_F_REFLECT) != 0;
+    const T* __restrict__ x = (const T*)p.x + (long)b * p.ih * p.iw * p.c;
+    const T* __restrict__ w = (const T*)p.w;
+    float acc[CV];
+#pragma unroll
+    for (int e = 0; e < CV; e++) acc[e] = (p.flags & SOX_F_BIAS) ? p.bias[c0 + e] : 0.0f;
+    typedef typename VecT<T, CV>::Vec Vec;
+    for (int ky = 0; ky < p.kh; ky++) {
+        int iy = sox_src_index(oy * p.sh + ky - p.pt, p.ih, reflect);
+        if (iy < 0 && p.pad_value == 0.0f) continue;
+        for (int kx = 0; kx < p.kw; kx++) {
+            int ix = sox_src_index(ox * p.sw + kx - p.pl, p.iw, reflect);
+            Vec wv = *(const Vec*)(w + (long)(ky * p.kw + kx) * p.c + c0);
+            if (iy < 0 || ix < 0) {
+                if (p.pad_value != 0.0f)
+#pragma unroll
+                    for (int e = 0; e < CV; e++) acc[e] = __builtin_fmaf(p.pad_value, to_f(wv[e]), acc[e]);
+                continue;
+            }
+            Vec xv = *(const Vec*)(x + ((long)iy * p.iw + ix) * p.c + c0);
+#pragma unroll
+            for (int e = 0; e < CV; e++) acc[e] = __builtin_fmaf(to_f(xv[e]), to_f(wv[e]), acc[e]);
+        }
+    }
+    const int act = (p.flags & SOX_F_ACT_MASK) >> SOX_F_ACT_SHIFT;
+    long o = (((long)b * p.oh + oy) * p.ow + ox) * p.c + c0;
+    Vec out;
+    if (p.flags & SOX_F_RESIDUAL) {
+        Vec av = *(const Vec*)((const T*)p.add + o);
+#pragma unroll
+        for (int e = 0; e < CV; e++) acc[e] = acc[e] + to_f(av[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < CV; e++) out[e] = (T)sox_act(acc[e], act);
+    *(Vec*)((T*)p.y + o) = out;
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_dw_f16_v(sox_dw_args p) { dw_body<half_t, 8>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_dw_f16_s(sox_dw_args p) { dw_body<half_t, 1>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_dw_f32_v(sox_dw_args p) { dw_body<float, 4>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_dw_f32_s(sox_dw_args p) { dw_body<float, 1>(p); }
+
+// ------------------------------------------------------------------------------------------
+// ConvTranspose, stride == kernel, no pad (Kernels/Nhwc.Det.cs:51-131): every input pixel owns
+// a disjoint kh x kw output patch. One work item = one (input pixel, tap, oc) output element;
+// w is [tap][ic][oc], so neighbouring items read neighbouring weights and the same x row.
+// ------------------------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void convt_body(const sox_convt_args& p) {
+    const int taps = p.kh * p.kw;
+    const long total = (long)p.n * p.ih * p.iw * taps * p.oc;
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const int o = (int)(idx % p.oc);
+    long r = idx / p.oc;
+    const int tap = (int)(r % taps);
+    long pix = r / taps;  // (b, y, x) of the input
+    const int x = (int)(pix % p.iw);
+    long q = pix / p.iw;
+    const int y = (int)(q % p.ih);
+    const int b = (int)(q / p.ih);
+    const T* __restrict__ xp = (const T*)p.x + pix * p.ic;
+    const T* __restrict__ w = (const T*)p.w + (long)tap * p.ic * p.oc + o;
+    float s = (p.flags & SOX_F_BIAS) ? p.bias[o] : 0.0f;
+    for (int c = 0; c < p.ic; c++) s = __builtin_fmaf(to_f(xp[c]), to_f(w[(long)c * p.oc]), s);
+    const int act = (p.flags & SOX_F_ACT_MASK) >> SOX_F_ACT_SHIFT;
+    const int dy = tap / p.kw, dx = tap - dy * p.kw;
+    const int ow = p.iw * p.kw, oh = p.ih * p.kh;
+    long out = (((long)b * oh + (y * p.kh + dy)) * ow + (x * p.kw + dx)) * p.oc + o;
+    ((T*)p.y)[out] = (T)sox_act(s, act);
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_convt_f16(sox_convt_args p) { convt_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_convt_f32(sox_convt_args p) { convt_body<float>(p); }
+
+// ------------------------------------------------------------------------------------------
+// Global-average-pool partials (gap_part.comp): part[b][chunk][c] = sum over the chunk's pixels.
+// Grid (ceil(c/64), chunks, n), 256 threads = 64 channels x 4 pixel phases, reduced in LDS.
+// ------------------------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void gap_body(const sox_gap_args& p) {
+    __shared__ float red[4][64];
+    const int lc = threadIdx.x & 63, ph = threadIdx.x >> 6;
+    const int c = blockIdx.x * 64 + lc;
+    const int chunk = blockIdx.y, b = blockIdx.z;
+    const long p0 = (long)chunk * p.hw / p.chunks, p1 = (long)(chunk + 1) * p.hw / p.chunks;
+    const T* __restrict__ x = (const T*)p.x + (long)b * p.hw * p.c;
+    float s = 0.0f;
+    if (c < p.c)
+        for (long px = p0 + ph; px < p1; px += 4) s += to_f(x[px * p.c + c]);
+    red[ph][lc] = s;
+    __syncthreads();
+    if (ph == 0 && c < p.c)
+        p.part[((long)b * p.chunks + chunk) * p.c + c] = (red[0][lc] + red[1][lc]) + (red[2][lc] + red[3][lc]);
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_gap_f16(sox_gap_args p) { gap_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_gap_f32(sox_gap_args p) { gap_body<float>(p); }
+
+// ------------------------------------------------------------------------------------------
+// SE gate (se_gate.comp; Kernels/Nhwc.Det.cs:287-314), one workgroup of 256 per image.
+// ------------------------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void se_body(const sox_se_args& p) {
+    extern __shared__ float sm[];
+    float* mean = sm;          // [c]
+    float* hid = sm + p.c;     // [r]
+    const int b = blockIdx.x;
+    const float inv = 1.0f / p.hw;
+    for (int c = threadIdx.x; c < p.c; c += blockDim.x) {
+        float s = 0.0f;
+        for (int k = 0; k < p.chunks; k++) s += p.part[((long)b * p.chunks + k) * p.c + c];
+        mean[c] = s * inv;
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j < p.r; j += blockDim.x) {
+        float s = (p.flags & 1) ? p.b1[j] : 0.0f;
+        const float* row = p.w1 + (long)j * p.c;
+        for (int k = 0; k < p.c; k++) s = __builtin_fmaf(row[k], mean[k], s);
+        hid[j] = (p.flags & 4) ? fmaxf(s, 0.0f) : s;
+    }
+    __syncthreads();
+    for (int c = threadIdx.x; c < p.c; c += blockDim.x) {
+        float z = (p.flags & 2) ? p.b2[c] : 0.0f;
+        const float* row = p.w2 + (long)c * p.r;
+        for (int j = 0; j < p.r; j++) z = __builtin_fmaf(row[j], hid[j], z);
+        float g = (p.flags & 8) ? fminf(fmaxf(z * p.alpha + p.beta, 0.0f), 1.0f) : sox_sigmoid(z);
+        ((T*)p.s)[(long)b * p.c + c] = (T)(g + p.offset);
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_se_f16(sox_se_args p) { se_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_se_f32(sox_se_args p) { se_body<float>(p); }
+
+// ------------------------------------------------------------------------------------------
+// Per-channel broadcast y[p, c] = act(x[p, c] op v[img, c]) (ChannelBroadcast, Nhwc.Det.cs:317-351).
+// ------------------------------------------------------------------------------------------
+template <typename T, int CV>
+__device__ __forceinline__ void chan_body(const sox_chan_args& p) {
+    const int cvn = p.c / CV;
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= p.rows * cvn) return;
+    const long row = idx / cvn;
+    const int c0 = (int)(idx % cvn) * CV;
+    const long img = row / p.hw;
+    typedef typename VecT<T, CV>::Vec Vec;
+    Vec xv = *(const Vec*)((const T*)p.x + row * p.c + c0);
+    Vec vv = *(const Vec*)((const T*)p.v + img * p.c + c0);
+    const int act = (p.flags & SOX_F_ACT_MASK) >> SOX_F_ACT_SHIFT;
+    const bool rev = p.flags & 1;
+    Vec out;
+#pragma unroll
+    for (int e = 0; e < CV; e++) {
+        float a = to_f(xv[e]), b = to_f(vv[e]);
+        out[e] = (T)sox_act(rev ? sox_ew(b, a, p.op) : sox_ew(a, b, p.op), act);
+    }
+    *(Vec*)((T*)p.y + row * p.c + c0) = out;
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_chan_f16_v(sox_chan_args p) { chan_body<half_t, 8>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_chan_f16_s(sox_chan_args p) { chan_body<half_t, 1>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_chan_f32_v(sox_chan_args p) { chan_body<float, 4>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_chan_f32_s(sox_chan_args p) { chan_body<float, 1>(p); }
+
+// ------------------------------------------------------------------------------------------
+// Same-shape elementwise binary op + act (ew2v.comp), 16-byte vectors, scalar tail.
+// ------------------------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void ew_body(const sox_ew_args& p) {
+    constexpr int CV = V16<T>::N;
+    typedef typename V16<T>::Vec Vec;
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long base = idx * CV;
+    const int act = (p.flags & SOX_F_ACT_MASK) >> SOX_F_ACT_SHIFT;
+    const T* a = (const T*)p.a;
+    const T* b = (const T*)p.b;
+    T* y = (T*)p.y;
+    if (base + CV <= p.count) {
+        Vec av = *(const Vec*)(a + base), bv = *(const Vec*)(b + base), out;
+#pragma unroll
+        for (int e = 0; e < CV; e++) out[e] = (T)sox_act(sox_ew(to_f(av[e]), to_f(bv[e]), p.op), act);
+        *(Vec*)(y + base) = out;
+    } else {
+        for (long i = base; i < p.count; i++) y[i] = (T)sox_act(sox_ew(to_f(a[i]), to_f(b[i]), p.op), act);
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_ew_f16(sox_ew_args p) { ew_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_ew_f32(sox_ew_args p) { ew_body<float>(p); }
+
+// ------------------------------------------------------------------------------------------
+// Unary: act / affine / hard-sigmoid / copy (unary.comp, unary2.comp, hsig.comp).
+// ------------------------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ float unary_op(float v, const sox_unary_args& p) {
+    switch (p.mode) {
+        case 0: return sox_act(v, p.act);
+        case 1: return v * p.alpha + p.beta;
+        case 2: return fminf(fmaxf(v * p.alpha + p.beta, 0.0f), 1.0f);
+        default: return v;
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ void unary_body(const sox_unary_args& p) {
+    constexpr int CV = V16<T>::N;
+    typedef typename V16<T>::Vec Vec;
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long base = idx * CV;
+    const T* x = (const T*)p.x;
+    T* y = (T*)p.y;
+    if (base + CV <= p.count) {
+        Vec xv = *(const Vec*)(x + base), out;
+#pragma unroll
+        for (int e = 0; e < CV; e++) out[e] = (T)unary_op<T>(to_f(xv[e]), p);
+        *(Vec*)(y + base) = out;
+    } else {
+        for (long i = base; i < p.count; i++) y[i] = (T)unary_op<T>(to_f(x[i]), p);
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_unary_f16(sox_unary_args p) { unary_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_unary_f32(sox_unary_args p) { unary_body<float>(p); }
+
+// ------------------------------------------------------------------------------------------
+// Nearest resize, asymmetric / floor (Nhwc.Det.cs:167-204) + optional [relu] addend; writes a
+// channel slice [y_off, y_off + c) of a ldy-channel output (so FPN concats need no copy).
+// ------------------------------------------------------------------------------------------
+template <typename T, int CV>
+__device__ __forceinline__ void nearest_body(const sox_nearest_args& p) {
+    const int cvn = p.c / CV;
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long total = (long)p.n * p.oh * p.ow * cvn;
+    if (idx >= total) return;
+    const int c0 = (int)(idx % cvn) * CV;
+    long pix = idx / cvn;
+    const int ox = (int)(pix % p.ow);
+    long q = pix / p.ow;
+    const int oy = (int)(q % p.oh);
+    const int b = (int)(q / p.oh);
+    const int ys = min((int)floorf(oy / p.sy), p.ih - 1);
+    const int xs = min((int)floorf(ox / p.sx), p.iw - 1);
+    typedef typename VecT<T, CV>::Vec Vec;
+    Vec v = *(const Vec*)((const T*)p.x + (((long)b * p.ih + ys) * p.iw + xs) * p.c + c0);
+    if (p.flags & 1) {
+        Vec av = *(const Vec*)((const T*)p.add + pix * p.c + c0);
+#pragma unroll
+        for (int e = 0; e < CV; e++) {
+            float a = to_f(av[e]);
+            v[e] = (T)(to_f(v[e]) + ((p.flags & 2) ? fmaxf(a, 0.0f) : a));
+        }
+    }
+    *(Vec*)((T*)p.y + pix * p.ldy + p.y_off + c0) = v;
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_nearest_f16_v(sox_nearest_args p) { nearest_body<half_t, 8>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_nearest_f16_s(sox_nearest_args p) { nearest_body<half_t, 1>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_nearest_f32_v(sox_nearest_args p) { nearest_body<float, 4>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_nearest_f32_s(sox_nearest_args p) { nearest_body<float, 1>(p); }
+
+// ------------------------------------------------------------------------------------------
+// Channel-slice copy (NHWC concat along C, concat_ax.comp).
+// ------------------------------------------------------------------------------------------
+template <typename T, int CV>
+__device__ __forceinline__ void slice_body(const sox_slice_copy_args& p) {
+    const int cvn = p.c / CV;
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= p.rows * cvn) return;
+    const long row = idx / cvn;
+    const int c0 = (int)(idx % cvn) * CV;
+    typedef typename VecT<T, CV>::Vec Vec;
+    *(Vec*)((T*)p.y + row * p.ldy + p.y_off + c0) = *(const Vec*)((const T*)p.x + row * p.c + c0);
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_slice_f16_v(sox_slice_copy_args p) { slice_body<half_t, 8>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_slice_f16_s(sox_slice_copy_args p) { slice_body<half_t, 1>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_slice_f32_v(sox_slice_copy_args p) { slice_body<float, 4>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_slice_f32_s(sox_slice_copy_args p) { slice_body<float, 1>(p); }
+
+// ------------------------------------------------------------------------------------------
+// Staging conversions (f32to16.comp / f16to32.comp): fp16 RNE, as the (Half) cast.
+// ------------------------------------------------------------------------------------------
+extern "C" __global__ void __launch_bounds__(256) sox_f32_to_f16(sox_cvt_args p) {
+    const long i = ((long)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    const float* x = (const float*)p.x;
+    half_t* y = (half_t*)p.y;
+    if (i + 4 <= p.count) {
+        float4v v = *(const float4v*)(x + i);
+        half4 h;
+        h[0] = (half_t)v[0]; h[1] = (half_t)v[1]; h[2] = (half_t)v[2]; h[3] = (half_t)v[3];
+        *(half4*)(y + i) = h;
+    } else {
+        for (long j = i; j < p.count; j++) y[j] = (half_t)x[j];
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_f16_to_f32(sox_cvt_args p) {
+    const long i = ((long)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    const half_t* x = (const half_t*)p.x;
+    float* y = (float*)p.y;
+    if (i + 4 <= p.count) {
+        half4 h = *(const half4*)(x + i);
+        float4v v;
+        v[0] = (float)h[0]; v[1] = (float)h[1]; v[2] = (float)h[2]; v[3] = (float)h[3];
+        *(float4v*)(y + i) = v;
+    } else {
+        for (long j = i; j < p.count; j++) y[j] = (float)x[j];
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Wave reductions (wave64).
+// ------------------------------------------------------------------------------------------
+SOX_DEV float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+SOX_DEV float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// ------------------------------------------------------------------------------------------
+// LayerNorm (Kernels/Ops.cs:544-574, Avx2Kernels.cs:562-600): one wave per row; single pass
+// mean and E[x^2] - mean^2 (clamped at 0), inv = 1/sqrt(var + eps), y = (x - mean) * (inv*g) + b.
+// ------------------------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void ln_body(const sox_ln_args& p) {
+    const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= p.rows) return;
+    const T* x = (const T*)p.x + row * p.len;
+    T* y = (T*)p.y + row * p.len;
+    float s = 0.0f, ss = 0.0f;
+    for (int i = lane; i < p.len; i += 64) {
+        float v = to_f(x[i]);
+        s += v;
+        ss = __builtin_fmaf(v, v, ss);
+    }
+    s = wave_sum(s);
+    ss = wave_sum(ss);
+    const float mean = s / p.len;
+    const float inv = 1.0f / sqrtf(fmaxf(ss / p.len - mean * mean, 0.0f) + p.eps);
+    for (int i = lane; i < p.len; i += 64)
+        y[i] = (T)__builtin_fmaf(to_f(x[i]) - mean, inv * p.gamma[i], p.beta[i]);
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_ln_f16(sox_ln_args p) { ln_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_ln_f32(sox_ln_args p) { ln_body<float>(p); }
+
+// ------------------------------------------------------------------------------------------
+// Row softmax (Kernels/Ops.Seq.cs:28-72): max, exp(x - max) by the shared exp core, 1/sum.
+// One 256-thread workgroup per row.
+// ------------------------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void softmax_body(const sox_softmax_args& p) {
+    __shared__ float red[4];
+    const long row = blockIdx.x;
+    const T* x = (const T*)p.x + row * p.len;
+    T* y = (T*)p.y + row * p.len;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    float m = -INFINITY;
+    for (int i = threadIdx.x; i < p.len; i += 256) m = fmaxf(m, to_f(x[i]));
+    m = wave_max(m);
+    if (lane == 0) red[wv] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < p.len; i += 256) s += sox_exp(to_f(x[i]) - m);
+    s = wave_sum(s);
+    if (lane == 0) red[wv] = s;
+    __syncthreads();
+    const float inv = 1.0f / ((red[0] + red[1]) + (red[2] + red[3]));
+    for (int i = threadIdx.x; i < p.len; i += 256) y[i] = (T)(sox_exp(to_f(x[i]) - m) * inv);
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_softmax_f16(sox_softmax_args p) { softmax_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_softmax_f32(sox_softmax_args p) { softmax_body<float>(p); }
+
+// ------------------------------------------------------------------------------------------
+// Fused attention (attn.comp): one workgroup per (batch, head); K and V staged in LDS as fp32;
+// one thread per query row with an online softmax (running max / sum rescaling). D <= 64.
+// ------------------------------------------------------------------------------------------
+template <typename T, int D>
+__device__ __forceinline__ void attn_body(const sox_attn_args& p) {
+    extern __shared__ float kv[];  // [s][D] keys then [s][D] values
+    const int bh = blockIdx.x, b = bh / p.heads, h = bh - b * p.heads;
+    const T* kp = (const T*)p.k + b * p.k_sb + h * p.k_sh;
+    const T* vp = (const T*)p.v + b * p.v_sb + h * p.v_sh;
+    float* ks = kv;
+    float* vs = kv + p.s * D;
+    for (int i = threadIdx.x; i < p.s * D; i += blockDim.x) {
+        int j = i / D, e = i - j * D;
+        ks[i] = e < p.d ? to_f(kp[j * p.k_st + e]) : 0.0f;
+        vs[i] = e < p.d ? to_f(vp[j * p.v_st + e]) : 0.0f;
+    }
+    __syncthreads();
+    for (int t = blockIdx.y * blockDim.x + threadIdx.x; t < p.t; t += gridDim.y * blockDim.x) {
+        const T* qp = (const T*)p.q + b * p.q_sb + h * p.q_sh + t * p.q_st;
+        float q[D], acc[D];
+#pragma unroll
+        for (int e = 0; e < D; e++) {
+            q[e] = e < p.d ? to_f(qp[e]) : 0.0f;
+            acc[e] = 0.0f;
+        }
+        float mx = -INFINITY, sum = 0.0f;
+        for (int j = 0; j < p.s; j++) {
+            float sc = 0.0f;
+#pragma unroll
+            for (int e = 0; e < D; e++) sc = __builtin_fmaf(q[e], ks[j * D + e], sc);
+            sc *= p.scale;
+            float nm = fmaxf(mx, sc);
+            float corr = sox_exp(mx - nm), pj = sox_exp(sc - nm);
+            sum = sum * corr + pj;
+#pragma unroll
+            for (int e = 0; e < D; e++) acc[e] = __builtin_fmaf(pj, vs[j * D + e], acc[e] * corr);
+            mx = nm;
+        }
+        const float inv = 1.0f / sum;
+        T* op = (T*)p.o + b * p.o_sb + h * p.o_sh + t * p.o_st;
+#pragma unroll
+        for (int e = 0; e < D; e++)
+            if (e < p.d) op[e] = (T)(acc[e] * inv);
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(128) sox_attn_f16_d32(sox_attn_args p) { attn_body<half_t, 32>(p); }
+extern "C" __global__ void __launch_bounds__(128) sox_attn_f16_d64(sox_attn_args p) { attn_body<half_t, 64>(p); }
+extern "C" __global__ void __launch_bounds__(128) sox_attn_f32_d32(sox_attn_args p) { attn_body<float, 32>(p); }
+extern "C" __global__ void __launch_bounds__(128) sox_attn_f32_d64(sox_attn_args p) { attn_body<float, 64>(p); }
+
+// ------------------------------------------------------------------------------------------
+// Max pool (+relu) over NHWC, constant padding ignored (maxpool.comp).
+// ------------------------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void pool_body(const sox_pool_args& p) {
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long total = (long)p.n * p.oh * p.ow * p.c;
+    if (idx >= total) return;
+    const int c = (int)(idx % p.c);
+    long pix = idx / p.c;
+    const int ox = (int)(pix % p.ow);
+    long q = pix / p.ow;
+    const int oy = (int)(q % p.oh);
+    const int b = (int)(q / p.oh);
+    const T* x = (const T*)p.x + (long)b * p.ih * p.iw * p.c;
+    float m = -INFINITY;
+    bool any = false;
+    for (int ky = 0; ky < p.kh; ky++) {
+        int iy = oy * p.sh + ky - p.pt;
+        if ((unsigned)iy >= (unsigned)p.ih) continue;
+        for (int kx = 0; kx < p.kw; kx++) {
+            int ix = ox * p.sw + kx - p.pl;
+            if ((unsigned)ix >= (unsigned)p.iw) continue;
+            m = fmaxf(m, to_f(x[((long)iy * p.iw + ix) * p.c + c]));
+            any = true;
+        }
+    }
+    if (!any) m = 0.0f;
+    if (p.flags & 1) m = fmaxf(m, 0.0f);
+    ((T*)p.y)[idx] = (T)m;
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_pool_f16(sox_pool_args p) { pool_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_pool_f32(sox_pool_args p) { pool_body<float>(p); }

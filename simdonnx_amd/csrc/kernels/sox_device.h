@@ -1,0 +1,90 @@
+// Device-side helpers shared by the gfx950 kernels: storage types, activation math.
+//
+// The activation math restates the reference's shared formulas so GPU and CPU agree to float
+// rounding: exp by the Cephes-style 2^n * degree-5 polynomial with hi/lo ln2 split and clamp
+// [-87.3, 88.7], erf by Abramowitz-Stegun 7.1.26, GELU = 0.5x(1 + erf(x/sqrt2))
+// (Kernels/SimdMath.cs:121-168; the GPU shaders use the same A&S erf, Shaders/conv_cm.comp:104-111).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../../include/sox_abi.h"
+
+typedef _Float16 half_t;
+typedef half_t half8 __attribute__((ext_vector_type(8)));
+typedef half_t half4 __attribute__((ext_vector_type(4)));
+typedef half_t half2v __attribute__((ext_vector_type(2)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+
+#define SOX_DEV static __device__ __forceinline__
+
+SOX_DEV float sox_exp(float x) {
+    x = fmaxf(x, -87.3f);
+    x = fminf(x, 88.7f);
+    float fx = __builtin_fmaf(x, 1.4426950408889634f, 0.5f);
+    float nf = floorf(fx);
+    float r = __builtin_fmaf(nf, -0.693359375f, x);
+    r = __builtin_fmaf(nf, 0.00021219444005469058f, r);
+    float p = 1.9875691500e-4f;
+    p = __builtin_fmaf(p, r, 1.3981999507e-3f);
+    p = __builtin_fmaf(p, r, 8.3334519073e-3f);
+    p = __builtin_fmaf(p, r, 4.1665795894e-2f);
+    p = __builtin_fmaf(p, r, 1.6666665459e-1f);
+    p = __builtin_fmaf(p, r, 5.0000001201e-1f);
+    float y = __builtin_fmaf(p, r * r, r) + 1.0f;
+    int ni = (int)nf + 127;
+    return y * __int_as_float(ni << 23);
+}
+
+SOX_DEV float sox_sigmoid(float x) { return 1.0f / (1.0f + sox_exp(-x)); }
+
+SOX_DEV float sox_erf(float x) {
+    float ax = fabsf(x);
+    float t = 1.0f / __builtin_fmaf(0.3275911f, ax, 1.0f);
+    float p = 1.061405429f;
+    p = __builtin_fmaf(p, t, -1.453152027f);
+    p = __builtin_fmaf(p, t, 1.421413741f);
+    p = __builtin_fmaf(p, t, -0.284496736f);
+    p = __builtin_fmaf(p, t, 0.254829592f);
+    float y = 1.0f - (p * t) * sox_exp(-(ax * ax));
+    return copysignf(y, x);
+}
+
+SOX_DEV float sox_gelu(float x) { return (0.5f * x) * (1.0f + sox_erf(x * 0.70710678118654752f)); }
+
+// ActivationKind epilogue (Kernels/Nhwc.cs:91-99).
+SOX_DEV float sox_act(float v, int act) {
+    switch (act) {
+        case SOX_ACT_RELU: return fmaxf(v, 0.0f);
+        case SOX_ACT_SIGMOID: return sox_sigmoid(v);
+        case SOX_ACT_GELU: return sox_gelu(v);
+        case SOX_ACT_HARDSWISH: return v * fminf(fmaxf(__builtin_fmaf(v, 1.0f / 6.0f, 0.5f), 0.0f), 1.0f);
+        case SOX_ACT_SWISH: return v * sox_sigmoid(v);
+        default: return v;
+    }
+}
+
+SOX_DEV float sox_ew(float a, float b, int op) {
+    switch (op) {
+        case 0: return a + b;
+        case 1: return a - b;
+        case 2: return a * b;
+        default: return a / b;
+    }
+}
+
+template <typename T> SOX_DEV float to_f(T v) { return (float)v; }
+template <typename T> SOX_DEV T from_f(float v) { return (T)v; }
+
+SOX_DEV int sox_reflect(int i, int dim) {
+    if (dim <= 1) return 0;
+    while (i < 0 || i >= dim) i = i < 0 ? -i : 2 * dim - 2 - i;
+    return i;
+}
+
+// Source index along one axis, -1 for a constant-pad position (Kernels/Nhwc.cs:72-80).
+SOX_DEV int sox_src_index(int s, int len, bool reflect) {
+    if ((unsigned)s < (unsigned)len) return s;
+    return reflect ? sox_reflect(s, len) : -1;
+}

@@ -1,0 +1,516 @@
+"""ExecPlan: the executable IR the backend consumes, restated from Engine/ExecPlan.cs.
+
+A plan is what SimdOnnx's GraphCompiler hands a GPU backend (PlanTarget != Cpu, NHWC layout
+planned, fusions applied): values (``CValue``, ExecPlan.cs:202-220), nodes (``ExecNode``,
+:235-276) with their parameter records (``ConvP`` :50-65, ``GemmP`` :87-93, ...), and the arena
+plan (``BufOffset`` / ``ArenaFloats``, :283-285).
+
+``PlanBuilder`` emits the fused nodes that GraphCompiler produces for the patterns it fuses
+(Conv+bias+act+residual, Gemm+bias+GELU, HardSigmoid*x -> HardSwish epilogue, SE -> ChannelGate,
+Resize(nearest)+Add, ConvTranspose+bias+act; GraphCompiler.cs:272-1332) and lays the activations
+out in one arena with the lifetime packing of ``PlanArena`` (GraphCompiler.cs:1336-1474:
+32-element aligned first fit over [first def, last use] intervals).
+"""
+from __future__ import annotations
+
+import dataclasses
+from dataclasses import dataclass, field
+from typing import Optional
+
+import numpy as np
+
+from . import native as N
+
+NHWC = (0, 2, 3, 1)  # Layout.Nhwc (Engine/Layout.cs:15): physical [n,h,w,c] of logical [n,c,h,w]
+ACT = N.ACT
+
+
+@dataclass
+class Value:
+    """CValue: logical shape, physical layout, arena buffer id or const data."""
+
+    shape: tuple
+    layout: Optional[tuple] = None
+    buf: int = -1
+    data: Optional[np.ndarray] = None
+    name: str = ""
+    alias_of: int = -1
+
+    @property
+    def is_const(self) -> bool:
+        return self.data is not None
+
+    @property
+    def count(self) -> int:
+        return int(np.prod(self.shape)) if self.shape else 1
+
+    @property
+    def phys(self) -> tuple:
+        if self.layout is None:
+            return tuple(self.shape)
+        return tuple(self.shape[i] for i in self.layout)
+
+
+@dataclass
+class ConvP:
+    pads: tuple  # top, left, bottom, right
+    strides: tuple
+    kernel: tuple
+    dilations: tuple = (1, 1)
+    group: int = 1
+    act: str = "none"
+    pad_mode: int = 0
+    pad_value: float = 0.0
+    bias: int = -1
+    add: int = -1
+    pool: Optional[tuple] = None  # (kernel, strides, pads, relu) of a fused max pool
+
+    def native(self):
+        p = N.ConvP()
+        p.pads[:] = list(self.pads)
+        p.strides[:] = list(self.strides)
+        p.dilations[:] = list(self.dilations)
+        p.kernel[:] = list(self.kernel)
+        p.group, p.act, p.pad_mode, p.pad_value = self.group, ACT[self.act], self.pad_mode, self.pad_value
+        p.bias_value, p.add_value = self.bias, self.add
+        if self.pool is not None:
+            k, s, pd, relu = self.pool
+            p.has_pool = 1
+            p.pool_kernel[:] = list(k)
+            p.pool_strides[:] = list(s)
+            p.pool_pads[:] = list(pd)
+            p.pool_relu = int(relu)
+        return p
+
+
+@dataclass
+class GemmP:
+    trans_b: bool = False
+    bias: int = -1
+    act: str = "none"
+
+    def native(self):
+        return N.GemmP(int(self.trans_b), self.bias, ACT[self.act])
+
+
+@dataclass
+class ConvTP:
+    kernel: tuple
+    bias: int = -1
+    act: str = "none"
+
+    def native(self):
+        p = N.ConvTP()
+        p.kernel[:] = list(self.kernel)
+        p.bias_value, p.act = self.bias, ACT[self.act]
+        return p
+
+
+@dataclass
+class EwP:
+    op: int  # EwOp: 0 add, 1 sub, 2 mul, 3 div
+    act: str = "none"
+
+    def native(self):
+        return N.EwP(self.op, ACT[self.act])
+
+
+@dataclass
+class LnP:
+    eps: float = 1e-5
+
+    def native(self):
+        return N.LnP(self.eps)
+
+
+@dataclass
+class ResizeNearestP:
+    scales: tuple
+    add_relu: bool = False
+
+    def native(self):
+        p = N.ResizeNearestP()
+        sc = list(self.scales) + [1.0] * (4 - len(self.scales))
+        p.scales[:] = sc[:4]
+        p.add_relu = int(self.add_relu)
+        return p
+
+
+@dataclass
+class ChannelGateP:
+    b1: int = -1
+    b2: int = -1
+    act1: str = "relu"
+    hard: bool = True
+    alpha: float = 1.0 / 6.0
+    beta: float = 0.5
+    offset: float = 0.0
+
+    def native(self):
+        return N.ChannelGateP(self.b1, self.b2, ACT[self.act1], int(self.hard), self.alpha, self.beta, self.offset)
+
+
+@dataclass
+class ConcatP:
+    axis: int
+
+    def native(self):
+        return N.ConcatP(self.axis)
+
+
+@dataclass
+class HardSigmoidP:
+    alpha: float
+    beta: float
+
+    def native(self):
+        return N.HardSigmoidP(self.alpha, self.beta)
+
+
+@dataclass
+class AttentionP:
+    scale: float
+    dims: tuple  # 3 x (n, h, t|s, d) logical axes
+    fix_axis: tuple = (-1, -1, -1)
+    fix_index: tuple = (0, 0, 0)
+    out_layout: Optional[tuple] = None
+
+    def native(self):
+        p = N.AttentionP()
+        p.scale = self.scale
+        for i in range(3):
+            p.dims[i][:] = list(self.dims[i])
+        p.fix_axis[:] = list(self.fix_axis)
+        p.fix_index[:] = list(self.fix_index)
+        p.out_layout[:] = list(self.out_layout) if self.out_layout is not None else [-1, -1, -1, -1]
+        return p
+
+
+@dataclass
+class PoolP:
+    kernel: tuple
+    strides: tuple
+    pads: tuple
+    relu: bool = False
+
+    def native(self):
+        p = N.PoolP()
+        p.kernel[:] = list(self.kernel)
+        p.strides[:] = list(self.strides)
+        p.pads[:] = list(self.pads)
+        p.fuse_relu = int(self.relu)
+        return p
+
+
+@dataclass
+class Node:
+    """ExecNode: op + value ids (+ params)."""
+
+    op: str
+    ins: list
+    outs: list
+    p: object = None
+    name: str = ""
+    ext: str = ""
+
+    def param_refs(self):
+        """Value ids read through the params (ExecNode.ParamRefs, ExecPlan.cs:246-263)."""
+        p = self.p
+        refs = []
+        if isinstance(p, ConvP):
+            refs = [p.bias, p.add]
+        elif isinstance(p, (GemmP, ConvTP)):
+            refs = [p.bias]
+        elif isinstance(p, ChannelGateP):
+            refs = [p.b1, p.b2]
+        return [r for r in refs if r >= 0]
+
+
+@dataclass
+class ExecPlan:
+    values: list
+    nodes: list
+    buf_offset: list
+    arena_floats: int
+    inputs: list
+    output: int
+    nhwc: bool = True
+
+    def buffer_of(self, vid: int) -> int:
+        return self.values[vid].buf
+
+    def to_native(self):
+        """Marshals the plan into a native ``sox_plan`` (the C# side would do the same from its ExecPlan)."""
+        lib = N.backend()
+        h = N.c_void_p()
+        N.check(lib.sox_plan_create(ctypes_byref(h)), "sox_plan_create")
+        try:
+            for v in self.values:
+                shape = (N.c_int32 * max(len(v.shape), 1))(*v.shape)
+                layout = (N.c_int32 * len(v.layout))(*v.layout) if v.layout is not None else None
+                data = None
+                nf = 0
+                if v.is_const:
+                    arr = np.ascontiguousarray(v.data, dtype=np.float32)
+                    data = arr.ctypes.data_as(N.c_void_p)
+                    nf = arr.size
+                vid = N.c_int32()
+                N.check(lib.sox_plan_add_value(h, shape, len(v.shape), layout, v.buf, data, nf, v.name.encode(),
+                                               ctypes_byref(vid)), f"value {v.name}")
+            for n in self.nodes:
+                ins = (N.c_int32 * max(len(n.ins), 1))(*n.ins)
+                outs = (N.c_int32 * len(n.outs))(*n.outs)
+                if n.p is None:
+                    pb, pn = None, 0
+                elif isinstance(n.p, (bytes, bytearray)):
+                    buf = ctypes_buffer(n.p)
+                    pb, pn = ctypes_addr(buf), len(n.p)
+                else:
+                    rec = n.p.native()
+                    pb, pn = ctypes_addr(rec), ctypes_sizeof(rec)
+                    n._rec = rec  # keep alive through the call
+                nid = N.c_int32()
+                N.check(lib.sox_plan_add_node(h, N.OP[n.op], ins, len(n.ins), outs, len(n.outs), pb, pn,
+                                              n.ext.encode() if n.ext else None, ctypes_byref(nid)),
+                        f"node {n.name or n.op}")
+            offs = (N.c_int64 * max(len(self.buf_offset), 1))(*self.buf_offset)
+            N.check(lib.sox_plan_set_arena(h, offs, len(self.buf_offset), self.arena_floats), "arena")
+            ins = (N.c_int32 * len(self.inputs))(*self.inputs)
+            N.check(lib.sox_plan_set_io(h, ins, len(self.inputs), self.output), "io")
+        except Exception:
+            lib.sox_plan_destroy(h)
+            raise
+        return h
+
+
+def ctypes_byref(x):
+    import ctypes
+    return ctypes.byref(x)
+
+
+def ctypes_buffer(b):
+    import ctypes
+    return ctypes.create_string_buffer(bytes(b), len(b))
+
+
+def ctypes_addr(x):
+    import ctypes
+    return ctypes.cast(ctypes.pointer(x), N.c_void_p) if not isinstance(x, ctypes.Array) else ctypes.cast(x, N.c_void_p)
+
+
+def ctypes_sizeof(x):
+    import ctypes
+    return ctypes.sizeof(x)
+
+
+def _out_size(i, k, s, p0, p1):
+    return (i + p0 + p1 - k) // s + 1
+
+
+class PlanBuilder:
+    """Builds fused NHWC ExecPlans node by node (what GraphCompiler emits for PlanTarget.Hip)."""
+
+    def __init__(self):
+        self.values: list = []
+        self.nodes: list = []
+        self._nbuf = 0
+        self.inputs: list = []
+
+    # ---- values ----
+    def _new_buf(self) -> int:
+        b = self._nbuf
+        self._nbuf += 1
+        return b
+
+    def activation(self, shape, layout=None, name="") -> int:
+        self.values.append(Value(tuple(int(s) for s in shape), layout, self._new_buf(), None, name))
+        return len(self.values) - 1
+
+    def image(self, n, c, h, w, name="") -> int:
+        """A rank-4 NHWC activation (logical [n,c,h,w], physical [n,h,w,c])."""
+        return self.activation((n, c, h, w), NHWC, name)
+
+    def input(self, shape, layout=None, name="input") -> int:
+        v = self.activation(shape, layout, name)
+        self.inputs.append(v)
+        return v
+
+    def const(self, data, name="") -> int:
+        arr = np.ascontiguousarray(data, dtype=np.float32)
+        self.values.append(Value(tuple(arr.shape), None, -1, arr, name))
+        return len(self.values) - 1
+
+    def alias(self, v, shape, layout=None, name="") -> int:
+        """Zero-copy reshape view (CValue.AliasOf): same buffer, new logical shape."""
+        src = self.values[v]
+        assert int(np.prod(shape)) == src.count, "alias must keep the element count"
+        self.values.append(Value(tuple(shape), layout, src.buf, None, name or src.name + "_view", alias_of=v))
+        return len(self.values) - 1
+
+    def nhwc_shape(self, v):
+        val = self.values[v]
+        return val.phys if len(val.shape) == 4 else None
+
+    def _node(self, op, ins, outs, p=None, name="", ext=""):
+        self.nodes.append(Node(op, list(ins), list(outs), p, name, ext))
+        return outs[0]
+
+    # ---- ops (fused forms) ----
+    def conv(self, x, w, b=None, *, stride=1, pad=None, group=1, act="none", add=None, pad_mode=0, pad_value=0.0,
+             pool=None, name=""):
+        """Conv (+bias)(+residual before act)(+act) [+ fused 2x2/2 max pool] (ConvP)."""
+        n, ih, iw, ic = self.values[x].phys
+        wv = w if isinstance(w, int) else self.const(w, name + ".w")
+        oc, _, kh, kw = self.values[wv].shape
+        s = (stride, stride) if isinstance(stride, int) else tuple(stride)
+        if pad is None:
+            pad = (kh // 2, kw // 2, kh // 2, kw // 2)
+        elif isinstance(pad, int):
+            pad = (pad, pad, pad, pad)
+        oh, ow = _out_size(ih, kh, s[0], pad[0], pad[2]), _out_size(iw, kw, s[1], pad[1], pad[3])
+        bv = -1 if b is None else (b if isinstance(b, int) else self.const(b, name + ".b"))
+        pp = None
+        if pool is not None:
+            pp = ((2, 2), (2, 2), (0, 0, 0, 0), bool(pool == "relu"))
+            oh, ow = oh // 2, ow // 2
+        y = self.image(n, oc, oh, ow, name)
+        p = ConvP(tuple(pad), s, (kh, kw), group=group, act=act, pad_mode=pad_mode, pad_value=pad_value, bias=bv,
+                  add=-1 if add is None else add, pool=pp)
+        return self._node("Conv", [x, wv], [y], p, name)
+
+    def gemm(self, a, w, b=None, *, act="none", trans_b=False, name=""):
+        """Gemm: act(A[..., K] . B + bias) with B a [K, N] (or [N, K]) const (GemmP)."""
+        av = self.values[a]
+        wv = w if isinstance(w, int) else self.const(w, name + ".w")
+        wshape = self.values[wv].shape
+        nn = wshape[0] if trans_b else wshape[1]
+        bv = -1 if b is None else (b if isinstance(b, int) else self.const(b, name + ".b"))
+        y = self.activation(tuple(av.shape[:-1]) + (nn,), None, name)
+        return self._node("Gemm", [a, wv], [y], GemmP(trans_b, bv, act), name)
+
+    def conv_transpose(self, x, w, b=None, *, act="none", name=""):
+        """ConvTranspose, stride == kernel, no pad (ConvTP)."""
+        n, ih, iw, ic = self.values[x].phys
+        wv = w if isinstance(w, int) else self.const(w, name + ".w")
+        _, oc, kh, kw = self.values[wv].shape
+        bv = -1 if b is None else (b if isinstance(b, int) else self.const(b, name + ".b"))
+        y = self.image(n, oc, ih * kh, iw * kw, name)
+        return self._node("ConvTranspose", [x, wv], [y], ConvTP((kh, kw), bv, act), name)
+
+    def channel_gate(self, x, w1, b1, w2, b2, *, act1="relu", hard=True, alpha=1.0 / 6.0, beta=0.5, offset=0.0,
+                     name=""):
+        """SE gate: GAP -> 1x1 (+act1) -> 1x1 -> (hard) sigmoid (+offset) -> [N,C,1,1] (ChannelGateP)."""
+        n, h, w, c = self.values[x].phys
+        w1v, w2v = self.const(w1, name + ".w1"), self.const(w2, name + ".w2")
+        b1v = -1 if b1 is None else self.const(b1, name + ".b1")
+        b2v = -1 if b2 is None else self.const(b2, name + ".b2")
+        y = self.image(n, c, 1, 1, name)
+        return self._node("ChannelGate", [x, w1v, w2v], [y], ChannelGateP(b1v, b2v, act1, hard, alpha, beta, offset),
+                          name)
+
+    def ew(self, a, b, op, *, act="none", name=""):
+        """Elementwise Add/Sub/Mul/Div with broadcast (EwP). Output takes the larger operand's shape."""
+        va, vb = self.values[a], self.values[b]
+        big = va if va.count >= vb.count else vb
+        y = self.activation(big.shape, big.layout, name)
+        return self._node("Elementwise", [a, b], [y], EwP(op, act), name)
+
+    def add(self, a, b, **kw):
+        return self.ew(a, b, 0, **kw)
+
+    def mul(self, a, b, **kw):
+        return self.ew(a, b, 2, **kw)
+
+    def resize_nearest(self, x, scale, add=None, add_relu=False, name=""):
+        """Nearest x`scale` upsample (+ [relu] same-shape addend) (ResizeNearestP)."""
+        n, h, w, c = self.values[x].phys
+        y = self.image(n, c, h * scale, w * scale, name)
+        ins = [x] if add is None else [x, add]
+        return self._node("ResizeNearest", ins, [y], ResizeNearestP((1.0, 1.0, float(scale), float(scale)), add_relu),
+                          name)
+
+    def concat_channels(self, xs, name=""):
+        n, h, w, _ = self.values[xs[0]].phys
+        c = sum(self.values[x].phys[3] for x in xs)
+        y = self.image(n, c, h, w, name)
+        return self._node("Concat", xs, [y], ConcatP(1), name)
+
+    def layer_norm(self, x, gamma, beta, eps=1e-5, name=""):
+        gv, bv = self.const(gamma, name + ".g"), self.const(beta, name + ".b")
+        val = self.values[x]
+        y = self.activation(val.shape, val.layout, name)
+        return self._node("LayerNorm", [x, gv, bv], [y], LnP(eps), name)
+
+    def softmax(self, x, name=""):
+        val = self.values[x]
+        y = self.activation(val.shape, val.layout, name)
+        return self._node("Softmax", [x], [y], None, name)
+
+    def unary(self, op, x, name=""):
+        val = self.values[x]
+        y = self.activation(val.shape, val.layout, name)
+        return self._node(op, [x], [y], None, name)
+
+    def attention(self, qkv, heads, head_dim, scale, name=""):
+        """Fused attention over a packed [N, T, 3*H*D] QKV tensor viewed as [N, T, 3, H, D]
+        (AttentionP with FixAxis 2 = 0/1/2); output [N, H, T, D] stored as [N, T, H, D]."""
+        nb, t, c3 = self.values[qkv].shape
+        view = self.alias(qkv, (nb, t, 3, heads, head_dim), None, name + ".qkv5")
+        y = self.activation((nb, heads, t, head_dim), (0, 2, 1, 3), name)
+        dims = ((0, 3, 1, 4),) * 3
+        p = AttentionP(scale, dims, (2, 2, 2), (0, 1, 2), (0, 2, 1, 3))
+        self._node("Attention", [view, view, view], [y], p, name)
+        # [N, T, H*D] token view of the output (its transpose dissolved into the layout)
+        return self.alias(y, (nb, t, heads * head_dim), None, name + ".tokens")
+
+    def ext(self, name, ins, out_shape, params: bytes = b"", layout=None, node_name=""):
+        """ExecOp.Ext node of a consumer-registered operator."""
+        y = self.activation(out_shape, layout, node_name or name)
+        return self._node("Ext", ins, [y], bytes(params), node_name or name, ext=name)
+
+    # ---- finish: arena planning ----
+    def build(self, output: int) -> ExecPlan:
+        return plan_arena(self.values, self.nodes, self.inputs, output, self._nbuf)
+
+
+def plan_arena(values, nodes, inputs, output, nbuf, align=32) -> ExecPlan:
+    """Lifetime-packed arena (the PlanArena analogue, GraphCompiler.cs:1336-1474): each buffer is
+    live from its producing node to its last reader (inputs from the start, the output to the end);
+    first-fit placement at `align`-element granularity; no buffer overlaps a live one."""
+    size = [0] * nbuf
+    for v in values:
+        if v.buf >= 0:
+            size[v.buf] = max(size[v.buf], v.count)
+    first = [None] * nbuf
+    last = [-1] * nbuf
+    for b in {values[i].buf for i in inputs}:
+        first[b] = -1
+    for i, n in enumerate(nodes):
+        for vid in list(n.ins) + n.param_refs():
+            b = values[vid].buf
+            if b >= 0:
+                last[b] = max(last[b], i)
+        for vid in n.outs:
+            b = values[vid].buf
+            if first[b] is None:
+                first[b] = i
+    end = len(nodes)
+    last[values[output].buf] = end
+    for b in {values[i].buf for i in inputs}:
+        last[b] = end  # inputs stay intact for the whole run (CompileOptions.ReleaseInputs = false)
+    offset = [0] * nbuf
+    live: list = []  # (start, stop, buf)
+    order = sorted((b for b in range(nbuf) if first[b] is not None), key=lambda b: (first[b], -size[b]))
+    top = 0
+    for b in order:
+        live = [iv for iv in live if last[iv[2]] >= first[b]]
+        sz = (size[b] + align - 1) // align * align
+        cand = 0
+        for s, e, _ in sorted(live):
+            if cand + sz <= s:
+                break
+            cand = max(cand, e)
+        offset[b] = cand
+        live.append((cand, cand + sz, b))
+        top = max(top, cand + sz)
+    return ExecPlan(values, nodes, offset, top, list(inputs), output)

@@ -1,0 +1,199 @@
+"""HIP kernels vs the CPU oracle, one fused node at a time (the VkKernelTests / GpuOpTests pattern,
+tests/Sdcb.SimdOnnx.Tests/VkKernelTests.cs:62-196, GpuOpTests.cs:17-325).
+
+Every case builds a one-node ExecPlan, runs it through HipBackend -> HipGraphModel ->
+HipInferenceSession (the C ABI of include/sox_backend.h) and compares with the oracle on the same
+inputs. Tolerances, max-rel = max|gpu - cpu| / max|cpu|:
+  fp32 storage: 1e-4;
+  fp16 storage: operands pre-rounded to fp16 so both sides multiply identical values
+  (VkKernelTests.cs:141-143), 2e-3 (fp32 accumulation, one fp16 rounding of the output).
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+from simdonnx_amd import synth
+from simdonnx_amd.backend import HipInferenceSession
+from simdonnx_amd.plan import NHWC, PlanBuilder
+from tests.conftest import max_rel
+
+pytestmark = pytest.mark.gpu
+
+G = np.load(os.path.join(os.path.dirname(__file__), "golden", "golden.npz"))
+ACTS = ["none", "relu", "sigmoid", "gelu", "hardswish", "swish"]
+TOL = {False: 1e-4, True: 2e-3}
+
+
+def f16(a):
+    return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+
+
+def run(hip, plan, inputs, f16_storage):
+    print(f"[gpu] plan {len(plan.nodes)} nodes f16={f16_storage}", flush=True)
+    with HipInferenceSession(hip.graph(plan, f16_storage)) as s:
+        for i, x in enumerate(inputs):
+            s.set_input(x, i)
+        return s.run().copy()
+
+
+def conv_plan(x, w, b, add, stride, pads, act, pad_mode, pad_value, group=1):
+    pb = PlanBuilder()
+    n, h, ww, c = x.shape
+    xv = pb.input((n, c, h, ww), NHWC, "x")
+    addv = None
+    ins = [x]
+    if add is not None:
+        addv = pb.input((add.shape[0], add.shape[3], add.shape[1], add.shape[2]), NHWC, "add")
+        ins.append(add)
+    y = pb.conv(xv, w, b, stride=stride, pad=pads, group=group, act=act, add=addv, pad_mode=pad_mode,
+                pad_value=pad_value, name="conv")
+    return pb.build(y), ins
+
+
+@pytest.mark.parametrize("half", [False, True], ids=["f32", "f16"])
+@pytest.mark.parametrize("i", range(int(G["conv_n"][0])))
+def test_conv_matches_oracle(hip, i, half):
+    ic, oc, k, s, h, w, mode, act, res = [int(v) for v in G[f"conv{i}_meta"]]
+    pv = float(G[f"conv{i}_pv"][0])
+    cv = f16 if half else (lambda a: a)
+    x, wt, b = cv(G[f"conv{i}_x"]), cv(G[f"conv{i}_w"]), G[f"conv{i}_b"]
+    add = cv(G[f"conv{i}_add"]) if res else None
+    pads = (k // 2,) * 4
+    plan, ins = conv_plan(x, wt, b, add, (s, s), pads, ACTS[act], mode, pv)
+    got = run(hip, plan, ins, half)
+    want = O.conv(x, wt, b, add, stride=(s, s), pads=pads, act=ACTS[act], pad_mode=mode, pad_value=pv)
+    assert max_rel(got, want) < TOL[half]
+
+
+@pytest.mark.parametrize("half", [False, True], ids=["f32", "f16"])
+@pytest.mark.parametrize("case", [(3, 16, 2, 64, 40), (64, 128, 1, 33, 29), (32, 96, 2, 30, 22), (8, 64, 2, 21, 17),
+                                  (128, 256, 1, 16, 16), (16, 160, 1, 24, 20)])
+def test_conv_shapes_batch(hip, case, half):
+    """conv_cm route coverage (VkKernelTests.ConvCm_MatchesCpu shapes): stems, stride 2, wide oc, batch 2."""
+    ic, oc, s, h, w = case
+    cv = f16 if half else (lambda a: a)
+    x = cv(synth.uniform(11, 1, (2, h, w, ic), -1, 1))
+    wt = cv(synth.uniform(11, 2, (oc, ic, 3, 3), -0.25, 0.25))
+    b = synth.uniform(11, 3, (oc,), -0.1, 0.1)
+    plan, ins = conv_plan(x, wt, b, None, (s, s), (1, 1, 1, 1), "relu", 0, 0.0)
+    got = run(hip, plan, ins, half)
+    want = O.conv(x, wt, b, stride=(s, s), pads=(1, 1, 1, 1), act="relu")
+    assert max_rel(got, want) < TOL[half]
+
+
+@pytest.mark.parametrize("half", [False, True], ids=["f32", "f16"])
+@pytest.mark.parametrize("i", range(int(G["gemm_n"][0])))
+def test_gemm_matches_oracle(hip, i, half):
+    m, k, n, tb, act = [int(v) for v in G[f"gemm{i}_meta"]]
+    cv = f16 if half else (lambda a: a)
+    a, bm, bias = cv(G[f"gemm{i}_a"]), cv(G[f"gemm{i}_b"]), G[f"gemm{i}_bias"]
+    pb = PlanBuilder()
+    av = pb.input((m, k), None, "a")
+    y = pb.gemm(av, bm, bias, act=ACTS[act], trans_b=bool(tb), name="gemm")
+    got = run(hip, pb.build(y), [a], half)
+    want = O.gemm(a, bm, bias, trans_b=bool(tb), act=ACTS[act])
+    assert max_rel(got, want) < TOL[half]
+
+
+@pytest.mark.parametrize("half", [False, True], ids=["f32", "f16"])
+@pytest.mark.parametrize("i", range(int(G["dw_n"][0])))
+def test_depthwise_matches_oracle(hip, i, half):
+    c, k, s, h, w, mode, act = [int(v) for v in G[f"dw{i}_meta"]]
+    cv = f16 if half else (lambda a: a)
+    x, wt, b = cv(G[f"dw{i}_x"]), cv(G[f"dw{i}_w"]), G[f"dw{i}_b"]
+    plan, ins = conv_plan(x, wt, b, None, (s, s), (k // 2,) * 4, ACTS[act], mode, 0.0, group=c)
+    got = run(hip, plan, ins, half)
+    want = O.conv(x, wt, b, stride=(s, s), pads=(k // 2,) * 4, group=c, act=ACTS[act], pad_mode=mode)
+    assert max_rel(got, want) < TOL[half]
+
+
+@pytest.mark.parametrize("half", [False, True], ids=["f32", "f16"])
+@pytest.mark.parametrize("i", range(int(G["ct_n"][0])))
+def test_conv_transpose_matches_oracle(hip, i, half):
+    ic, oc, k, h, w, act = [int(v) for v in G[f"ct{i}_meta"]]
+    cv = f16 if half else (lambda a: a)
+    x, wt, b = cv(G[f"ct{i}_x"]), cv(G[f"ct{i}_w"]), G[f"ct{i}_b"]
+    pb = PlanBuilder()
+    xv = pb.input((1, ic, h, w), NHWC, "x")
+    y = pb.conv_transpose(xv, wt, b, act=ACTS[act], name="convt")
+    got = run(hip, pb.build(y), [x], half)
+    want = O.conv_transpose(x, wt, b, act=ACTS[act])
+    assert max_rel(got, want) < TOL[half]
+
+
+@pytest.mark.parametrize("half", [False, True], ids=["f32", "f16"])
+def test_se_block_matches_oracle(hip, half):
+    """ChannelGate + broadcast multiply (the fused SE of GraphCompiler.cs:355, VkGraph.cs:547-551)."""
+    cv = f16 if half else (lambda a: a)
+    x = cv(G["se_x"])
+    n, h, w, c = x.shape
+    pb = PlanBuilder()
+    xv = pb.input((n, c, h, w), NHWC, "x")
+    gate = pb.channel_gate(xv, G["se_w1"], G["se_b1"], G["se_w2"], G["se_b2"], name="se")
+    y = pb.mul(xv, gate, name="scale")
+    got = run(hip, pb.build(y), [x], half)
+    s = O.channel_gate(x, G["se_w1"], G["se_b1"], G["se_w2"], G["se_b2"])
+    want = x * s[:, None, None, :]
+    assert max_rel(got, want) < TOL[half]
+
+
+@pytest.mark.parametrize("half", [False, True], ids=["f32", "f16"])
+def test_nearest_add_and_concat(hip, half):
+    cv = f16 if half else (lambda a: a)
+    x, add = cv(G["near_x"]), cv(G["near_add"])
+    pb = PlanBuilder()
+    xv = pb.input((1, 16, 7, 9), NHWC, "x")
+    av = pb.input((1, 16, 14, 18), NHWC, "add")
+    up = pb.resize_nearest(xv, 2, add=av, add_relu=True, name="up")
+    y = pb.concat_channels([up, av], name="cat")
+    got = run(hip, pb.build(y), [x, add], half)
+    want = np.concatenate([O.resize_nearest(x, 2, 2, add, True), add], axis=-1)
+    assert max_rel(got, want) < TOL[half]
+
+
+@pytest.mark.parametrize("half", [False, True], ids=["f32", "f16"])
+def test_layernorm_softmax(hip, half):
+    cv = f16 if half else (lambda a: a)
+    x = cv(G["ln_x"])
+    pb = PlanBuilder()
+    xv = pb.input((37, 192), None, "x")
+    y = pb.layer_norm(xv, G["ln_g"], G["ln_b"], 1e-5, name="ln")
+    got = run(hip, pb.build(y), [x], half)
+    assert max_rel(got, O.layer_norm(x, G["ln_g"], G["ln_b"], 1e-5)) < TOL[half]
+    x = cv(G["sm_x"])
+    pb = PlanBuilder()
+    xv = pb.input(x.shape, None, "x")
+    y = pb.softmax(xv, name="softmax")
+    got = run(hip, pb.build(y), [x], half)
+    assert max_rel(got, O.softmax(x)) < TOL[half]
+
+
+@pytest.mark.parametrize("half", [False, True], ids=["f32", "f16"])
+def test_attention_packed_qkv(hip, half):
+    """Fused attention over a packed [N, T, 3*H*D] qkv (GpuOpTests attention packed-qkv case)."""
+    nb, t, heads, d = 4, 80, 6, 32
+    cv = f16 if half else (lambda a: a)
+    qkv = cv(synth.uniform(5, 1, (nb, t, 3 * heads * d), -1, 1))
+    pb = PlanBuilder()
+    xv = pb.input(qkv.shape, None, "qkv")
+    y = pb.attention(xv, heads, d, d ** -0.5, name="attn")
+    got = run(hip, pb.build(y), [qkv], half)
+    q5 = qkv.reshape(nb, t, 3, heads, d)
+    q, k, v = (np.ascontiguousarray(q5[:, :, j].transpose(0, 2, 1, 3)).reshape(nb * heads, t, d) for j in range(3))
+    want = O.attention(q, k, v, d ** -0.5).reshape(nb, heads, t, d).transpose(0, 2, 1, 3).reshape(nb, t, heads * d)
+    assert max_rel(got.reshape(want.shape), want) < TOL[half]
+
+
+def test_replay_matches_direct(hip):
+    """A HIP-graph replay of the dispatch list gives the direct launches' bits on every replay."""
+    x = f16(G["conv12_x"])
+    plan, ins = conv_plan(x, f16(G["conv12_w"]), G["conv12_b"], None, (1, 1), (1, 1, 1, 1), "relu", 0, 0.0)
+    with HipInferenceSession(hip.graph(plan, True)) as s:
+        s.set_input(x)
+        direct = s.run().copy()
+        s.set_replay(True)
+        for _ in range(3):
+            s.set_input(x)
+            assert np.array_equal(s.run(), direct)
