@@ -95,6 +95,96 @@ def bench_conv(steps: int):
     return dict(us=us, tflops=fl / (us * 1e-6) / 1e12, frac_fp32_peak=fl / (us * 1e-6) / 1e12 / PEAK_FP32_TFLOPS)
 
 
+NETWORKS = {
+    "mobilenetv3": ("mobilenetv3_small", "MobileNetV3-small block stack, 1x3x640x640", 1),
+    "detector": ("dbnet", "DBNet-style detector (MobileNetV3-small + FPN + ConvT head), 1x3x960x960", 1),
+    "recognizer": ("svtr", "SVTR-style recognizer, 32x3x48x320", 32),
+}
+
+
+def bench_network(key: str, steps: int):
+    """ms per image of a whole network plan, HIP-graph replay, inputs resident (and with staging),
+    plus the per-kernel-class roofline from a per-dispatch event profile."""
+    from simdonnx_amd import graphs
+    from simdonnx_amd.backend import HipBackend, HipInferenceSession
+    fn, desc, images = NETWORKS[key]
+    hip = HipBackend.default()
+    plan, ins = getattr(graphs, fn)()
+    g = hip.graph(plan, True)
+    with HipInferenceSession(g) as s:
+        s.set_input(ins[0])
+        s.set_replay(True)
+        s.run()
+        s.time(5)
+        ms = s.time(steps) / steps
+        ms_e2e = s.time(max(steps // 2, 1), staging=True) / max(steps // 2, 1)
+        prof = s.profile(5)
+    ndisp = len(g.dispatches)
+    g.release()
+    per_node = {}
+    for name, node, t in prof:
+        per_node.setdefault(node, [name, 0.0])[1] += t
+    classes = {}
+    tot_fl = tot_by = 0
+    for node, (name, t) in per_node.items():
+        fl, by = graphs.node_cost(plan, plan.nodes[node])
+        tot_fl += fl
+        tot_by += by
+        c = classes.setdefault(name, dict(ms=0.0, n=0, flops=0, bytes=0))
+        c["ms"] += t
+        c["n"] += 1
+        c["flops"] += fl
+        c["bytes"] += by
+    out = []
+    for name, c in sorted(classes.items(), key=lambda kv: -kv[1]["ms"]):
+        gbs = c["bytes"] / (c["ms"] * 1e-3) / 1e9
+        tfl = c["flops"] / (c["ms"] * 1e-3) / 1e12
+        bound = "mfma" if name in ("conv", "gemm") and c["flops"] / max(c["bytes"], 1) > 313 else "hbm"
+        frac = tfl / PEAK_FP16_TFLOPS if bound == "mfma" else gbs / PEAK_HBM_GBS
+        out.append(dict(kernel=name, nodes=c["n"], ms=round(c["ms"], 4), gb_s=round(gbs, 1), tflop_s=round(tfl, 2),
+                        bound=bound, frac=round(frac, 4)))
+    return dict(workload=desc, ms_per_image=round(ms / images, 4), images_per_s=round(images / (ms * 1e-3), 1),
+                ms_per_batch=round(ms, 4), ms_per_image_with_staging=round(ms_e2e / images, 4), dispatches=ndisp,
+                gflop=round(tot_fl / 1e9, 3), algorithmic_mb=round(tot_by / 1e6, 1),
+                kernel_sum_ms=round(sum(t for _, _, t in prof), 4), kernels=out[:8])
+
+
+def bench_copy(steps: int):
+    """Plain copy of 128 Mi fp16 elements through the backend (the traffic-counter calibration kernel)."""
+    from simdonnx_amd.backend import HipBackend, HipInferenceSession
+    from simdonnx_amd.plan import PlanBuilder
+    import numpy as np
+    pb = PlanBuilder()
+    n = 128 << 20
+    x = pb.input((n,), None, "x")
+    y = pb.unary("Copy", x, name="copy")
+    plan = pb.build(y)
+    hip = HipBackend.default()
+    g = hip.graph(plan, True)
+    with HipInferenceSession(g) as s:
+        s.set_input(np.zeros(n, np.float32))
+        s.run()
+        ms = s.time(steps) / steps
+    g.release()
+    return dict(bytes_per_launch=2 * n * 2, ms=ms, gb_s=2 * n * 2 / (ms * 1e-3) / 1e9)
+
+
+def cpu_detector_ms():
+    """The oracle running the whole detector plan (reference CPU kernels restated), ms per image."""
+    import oracle as O
+    from oracle.interp import run_plan
+    from simdonnx_amd import graphs
+    O.set_threads(cpu_threads())
+    plan, ins = graphs.dbnet()
+    run_plan(plan, ins)
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run_plan(plan, ins)
+        ts.append(time.perf_counter() - t0)
+    return round(statistics.median(ts) * 1e3, 2)
+
+
 def cpu_baseline(budget_s: float = 12.0):
     """The oracle Gemm + GELU on the full workload (M = 8192), all host threads, median of runs."""
     import oracle as O
@@ -128,18 +218,25 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-extra", action="store_true", help="skip the secondary workloads")
+    ap.add_argument("--only", choices=["gemm", "conv", "detector", "recognizer", "mobilenetv3", "copy"],
+                    help="run one workload only (profiling runs); prints its own JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this backend is single-device (the reference's GPU backends are; "
               "VkDevice.cs:128). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    if args.only:
+        fn = {"gemm": lambda: bench_gemm(args.steps, args.warmup), "conv": lambda: bench_conv(args.steps),
+              "copy": lambda: bench_copy(args.steps)}.get(args.only) or (lambda: bench_network(args.only, args.steps))
+        r = fn()
+        print(json.dumps({"only": args.only, **{k: v for k, v in r.items() if k != "kernel_ms"}}), flush=True)
+        return
     r = bench_gemm(args.steps, args.warmup)
     per_s = r["per_launch_ms"] * 1e-3
     tflops = r["flops"] / per_s / 1e12
     log(f"gemm: {r['per_launch_ms']*1e3:.1f} us/launch, {tflops:.1f} TFLOP/s, dispatches {r['dispatches']}")
     out = {
-        "metric": "fused MatMul+bias+GELU TFLOP/s (fp16 MFMA, fp32 accum)",
+        "metric": "fused MatMul+bias+GELU TFLOP/s (fp16 MFMA, fp32 accum); detector ms/image",
         "value": round(tflops, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -157,13 +254,22 @@ def main():
                      "frac": round(tflops / PEAK_FP16_TFLOPS, 4),
                      "traffic": traffic_from_profiles("matmul_bias_gelu")},
     }
-    if not args.no_extra:
+    for key in ("detector", "recognizer", "mobilenetv3"):
         try:
-            out["conv3x3_bias_relu_fp32"] = bench_conv(200)
+            out[key] = bench_network(key, 50)
+            log(f"{key}: {out[key]['ms_per_image']} ms/image")
         except Exception as e:  # reported, never hidden
-            out["conv3x3_bias_relu_fp32"] = {"error": str(e)}
+            out[key] = {"error": repr(e)}
+    try:
+        out["conv3x3_bias_relu_fp32"] = bench_conv(200)
+    except Exception as e:
+        out["conv3x3_bias_relu_fp32"] = {"error": repr(e)}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
+        try:
+            out["cpu_baseline"]["detector_ms_per_image"] = cpu_detector_ms()
+        except Exception as e:
+            out["cpu_baseline"]["detector_ms_per_image"] = repr(e)
     print(json.dumps(out), flush=True)
 
 

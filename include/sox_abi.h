@@ -93,6 +93,7 @@ typedef struct sox_gap_args {
 /*
  * Squeeze-excitation gate (se_gate.comp; Kernels/Nhwc.Det.cs:287-314), one workgroup per image:
  *   mean = sum(part)/hw; hid = act1(b1 + W1 mean); z = b2 + W2 hid; s = gate(z) + offset  (out [n][c]).
+ *   w1 is packed transposed [c][r], w2 transposed [r][c] (coalesced per-output columns).
  */
 typedef struct sox_se_args {
     const float* part;
@@ -114,7 +115,7 @@ typedef struct sox_chan_args {
     int64_t rows;  /* n*h*w */
     int32_t c, hw;
     int32_t op;    /* EwOp: 0 add, 1 sub, 2 mul, 3 div */
-    int32_t flags; /* bit0 reversed operands, act<<4 */
+    int32_t flags; /* bit0 reversed operands, bit1 v is one [c] vector for every image, act<<4 */
 } sox_chan_args;
 
 /* Same-shape elementwise binary op + act (ew2v.comp). */

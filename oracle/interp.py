@@ -17,14 +17,45 @@ def _phys(plan, vid, arr):
     return np.ascontiguousarray(arr, dtype=np.float32).reshape(plan.values[vid].phys)
 
 
-def run_plan(plan, inputs, keep=False):
-    """Returns the output (physical layout); with keep=True also the dict of every value."""
+def f32_params(plan):
+    """Value ids a GPU plan keeps in fp32 on fp16 graphs: bias, LayerNorm and SE parameters
+    (ConstKind.F32, Engine/Extensions.cs:145)."""
+    ids = set()
+    for n in plan.nodes:
+        if n.op in ("Conv", "Gemm", "ConvTranspose") and n.p.bias >= 0:
+            ids.add(n.p.bias)
+        if n.op == "LayerNorm":
+            ids.update(n.ins[1:])
+        if n.op == "ChannelGate":
+            ids.update(n.ins[1:])
+            ids.update(r for r in (n.p.b1, n.p.b2) if r >= 0)
+    return ids
+
+
+def _f16(a):
+    return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+
+
+def run_plan(plan, inputs, keep=False, f16_storage=False):
+    """Returns the output (physical layout); with keep=True also the dict of every value.
+
+    f16_storage=True applies the reference GPU numeric contract on the CPU: graph inputs, weights
+    and every stored activation are rounded to IEEE fp16 (round to nearest even) at the points the
+    GPU stores them (Backends/Vulkan/VkGraph.cs:33-43, Engine/Extensions.cs:311-316), while bias /
+    norm / SE parameters stay fp32 and all math stays fp32."""
     env = {}
     vals = plan.values
+    keep32 = f32_params(plan) if f16_storage else set()
+    rnd = _f16 if f16_storage else (lambda a: a)
+    consts = {}
 
     def get(vid):
         v = vals[vid]
         if v.is_const:
+            if f16_storage and vid not in keep32:
+                if vid not in consts:
+                    consts[vid] = _f16(v.data)
+                return consts[vid]
             return v.data
         if vid in env:
             return env[vid]
@@ -33,7 +64,7 @@ def run_plan(plan, inputs, keep=False):
         raise KeyError(f"value {vid} ({v.name}) read before written")
 
     for vid, x in zip(plan.inputs, inputs):
-        env[vid] = _phys(plan, vid, x)
+        env[vid] = rnd(_phys(plan, vid, x))
     for node in plan.nodes:
         p = node.p
         out = node.outs[0]
@@ -76,7 +107,7 @@ def run_plan(plan, inputs, keep=False):
                 full, vec, rev = (a, b, False) if a.size > b.size else (b, a, True)
                 nb = full.shape[0]
                 c = full.shape[-1]
-                vec = vec.reshape(nb, c)
+                vec = np.broadcast_to(vec.reshape(-1, c), (nb, c))  # [N,C,1,1] gate or a [C,1,1] const
                 y = np.concatenate([O.channel_broadcast(full[i].reshape(-1, c), vec[i], op=p.op, rev=rev, act=act)
                                     .reshape(1, -1) for i in range(nb)])
         elif node.op in ("Relu", "Sigmoid", "Gelu", "HardSwish", "Swish"):
@@ -105,6 +136,6 @@ def run_plan(plan, inputs, keep=False):
             y = np.ascontiguousarray(o.transpose(0, 2, 1, 3))  # stored [N, T, H, D]
         else:
             raise NotImplementedError(f"oracle interpreter: {node.op}")
-        env[out] = np.ascontiguousarray(y, dtype=np.float32).reshape(oshape)
+        env[out] = rnd(np.ascontiguousarray(y, dtype=np.float32).reshape(oshape))
     res = get(plan.output)
     return (res, env) if keep else res

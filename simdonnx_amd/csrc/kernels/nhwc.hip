@@ -19,6 +19,19 @@ template <typename T, int CV> struct VecT {
     typedef T Vec __attribute__((ext_vector_type(CV)));
 };
 
+// Wave reductions (wave64).
+SOX_DEV float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+SOX_DEV float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
 // ------------------------------------------------------------------------------------------
 // Depthwise k x k (Kernels/Nhwc.cs:496-631): acc = bias[c] + sum over taps (row-major) x*w,
 // + residual, act. One work item = CV channels of one output pixel; taps outside a
@@ -114,31 +127,68 @@ extern "C" __global__ void __launch_bounds__(256) sox_convt_f32(sox_convt_args p
 
 // ------------------------------------------------------------------------------------------
 // Global-average-pool partials (gap_part.comp): part[b][chunk][c] = sum over the chunk's pixels.
-// Grid (ceil(c/64), chunks, n), 256 threads = 64 channels x 4 pixel phases, reduced in LDS.
+// Grid (chunks, n); the 256 threads are (c / CV) channel vectors x P pixel phases, each thread
+// accumulating CV channels of every P-th pixel of the chunk (16-byte loads, many in flight),
+// then the P phases are reduced in LDS in a fixed order.
 // ------------------------------------------------------------------------------------------
-template <typename T>
+template <typename T, int CV>
 __device__ __forceinline__ void gap_body(const sox_gap_args& p) {
-    __shared__ float red[4][64];
-    const int lc = threadIdx.x & 63, ph = threadIdx.x >> 6;
-    const int c = blockIdx.x * 64 + lc;
-    const int chunk = blockIdx.y, b = blockIdx.z;
+    __shared__ float red[256 * CV];
+    const int cg = p.c / CV;
+    const int P = max(1, 256 / cg);
+    const int t = threadIdx.x;
+    const int g = t % cg, ph = t / cg;
+    const int chunk = blockIdx.x, b = blockIdx.y;
     const long p0 = (long)chunk * p.hw / p.chunks, p1 = (long)(chunk + 1) * p.hw / p.chunks;
-    const T* __restrict__ x = (const T*)p.x + (long)b * p.hw * p.c;
-    float s = 0.0f;
-    if (c < p.c)
-        for (long px = p0 + ph; px < p1; px += 4) s += to_f(x[px * p.c + c]);
-    red[ph][lc] = s;
+    typedef typename VecT<T, CV>::Vec Vec;
+    if (cg > 256) {  // more channel vectors than threads: each thread owns whole channel vectors
+        const T* __restrict__ xb = (const T*)p.x + (long)b * p.hw * p.c;
+        for (int gg = t; gg < cg; gg += 256) {
+            float a2[CV];
+#pragma unroll
+            for (int e = 0; e < CV; e++) a2[e] = 0.0f;
+            for (long px = p0; px < p1; px++) {
+                Vec v = *(const Vec*)(xb + px * p.c + gg * CV);
+#pragma unroll
+                for (int e = 0; e < CV; e++) a2[e] += to_f(v[e]);
+            }
+#pragma unroll
+            for (int e = 0; e < CV; e++) p.part[((long)b * p.chunks + chunk) * p.c + gg * CV + e] = a2[e];
+        }
+        return;
+    }
+    float acc[CV];
+#pragma unroll
+    for (int e = 0; e < CV; e++) acc[e] = 0.0f;
+    if (ph < P && t < cg * P) {
+        const T* __restrict__ x = (const T*)p.x + (long)b * p.hw * p.c + g * CV;
+        for (long px = p0 + ph; px < p1; px += P) {
+            Vec v = *(const Vec*)(x + px * p.c);
+#pragma unroll
+            for (int e = 0; e < CV; e++) acc[e] += to_f(v[e]);
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < CV; e++) red[t * CV + e] = acc[e];
     __syncthreads();
-    if (ph == 0 && c < p.c)
-        p.part[((long)b * p.chunks + chunk) * p.c + c] = (red[0][lc] + red[1][lc]) + (red[2][lc] + red[3][lc]);
+    for (int ch = t; ch < p.c; ch += 256) {
+        int gg = ch / CV, e = ch - gg * CV;
+        float s = 0.0f;
+        for (int q = 0; q < P && q * cg + gg < 256; q++) s += red[(q * cg + gg) * CV + e];
+        p.part[((long)b * p.chunks + chunk) * p.c + ch] = s;
+    }
 }
 
-extern "C" __global__ void __launch_bounds__(256) sox_gap_f16(sox_gap_args p) { gap_body<half_t>(p); }
-extern "C" __global__ void __launch_bounds__(256) sox_gap_f32(sox_gap_args p) { gap_body<float>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_gap_f16_v(sox_gap_args p) { gap_body<half_t, 8>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_gap_f16_s(sox_gap_args p) { gap_body<half_t, 1>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_gap_f32_v(sox_gap_args p) { gap_body<float, 4>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_gap_f32_s(sox_gap_args p) { gap_body<float, 1>(p); }
 
 // ------------------------------------------------------------------------------------------
 // SE gate (se_gate.comp; Kernels/Nhwc.Det.cs:287-314), one workgroup of 256 per image.
 // ------------------------------------------------------------------------------------------
+// w1 arrives transposed as [c][r] and w2 as [r][c] (SE weight packing of the HIP backend), so one
+// thread per output reads a coalesced column and no cross-lane reduction is needed.
 template <typename T>
 __device__ __forceinline__ void se_body(const sox_se_args& p) {
     extern __shared__ float sm[];
@@ -153,23 +203,23 @@ __device__ __forceinline__ void se_body(const sox_se_args& p) {
     }
     __syncthreads();
     for (int j = threadIdx.x; j < p.r; j += blockDim.x) {
-        float s = (p.flags & 1) ? p.b1[j] : 0.0f;
-        const float* row = p.w1 + (long)j * p.c;
-        for (int k = 0; k < p.c; k++) s = __builtin_fmaf(row[k], mean[k], s);
+        float s = 0.0f;
+        for (int k = 0; k < p.c; k++) s = __builtin_fmaf(p.w1[(long)k * p.r + j], mean[k], s);
+        s += (p.flags & 1) ? p.b1[j] : 0.0f;
         hid[j] = (p.flags & 4) ? fmaxf(s, 0.0f) : s;
     }
     __syncthreads();
     for (int c = threadIdx.x; c < p.c; c += blockDim.x) {
-        float z = (p.flags & 2) ? p.b2[c] : 0.0f;
-        const float* row = p.w2 + (long)c * p.r;
-        for (int j = 0; j < p.r; j++) z = __builtin_fmaf(row[j], hid[j], z);
+        float z = 0.0f;
+        for (int j = 0; j < p.r; j++) z = __builtin_fmaf(p.w2[(long)j * p.c + c], hid[j], z);
+        z += (p.flags & 2) ? p.b2[c] : 0.0f;
         float g = (p.flags & 8) ? fminf(fmaxf(z * p.alpha + p.beta, 0.0f), 1.0f) : sox_sigmoid(z);
         ((T*)p.s)[(long)b * p.c + c] = (T)(g + p.offset);
     }
 }
 
-extern "C" __global__ void __launch_bounds__(256) sox_se_f16(sox_se_args p) { se_body<half_t>(p); }
-extern "C" __global__ void __launch_bounds__(256) sox_se_f32(sox_se_args p) { se_body<float>(p); }
+extern "C" __global__ void __launch_bounds__(1024) sox_se_f16(sox_se_args p) { se_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(1024) sox_se_f32(sox_se_args p) { se_body<float>(p); }
 
 // ------------------------------------------------------------------------------------------
 // Per-channel broadcast y[p, c] = act(x[p, c] op v[img, c]) (ChannelBroadcast, Nhwc.Det.cs:317-351).
@@ -181,7 +231,7 @@ __device__ __forceinline__ void chan_body(const sox_chan_args& p) {
     if (idx >= p.rows * cvn) return;
     const long row = idx / cvn;
     const int c0 = (int)(idx % cvn) * CV;
-    const long img = row / p.hw;
+    const long img = (p.flags & 2) ? 0 : row / p.hw;
     typedef typename VecT<T, CV>::Vec Vec;
     Vec xv = *(const Vec*)((const T*)p.x + row * p.c + c0);
     Vec vv = *(const Vec*)((const T*)p.v + img * p.c + c0);
@@ -347,20 +397,6 @@ extern "C" __global__ void __launch_bounds__(256) sox_f16_to_f32(sox_cvt_args p)
     }
 }
 
-// ------------------------------------------------------------------------------------------
-// Wave reductions (wave64).
-// ------------------------------------------------------------------------------------------
-SOX_DEV float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-
-SOX_DEV float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
 
 // ------------------------------------------------------------------------------------------
 // LayerNorm (Kernels/Ops.cs:544-574, Avx2Kernels.cs:562-600): one wave per row; single pass
@@ -506,3 +542,169 @@ __device__ __forceinline__ void pool_body(const sox_pool_args& p) {
 
 extern "C" __global__ void __launch_bounds__(256) sox_pool_f16(sox_pool_args p) { pool_body<half_t>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_pool_f32(sox_pool_args p) { pool_body<float>(p); }
+
+// ------------------------------------------------------------------------------------------
+// Attention on matrix cores (attn.comp's SDPA, D = 32 or 64, S <= 128), fp16 storage.
+// One wave per (batch, head, 16 queries). S^T = K Q^T is built with v_mfma_f32_16x16x32_f16
+// straight from global memory (lane l: K row s = 16j + l%16, Q row t = l%16, 8 consecutive d),
+// so lane l ends up holding the scores of query t = l%16 for keys s = 16j + 4(l/16) + i. The
+// softmax over s is an in-register max/sum plus two cross-lane steps (lanes l, l^16, l^32, l^48).
+// O = P V reuses that register layout directly as the MFMA A operand: within each 32-key step the
+// lane's 8 keys are {32c + 4g + i, 32c + 16 + 4g + i} (g = l/16), and the B operand (V) is read at
+// the same key permutation, which leaves the sum over keys unchanged.
+// ------------------------------------------------------------------------------------------
+template <int NJ, int KD>
+__device__ __forceinline__ void attn_mfma_body(const sox_attn_args& p) {
+    const int lane = threadIdx.x & 63;
+    const int l16 = lane & 15, g = lane >> 4;
+    const int bh = blockIdx.x, tb = blockIdx.y;
+    const int b = bh / p.heads, h = bh - b * p.heads;
+    const half_t* __restrict__ q = (const half_t*)p.q + b * p.q_sb + h * p.q_sh;
+    const half_t* __restrict__ k = (const half_t*)p.k + b * p.k_sb + h * p.k_sh;
+    const half_t* __restrict__ v = (const half_t*)p.v + b * p.v_sb + h * p.v_sh;
+    const int t = tb * 16 + l16;
+    half8 qf[KD];
+#pragma unroll
+    for (int kd = 0; kd < KD; kd++)
+        qf[kd] = t < p.t ? *(const half8*)(q + (long)t * p.q_st + 32 * kd + 8 * g) : (half8)(half_t)0;
+    float4v sc[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int s = 16 * j + l16;
+        float4v acc = (float4v)0.0f;
+#pragma unroll
+        for (int kd = 0; kd < KD; kd++) {
+            half8 kf = s < p.s ? *(const half8*)(k + (long)s * p.k_st + 32 * kd + 8 * g) : (half8)(half_t)0;
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[kd], acc, 0, 0, 0);
+        }
+        sc[j] = acc;
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NJ; j++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int s = 16 * j + 4 * g + i;
+            float x = s < p.s ? sc[j][i] * p.scale : -INFINITY;
+            sc[j][i] = x;
+            m = fmaxf(m, x);
+        }
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; j++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int s = 16 * j + 4 * g + i;
+            float e = s < p.s ? sox_exp(sc[j][i] - m) : 0.0f;
+            sc[j][i] = e;
+            sum += e;
+        }
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    constexpr int NC = (NJ + 1) / 2, JD = 2 * KD;
+    float4v o[JD];
+#pragma unroll
+    for (int jd = 0; jd < JD; jd++) o[jd] = (float4v)0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        half8 pa;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            pa[i] = (half_t)sc[2 * c][i];
+            pa[4 + i] = 2 * c + 1 < NJ ? (half_t)sc[2 * c + 1][i] : (half_t)0;
+        }
+#pragma unroll
+        for (int jd = 0; jd < JD; jd++) {
+            const int d = 16 * jd + l16;
+            half8 vb;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int s = 32 * c + 4 * g + (e < 4 ? e : 12 + e);
+                vb[e] = s < p.s ? v[(long)s * p.v_st + d] : (half_t)0;
+            }
+            o[jd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o[jd], 0, 0, 0);
+        }
+    }
+    half_t* __restrict__ out = (half_t*)p.o + b * p.o_sb + h * p.o_sh;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int tt = tb * 16 + 4 * g + i;
+        const float inv = 1.0f / __shfl(sum, 4 * g + i, 64);
+        if (tt < p.t)
+#pragma unroll
+            for (int jd = 0; jd < JD; jd++) out[(long)tt * p.o_st + 16 * jd + l16] = (half_t)(o[jd][i] * inv);
+    }
+}
+
+#define SOX_ATTN_MFMA(S, D)                                                                                  \
+    extern "C" __global__ void __launch_bounds__(64) sox_attn_f16_mfma_s##S##_d##D(sox_attn_args p) {         \
+        attn_mfma_body<S / 16, D / 32>(p);                                                                   \
+    }
+SOX_ATTN_MFMA(32, 32)
+SOX_ATTN_MFMA(64, 32)
+SOX_ATTN_MFMA(80, 32)
+SOX_ATTN_MFMA(128, 32)
+SOX_ATTN_MFMA(32, 64)
+SOX_ATTN_MFMA(64, 64)
+SOX_ATTN_MFMA(80, 64)
+SOX_ATTN_MFMA(128, 64)
+
+// ------------------------------------------------------------------------------------------
+// Direct conv for few input channels (3-channel stems; convpool.comp / conv_tile.comp's role):
+// one work item = one output pixel x OCV output channels; the packed [oc][kpad] weights are
+// staged once per workgroup in LDS as fp32. acc = bias + sum over taps, channels (FMA), then
+// residual and activation, one 16-byte store.
+// ------------------------------------------------------------------------------------------
+template <typename T, int OCV>
+__device__ __forceinline__ void conv_direct_body(const sox_igemm_args& p) {
+    extern __shared__ float wl[];  // [oc][K]
+    const int K = p.k;
+    for (int i = threadIdx.x; i < p.n * K; i += blockDim.x) {
+        int o = i / K, kk = i - o * K;
+        wl[i] = to_f(((const T*)p.w)[(long)o * p.kpad + kk]);
+    }
+    __syncthreads();
+    const int ocg = p.n / OCV;
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long)p.m * ocg) return;
+    const int og = (int)(idx % ocg);
+    const long m = idx / ocg;
+    const int ohw = p.oh * p.ow;
+    const int b = (int)(m / ohw), r = (int)(m - (long)b * ohw);
+    const int oy = r / p.ow, ox = r - oy * p.ow;
+    const bool reflect = (p.flags & SOX_F_REFLECT) != 0;
+    const T* __restrict__ x = (const T*)p.x + (long)b * p.ih * p.iw * p.ic;
+    float acc[OCV];
+#pragma unroll
+    for (int e = 0; e < OCV; e++) acc[e] = (p.flags & SOX_F_BIAS) ? p.bias[og * OCV + e] : 0.0f;
+    const float* w0 = wl + (long)og * OCV * K;
+    for (int ky = 0; ky < p.kh; ky++) {
+        int iy = sox_src_index(oy * p.sh + ky - p.pt, p.ih, reflect);
+        for (int kx = 0; kx < p.kw; kx++) {
+            int ix = sox_src_index(ox * p.sw + kx - p.pl, p.iw, reflect);
+            const int k0 = (ky * p.kw + kx) * p.ic;
+            for (int c = 0; c < p.ic; c++) {
+                float xv = iy < 0 || ix < 0 ? p.pad_value : to_f(x[((long)iy * p.iw + ix) * p.ic + c]);
+#pragma unroll
+                for (int e = 0; e < OCV; e++) acc[e] = __builtin_fmaf(xv, w0[e * K + k0 + c], acc[e]);
+            }
+        }
+    }
+    const int act = (p.flags & SOX_F_ACT_MASK) >> SOX_F_ACT_SHIFT;
+    typedef typename VecT<T, OCV>::Vec Vec;
+    const long o = m * p.ldy + og * OCV;
+    if (p.flags & SOX_F_RESIDUAL) {
+        Vec av = *(const Vec*)((const T*)p.add + o);
+#pragma unroll
+        for (int e = 0; e < OCV; e++) acc[e] = acc[e] + to_f(av[e]);
+    }
+    Vec out;
+#pragma unroll
+    for (int e = 0; e < OCV; e++) out[e] = (T)sox_act(acc[e], act);
+    *(Vec*)((T*)p.y + o) = out;
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_f16(sox_igemm_args p) { conv_direct_body<half_t, 8>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_f32(sox_igemm_args p) { conv_direct_body<float, 4>(p); }

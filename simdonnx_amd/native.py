@@ -26,7 +26,7 @@ OP = dict(Conv=0, MaxPool=1, Elementwise=2, Relu=3, Sigmoid=4, Erf=5, Gelu=6, La
           HardSwish=24, Swish=25, Ext=26, ChannelGate=27, Attention=28, LeakyRelu=29, Tanh=30, Clip=31,
           DepthToSpace=32, SpaceToDepth=33)
 ACT = dict(none=0, relu=1, sigmoid=2, gelu=3, hardswish=4, swish=5)
-CK = dict(raw=0, f32=1, convwt=2, gemmnk=3, dww=4, convtw=5)
+CK = dict(raw=0, f32=1, convwt=2, gemmnk=3, dww=4, convtw=5, f32t=7)
 SLOT_ARENA, SLOT_CONSTS, SLOT_DUMMY = 0, 1, 2
 RUN_STAGING, RUN_DISPATCHES = 1, 2
 

@@ -197,3 +197,27 @@ def test_replay_matches_direct(hip):
         for _ in range(3):
             s.set_input(x)
             assert np.array_equal(s.run(), direct)
+
+
+@pytest.mark.parametrize("kernel", ["sox_gemm_f16_256x128_s2", "sox_gemm_f16_256x128_s3", "sox_gemm_f16_128x128_s2",
+                                    "sox_gemm_f16_128x128_s3", "sox_gemm_f16_128x256_s2", "sox_gemm_f16_128x64_s3",
+                                    "sox_gemm_f16_64x64_s3"])
+@pytest.mark.parametrize("act", ["gelu", "relu", "none"])
+def test_pipelined_gemm_variants(hip, kernel, act, monkeypatch):
+    """Every LDS-DMA Gemm tiling against the oracle, with M and N tails (M=300, N=264) and K=192."""
+    monkeypatch.setenv("SIMDONNX_HIP_GEMM", kernel)
+    m, k, n = 300, 192, 264
+    a = f16(synth.uniform(21, 1, (m, k), -1, 1))
+    w = f16(synth.normal(21, 2, (k, n), 0.1))
+    b = synth.uniform(21, 3, (n,), -0.1, 0.1)
+    pb = PlanBuilder()
+    av = pb.input((m, k), None, "a")
+    y = pb.gemm(av, w, b, act=act, name="gemm")
+    plan = pb.build(y)
+    g = hip.graph(plan, True)
+    assert g.dispatches[0][0] == "gemm"
+    with HipInferenceSession(g) as s:
+        s.set_input(a)
+        got = s.run().copy()
+    want = O.gemm(a, w, b, act=act)
+    assert max_rel(got, want) < TOL[True]

@@ -38,3 +38,58 @@ def test_matmul_bias_gelu_fp32(hip):
     got = run_gpu(hip, plan, ins, False)
     want = run_plan(plan, ins)
     assert max_rel(got, want) <= 1e-4
+
+
+@pytest.mark.parametrize("half", [True, False], ids=["f16", "f32"])
+def test_mobilenetv3_small(hip, half):
+    plan, ins = graphs.mobilenetv3_small()
+    got = run_gpu(hip, plan, ins, half)
+    want = run_plan(plan, ins)
+    assert max_rel(got, want) <= (2e-2 if half else 1e-4)
+
+
+def test_dbnet_detector_fp32(hip):
+    plan, ins = graphs.dbnet()
+    got = run_gpu(hip, plan, ins, False)
+    want = run_plan(plan, ins)
+    assert got.shape == (1, 960, 960, 1)
+    assert max_rel(got, want) <= 1e-4
+
+
+def test_dbnet_detector_fp16(hip):
+    """fp16 storage on this synthetic He-normal detector cannot reach 2e-2 against the fp32 CPU
+    reference: the same rounding applied on the CPU (oracle with f16_storage) already deviates
+    ~5e-2 (logits up to |72|, 39% of pixels on the sigmoid's steep part). The GPU must stay within
+    the reference's fp16 debug threshold (6e-2, VkDebugTests.cs) and within 1.25x of that inherent
+    contract error; the mean error must stay at fp16 level."""
+    plan, ins = graphs.dbnet()
+    got = run_gpu(hip, plan, ins, True)
+    want = run_plan(plan, ins)
+    emu = run_plan(plan, ins, f16_storage=True)
+    inherent = max_rel(emu, want)
+    err = max_rel(got, want)
+    print(f"[gpu] detector fp16 max-rel {err:.4f}, CPU fp16-contract emulation {inherent:.4f}", flush=True)
+    assert err <= 6e-2 and err <= max(2e-2, 1.25 * inherent)
+    assert float(np.abs(got - want).mean()) <= 2e-3
+
+
+def test_svtr_recognizer_fp16(hip):
+    plan, ins = graphs.svtr()
+    got = run_gpu(hip, plan, ins, True)
+    want = run_plan(plan, ins)
+    assert got.shape == (32, 80, 6625)
+    assert max_rel(got, want) <= 2e-2
+    # each row is a distribution (size-independent property of the softmax head)
+    np.testing.assert_allclose(got.sum(-1), 1.0, atol=5e-3)
+
+
+def test_detector_replay_is_bitwise_stable(hip):
+    """HIP-graph replay of the whole detector matches the direct launches bit for bit, on every replay."""
+    plan, ins = graphs.dbnet(size=320)
+    with HipInferenceSession(hip.graph(plan, True)) as s:
+        s.set_input(ins[0])
+        direct = s.run().copy()
+        s.set_replay(True)
+        for _ in range(3):
+            s.set_input(ins[0])
+            assert np.array_equal(s.run(), direct)
