@@ -102,9 +102,10 @@ NETWORKS = {
 }
 
 
-def bench_network(key: str, steps: int):
-    """ms per image of a whole network plan, HIP-graph replay, inputs resident (and with staging),
-    plus the per-kernel-class roofline from a per-dispatch event profile."""
+def bench_network(key: str, steps: int, replay: bool = True):
+    """ms per image of a whole network plan, HIP-graph replay (or node-by-node launches with
+    replay=False), inputs resident (and with staging), plus the per-kernel-class roofline from a
+    per-dispatch event profile."""
     from simdonnx_amd import graphs
     from simdonnx_amd.backend import HipBackend, HipInferenceSession
     fn, desc, images = NETWORKS[key]
@@ -113,7 +114,7 @@ def bench_network(key: str, steps: int):
     g = hip.graph(plan, True)
     with HipInferenceSession(g) as s:
         s.set_input(ins[0])
-        s.set_replay(True)
+        s.set_replay(replay)
         s.run()
         s.time(5)
         ms = s.time(steps) / steps
@@ -218,6 +219,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-replay", action="store_true",
+                    help="launch network dispatches one by one instead of replaying a HIP graph (profiler runs)")
     ap.add_argument("--only", choices=["gemm", "conv", "detector", "recognizer", "mobilenetv3", "copy"],
                     help="run one workload only (profiling runs); prints its own JSON line")
     args = ap.parse_args()
@@ -227,7 +230,7 @@ def main():
         sys.exit(2)
     if args.only:
         fn = {"gemm": lambda: bench_gemm(args.steps, args.warmup), "conv": lambda: bench_conv(args.steps),
-              "copy": lambda: bench_copy(args.steps)}.get(args.only) or (lambda: bench_network(args.only, args.steps))
+              "copy": lambda: bench_copy(args.steps)}.get(args.only) or (lambda: bench_network(args.only, args.steps, not args.no_replay))
         r = fn()
         print(json.dumps({"only": args.only, **{k: v for k, v in r.items() if k != "kernel_ms"}}), flush=True)
         return
@@ -256,7 +259,7 @@ def main():
     }
     for key in ("detector", "recognizer", "mobilenetv3"):
         try:
-            out[key] = bench_network(key, 50)
+            out[key] = bench_network(key, 50, not args.no_replay)
             log(f"{key}: {out[key]['ms_per_image']} ms/image")
         except Exception as e:  # reported, never hidden
             out[key] = {"error": repr(e)}

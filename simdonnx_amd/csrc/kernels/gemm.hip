@@ -3,21 +3,29 @@
 //   Y[M,N] = act(A[M,K] . W[N,K]^T + bias[N]),  A dense rows (lda), W packed [N][kpad] k-fastest,
 //   fp16 storage, fp32 accumulation, fp16 output.
 //
-// Structure (256 threads = 4 waves, BM x BN tile, BK-deep K slices):
-//  * K slices move global -> LDS with global_load_lds_dwordx4 (no register staging), STAGES deep:
-//    slice k+STAGES-1 is in flight while slice k is multiplied. Completion is tracked with an
-//    explicit s_waitcnt vmcnt + s_barrier per slice.
-//  * LDS rows are BK fp16 (128 B for BK = 64) of 16-byte chunks stored XOR-swizzled
-//    (slot = chunk ^ f(row), f(r) = (r & 7) ^ ((r >> 3) & 1)), so the 16 lanes of an MFMA
-//    fragment read (16 rows, same chunk) hit 16 distinct 16-byte bank groups. The swizzle is applied
-//    on the load side: each lane of a DMA instruction fetches the chunk that belongs at its slot.
-//  * v_mfma_f32_16x16x32_f16 with W as the row operand and A as the column operand: lane l then
-//    holds Y^T[n = 4(l/16) + q][m = l%16], i.e. 4 consecutive output channels of one row, so the
-//    epilogue applies bias / activation on float4s and writes 8-byte packets to an LDS staging tile,
-//    from which the workgroup stores full 16-byte row segments (coalesced, no partial lines).
-//  * Tile order is XCD-aware: the hardware deals workgroups round-robin to the 8 XCDs, so block b
-//    is remapped to tile (b % 8) * (tiles / 8) + b / 8, and tiles are walked in groups of GM
-//    M-tiles, so the workgroups resident on one XCD share A rows and W columns in its L2.
+// Structure (NW waves, BM x BN output tile, BK-deep K slices):
+//  * v_mfma_f32_32x32x16_f16 (the gfx950 instruction that sustains the dense fp16 rate with one wave
+//    per SIMD; the 16x16x32 form needs two waves per SIMD and still tops out lower). W is the row
+//    operand and A the column operand, so lane l holds Y^T[n = 8(q/4) + 4(l/32) + q%4][m = l%32]:
+//    4 runs of 4 consecutive output channels of one row, i.e. float4 bias/activation and 8-byte stores
+//    straight from the accumulators.
+//  * K slices move global -> LDS with global_load_lds_dwordx4 (no register staging), STAGES deep.
+//    LDS rows are BK fp16 (CPR 16-byte chunks) stored XOR-swizzled (slot = chunk ^ f(row),
+//    f(r) = (r / (16 / CPR)) % CPR), so the 16 lanes that one ds_read_b128 cycle serves (16 consecutive
+//    rows, same chunk) hit 16 distinct 16-byte bank groups. The swizzle is applied on the load side.
+//  * Register pipeline: k-step s+1's fragments are read while k-step s multiplies; the last k-step of
+//    a slice reads the NEXT slice's first step. One s_barrier per slice, placed there: it publishes
+//    slice g+1 (explicit vmcnt, loads complete in order) and retires slice g's stage, which is
+//    refilled at once with slice g+STAGES.
+//  * The bias never passes through vector registers on its own: each stage carries the tile's BN bias
+//    floats (loaded by the same DMA), and a tile's accumulators start from them, so the epilogue is
+//    activation + store only and no global load result is waited on outside the slice protocol.
+//  * Persistent: each workgroup walks its tiles as ONE ring of K-slices, so the next tile's slices load
+//    while the current tile's epilogue runs. Workgroups are numbered XCD-major (consecutive dispatch
+//    ids land on different XCDs), so the tiles in flight on one XCD are a compact group of GM M-tiles
+//    x some N-tiles and share A rows and W columns in that XCD's L2.
+#include <type_traits>
+
 #include "sox_device.h"
 
 #define LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
@@ -27,179 +35,275 @@ template <int N> SOX_DEV void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
+SOX_DEV void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
 
-SOX_DEV int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+template <int I, int N, class F> SOX_DEV void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
 
-// erf-GELU with the A&S 7.1.26 polynomial evaluated with the hardware reciprocal and exp2 (fp16
-// outputs: the approximations' ~1e-7 relative error is far below the fp16 output rounding).
+// LDS chunk swizzle for rows of CPR 16-byte chunks: rows sharing a 256-byte bank window get distinct
+// slots, so 16 consecutive rows read at one chunk hit 16 distinct 16-byte bank groups.
+template <int CPR> SOX_DEV int swz(int r) { return (r / (16 / CPR)) % CPR; }
+
+// erf-GELU with the A&S 7.1.26 erf, rearranged for few instructions:
+//   gelu(x) = x Phi(x) = max(x, 0) - 0.5 |x| (1 - erf(|x| / sqrt2)),
+//   1 - erf(z) = t P(t) exp(-z^2),  t = 1 / (1 + 0.3275911 z)   (z >= 0),
+// with the 0.5 folded into P's coefficients, the hardware reciprocal and exp2 (fp16 outputs: their
+// ~1e-7 relative error is far below the output rounding). |x| is capped at 16 inside the erf term
+// (where that term is < 1e-50) so x = +-inf gives +inf / 0.
 SOX_DEV float gelu_fast(float x) {
-    float z = x * 0.70710678118654752f;
-    float az = fabsf(z);
-    float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f, az, 1.0f));
-    float p = 1.061405429f;
-    p = __builtin_fmaf(p, t, -1.453152027f);
-    p = __builtin_fmaf(p, t, 1.421413741f);
-    p = __builtin_fmaf(p, t, -0.284496736f);
-    p = __builtin_fmaf(p, t, 0.254829592f);
-    float e = __builtin_amdgcn_exp2f(-(az * az) * 1.4426950408889634f);
-    float erf = copysignf(1.0f - (p * t) * e, z);
-    return (0.5f * x) * (1.0f + erf);
+    const float ax = fminf(fabsf(x), 16.0f);
+    const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f * 0.70710678118654752f, ax, 1.0f));
+    float p = 0.5f * 1.061405429f;
+    p = __builtin_fmaf(p, t, 0.5f * -1.453152027f);
+    p = __builtin_fmaf(p, t, 0.5f * 1.421413741f);
+    p = __builtin_fmaf(p, t, 0.5f * -0.284496736f);
+    p = __builtin_fmaf(p, t, 0.5f * 0.254829592f);
+    const float e = __builtin_amdgcn_exp2f((ax * -0.72134752044448170f) * ax);  // exp(-x^2 / 2)
+    return __builtin_fmaf(-(ax * (p * t)), e, fmaxf(x, 0.0f));
 }
 
 SOX_DEV float act_fast(float v, int act) { return act == SOX_ACT_GELU ? gelu_fast(v) : sox_act(v, act); }
 
-template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GM>
+// Epilogue of one wave's WM x WN block: lane l (l32 = l % 32, hl = l / 32) of 32x32 block (j, i) holds
+// output row m0 + 32 i + l32 and, for q = 0..3, channels n0 + 32 j + 8 q + 4 hl .. +3 in accumulator
+// elements 4q .. 4q+3 (the bias is already in the accumulators): activation on a float4, one 8-byte
+// store each.
+template <int ACT, int TJ, int TI>
+SOX_DEV void store_tile(half_t* __restrict__ Y, int ldy, int M, int N, int m0, int n0, const float16v (&acc)[TJ][TI],
+                        int act = 0) {
+    const int lane = threadIdx.x & 63, l32 = lane & 31, hl = lane >> 5;
+    // static_for, not #pragma unroll: the accumulators must only ever be indexed by constants, or they
+    // leave registers
+    static_for<0, TJ * TI>([&](auto ji) {
+        constexpr int j = decltype(ji)::value / TI, i = decltype(ji)::value % TI;
+        const int m = m0 + i * 32 + l32;
+        static_for<0, 4>([&](auto qq) {
+            constexpr int q = decltype(qq)::value;
+            const int n = n0 + j * 32 + 8 * q + 4 * hl;
+            half4 h;
+            static_for<0, 4>([&](auto ee) {
+                constexpr int e = decltype(ee)::value;
+                const float v = acc[j][i][4 * q + e];
+                h[e] = (half_t)(ACT == SOX_ACT_GELU ? gelu_fast(v) : ACT >= 0 ? sox_act(v, ACT) : act_fast(v, act));
+            });
+            if (m < M && n < N) *(half4*)(Y + (long)m * ldy + n) = h;
+        });
+        __builtin_amdgcn_sched_barrier(0);  // one block at a time: bounded register pressure
+    });
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int NW, int GM>
 __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
     constexpr int CPR = BK / 8;                 // 16-byte chunks per LDS row
     constexpr int ROWB = BK * 2;                // LDS row bytes
-    constexpr int A_BYTES = BM * ROWB, B_BYTES = BN * ROWB;
-    constexpr int A_IT = A_BYTES / 1024 / 4;    // DMA instructions per wave per slice (1 KiB each)
-    constexpr int B_IT = B_BYTES / 1024 / 4;
-    constexpr int LOADS = A_IT + B_IT;
-    constexpr int TJ = WN / 16, TI = WM / 16;   // MFMA blocks: n (rows) x m (cols)
+    constexpr int KS = BK / 16;                 // MFMA k-steps per slice
+    constexpr int A_BYTES = BM * ROWB, B_BYTES = BN * ROWB, BIAS_BYTES = BN * 4;
+    constexpr int STAGE_BYTES = A_BYTES + B_BYTES + BIAS_BYTES;
+    constexpr int BIAS_LANES = BIAS_BYTES / 16 / NW;  // lanes of each wave's bias DMA (16 B each)
+    constexpr int A_IT = A_BYTES / 1024 / NW;   // DMA instructions per wave per slice (1 KiB each)
+    constexpr int B_IT = B_BYTES / 1024 / NW;
+    constexpr int LOADS = A_IT + B_IT + 1;      // + the bias DMA
+    constexpr int TI = WM / 32, TJ = WN / 32;   // 32x32 MFMA blocks: m (columns) x n (rows)
     constexpr int WAVES_N = BN / WN;
-    constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
-    constexpr int EPI_ROW = BN + 8;             // epilogue staging row (fp16), 16 B pad
-    constexpr int LDS_BYTES = STAGE_BYTES * STAGES > BM * EPI_ROW * 2 ? STAGE_BYTES * STAGES : BM * EPI_ROW * 2;
-    static_assert(CPR == 8, "the swizzle assumes 8 chunks per row (BK = 64)");
-    static_assert((BM / WM) * (BN / WN) == 4 && A_IT >= 1 && B_IT >= 1, "tiling");
-    static_assert((STAGES - 2) * LOADS < 64, "vmcnt range");
+    constexpr int RPI = 1024 / ROWB;            // rows per 1 KiB DMA instruction
+    static_assert(CPR == 4 || CPR == 8, "BK = 32 or 64");
+    static_assert(KS % 2 == 0, "fragment sets alternate per k-step and must realign per slice");
+    static_assert((BM / WM) * (BN / WN) == NW && WM % 32 == 0 && WN % 32 == 0, "tiling");
+    static_assert(A_IT * 1024 * NW == A_BYTES && B_IT * 1024 * NW == B_BYTES, "DMA split");
+    static_assert(BIAS_LANES * 16 * NW == BIAS_BYTES && BIAS_LANES <= 64 && STAGE_BYTES % 16 == 0, "bias DMA split");
+    static_assert(STAGES >= 2 && (STAGES - 1) * LOADS < 64, "vmcnt range");
 
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[LDS_BYTES];
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[STAGE_BYTES * STAGES];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int l16 = lane & 15, g = lane >> 4;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int l32 = lane & 31, hl = lane >> 5;
     const int M = p.m, N = p.n, K = p.k;
     const int tiles_n = p.tiles_n, tiles_m = (M + BM - 1) / BM, ntiles = tiles_m * tiles_n;
-
-    // ---- XCD-aware, grouped tile order ----
-    int bid = blockIdx.x;
-    if (ntiles % 8 == 0) bid = (bid % 8) * (ntiles / 8) + bid / 8;
-    const int group = bid / (GM * tiles_n), first_m = group * GM;
-    const int gsize = min(tiles_m - first_m, GM);
-    const int in_group = bid - group * GM * tiles_n;
-    const int bm = (first_m + in_group % gsize) * BM;
-    const int bn = (in_group / gsize) * BN;
-
     const int wm0 = (wave / WAVES_N) * WM, wn0 = (wave % WAVES_N) * WN;
     const half_t* __restrict__ A = (const half_t*)p.x;
     const half_t* __restrict__ W = (const half_t*)p.w;
+    half_t* __restrict__ Y = (half_t*)p.y;
+    const int act = (p.flags & SOX_F_ACT_MASK) >> SOX_F_ACT_SHIFT;
+    const bool has_bias = (p.flags & SOX_F_BIAS) != 0;
+    const int nk = K / BK;
 
-    // ---- DMA source addresses: lane l of instruction i of this wave fills LDS slot l of the
-    //      1 KiB block (wave * IT + i); that slot is (row, slot) -> global chunk slot ^ swz(row)
+    // XCD-major workgroup number: dispatch id b runs on XCD b % 8, so XCD x gets the contiguous
+    // numbers [x G/8, (x+1) G/8) and with them consecutive tiles of every round
+    const int G = gridDim.x;
+    const int vid = (G % 8 == 0) ? (blockIdx.x % 8) * (G / 8) + blockIdx.x / 8 : blockIdx.x;
+    const int my_tiles = vid < ntiles ? (ntiles - 1 - vid) / G + 1 : 0;
+    const int total = my_tiles * nk;  // this workgroup's ring of K-slices
+    auto tile_origin = [&](int t, int& bm, int& bn) {  // M-tiles walked in groups of GM
+        const int group = t / (GM * tiles_n), first_m = group * GM;
+        const int gsize = min(tiles_m - first_m, GM);
+        const int in_group = t - group * GM * tiles_n;
+        bm = (first_m + in_group % gsize) * BM;
+        bn = (in_group / gsize) * BN;
+    };
+
+    // DMA sources of the tile being issued: lane l of instruction i of this wave fills LDS slot l of the
+    // 1 KiB block (wave * IT + i), i.e. row (wave * IT + i) * RPI + l / CPR, slot l % CPR, which holds
+    // global chunk slot ^ swz(row). Rows past M / N re-read the last row (never stored).
     const half_t* a_src[A_IT];
     const half_t* b_src[B_IT];
+    const float* c_src;  // this lane's 4 bias floats (a duplicate A chunk when there is no bias)
+    auto set_sources = [&](int t) {
+        int bm, bn;
+        tile_origin(t, bm, bn);
+        c_src = has_bias ? p.bias + min(bn + (wave * BIAS_LANES + lane) * 4, N - 4) : (const float*)A;
 #pragma unroll
-    for (int i = 0; i < A_IT; i++) {
-        int r = (wave * A_IT + i) * 8 + lane / 8;
-        int c = (lane % 8) ^ swz(r);
-        int m = min(bm + r, M - 1);
-        a_src[i] = A + (long)m * p.lda + c * 8;
-    }
+        for (int i = 0; i < A_IT; i++) {
+            const int r = (wave * A_IT + i) * RPI + lane / CPR;
+            const int c = (lane % CPR) ^ swz<CPR>(r);
+            a_src[i] = A + (long)min(bm + r, M - 1) * p.lda + c * 8;
+        }
 #pragma unroll
-    for (int i = 0; i < B_IT; i++) {
-        int r = (wave * B_IT + i) * 8 + lane / 8;
-        int c = (lane % 8) ^ swz(r);
-        int n = min(bn + r, N - 1);
-        b_src[i] = W + (long)n * p.kpad + c * 8;
-    }
-
-    auto issue = [&](int slice) {
-        unsigned char* st = smem + (slice % STAGES) * STAGE_BYTES;
-        const int k0 = slice * BK;
+        for (int i = 0; i < B_IT; i++) {
+            const int r = (wave * B_IT + i) * RPI + lane / CPR;
+            const int c = (lane % CPR) ^ swz<CPR>(r);
+            b_src[i] = W + (long)min(bn + r, N - 1) * p.kpad + c * 8;
+        }
+    };
+    // ring slice gs = (index in this workgroup's tile list) * nk + k-slice. Slices past the end are
+    // still issued (re-reading the last tile's rows into a stage nobody reads again), so every slice
+    // has the same number of loads in flight and one static vmcnt covers them all.
+    auto issue = [&](int gs) {
+        const int kt = gs % nk;
+        if (kt == 0 && gs < total) set_sources(vid + (gs / nk) * G);
+        unsigned char* st = smem + (gs % STAGES) * STAGE_BYTES;
+        const int k0 = kt * BK;
 #pragma unroll
         for (int i = 0; i < A_IT; i++)
             __builtin_amdgcn_global_load_lds(a_src[i] + k0, LDS_PTR(st + (wave * A_IT + i) * 1024), 16, 0, 0);
 #pragma unroll
         for (int i = 0; i < B_IT; i++)
             __builtin_amdgcn_global_load_lds(b_src[i] + k0, LDS_PTR(st + A_BYTES + (wave * B_IT + i) * 1024), 16, 0, 0);
+        // the tile's bias rides along with every slice (same bytes each time) so every slice has the
+        // same load count; the accumulators of a new tile start from it
+        if (lane < BIAS_LANES)
+            __builtin_amdgcn_global_load_lds(c_src, LDS_PTR(st + A_BYTES + B_BYTES + wave * BIAS_LANES * 16), 16, 0, 0);
     };
 
-    float4v acc[TJ][TI];
+    // fragment offsets: k-step s of a lane covers chunk 2s + l/32 of rows (row0 + l%32)
+    int a_off[KS][TI], b_off[KS][TJ];
 #pragma unroll
-    for (int j = 0; j < TJ; j++)
-#pragma unroll
-        for (int i = 0; i < TI; i++) acc[j][i] = (float4v)0.0f;
-
-    const int nk = K / BK;
-#pragma unroll
-    for (int s = 0; s < STAGES - 1; s++)
-        if (s < nk) issue(s);
-
-    // fragment read offsets (bytes within a stage): row * ROWB + ((chunk ^ swz(row)) * 16)
-    int a_row[TI], b_row[TJ];
-#pragma unroll
-    for (int i = 0; i < TI; i++) a_row[i] = wm0 + i * 16 + l16;
-#pragma unroll
-    for (int j = 0; j < TJ; j++) b_row[j] = wn0 + j * 16 + l16;
-
-    for (int kt = 0; kt < nk; kt++) {
-        // slice kt complete for this wave (later slices may stay in flight), then for all waves
-        if (kt + STAGES - 2 < nk) wait_vmcnt<(STAGES - 2) * LOADS>();
-        else wait_vmcnt<0>();
-        __builtin_amdgcn_s_barrier();
-        if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1);
-        const unsigned char* st = smem + (kt % STAGES) * STAGE_BYTES;
-#pragma unroll
-        for (int s = 0; s < BK / 32; s++) {
-            const int chunk = s * 4 + g;
-            half8 af[TI], bf[TJ];
-#pragma unroll
-            for (int j = 0; j < TJ; j++)
-                bf[j] = *(const half8*)(st + A_BYTES + b_row[j] * ROWB + ((chunk ^ swz(b_row[j])) << 4));
-#pragma unroll
-            for (int i = 0; i < TI; i++)
-                af[i] = *(const half8*)(st + a_row[i] * ROWB + ((chunk ^ swz(a_row[i])) << 4));
-#pragma unroll
-            for (int j = 0; j < TJ; j++)
-#pragma unroll
-                for (int i = 0; i < TI; i++)
-                    acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[j], af[i], acc[j][i], 0, 0, 0);
-        }
-    }
-
-    // ---- epilogue: bias + act on float4s (4 consecutive n), fp16 into the LDS staging tile ----
-    __syncthreads();  // every wave is done with the stage buffers
-    const int act = (p.flags & SOX_F_ACT_MASK) >> SOX_F_ACT_SHIFT;
-    const bool has_bias = (p.flags & SOX_F_BIAS) != 0;
-    half_t* epi = (half_t*)smem;
-#pragma unroll
-    for (int j = 0; j < TJ; j++) {
-        const int nl = wn0 + j * 16 + 4 * g;  // local n of q = 0
-        float4v bias = (float4v)0.0f;
-        if (has_bias && bn + nl + 3 < N) bias = *(const float4v*)(p.bias + bn + nl);
-        else if (has_bias)
-            for (int q = 0; q < 4; q++) bias[q] = bn + nl + q < N ? p.bias[bn + nl + q] : 0.0f;
+    for (int s = 0; s < KS; s++) {
 #pragma unroll
         for (int i = 0; i < TI; i++) {
-            const int ml = wm0 + i * 16 + l16;
-            half4 h;
+            const int r = wm0 + i * 32 + l32;
+            a_off[s][i] = r * ROWB + (((2 * s + hl) ^ swz<CPR>(r)) << 4);
+        }
 #pragma unroll
-            for (int q = 0; q < 4; q++) h[q] = (half_t)act_fast(acc[j][i][q] + bias[q], act);
-            *(half4*)(epi + ml * EPI_ROW + nl) = h;
+        for (int j = 0; j < TJ; j++) {
+            const int r = wn0 + j * 32 + l32;
+            b_off[s][j] = A_BYTES + r * ROWB + (((2 * s + hl) ^ swz<CPR>(r)) << 4);
         }
     }
-    __syncthreads();
-    // ---- coalesced stores: 16 B per thread, consecutive threads along a row ----
-    constexpr int CH = BN / 8;  // 16-byte chunks per output row
-    half_t* __restrict__ Y = (half_t*)p.y;
-#pragma unroll 4
-    for (int idx = tid; idx < BM * CH; idx += 256) {
-        const int r = idx / CH, c = idx - r * CH;
-        const int m = bm + r, n = bn + c * 8;
-        if (m < M && n < N) *(half8*)(Y + (long)m * p.ldy + n) = *(const half8*)(epi + r * EPI_ROW + c * 8);
+
+    if (total == 0) return;
+    int bm_cur, bn_cur;  // origin of the tile being multiplied
+    tile_origin(vid, bm_cur, bn_cur);
+
+    float16v acc[TJ][TI];
+    half8 fa0[TI], fb0[TJ], fa1[TI], fb1[TJ];
+    auto read_step = [&](int gs, int s, half8 (&fa)[TI], half8 (&fb)[TJ]) {
+        const unsigned char* st = smem + (gs % STAGES) * STAGE_BYTES;
+#pragma unroll
+        for (int j = 0; j < TJ; j++) fb[j] = *(const half8*)(st + b_off[s][j]);
+#pragma unroll
+        for (int i = 0; i < TI; i++) fa[i] = *(const half8*)(st + a_off[s][i]);
+    };
+    // accumulators of a new tile = its bias (from the LDS stage of the tile's first slice)
+    auto init_acc = [&](int gs) {
+        const float* bl = (const float*)(smem + (gs % STAGES) * STAGE_BYTES + A_BYTES + B_BYTES);
+        static_for<0, TJ>([&](auto jj) {
+            constexpr int j = decltype(jj)::value;
+            float4v b4[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                b4[q] = has_bias ? *(const float4v*)(bl + wn0 + j * 32 + 8 * q + 4 * hl) : (float4v)0.0f;
+            float16v v;
+            static_for<0, 16>([&](auto qe) { v[decltype(qe)::value] = b4[decltype(qe)::value / 4][decltype(qe)::value % 4]; });
+            static_for<0, TI>([&](auto ii) { acc[j][decltype(ii)::value] = v; });
+        });
+    };
+
+#pragma unroll
+    for (int s = 0; s < STAGES; s++) issue(s);
+    wait_vmcnt<(STAGES - 1) * LOADS>();  // slice 0
+    __builtin_amdgcn_s_barrier();
+    init_acc(0);
+    read_step(0, 0, fa0, fb0);
+    for (int gs = 0; gs < total; gs++) {
+        static_for<0, KS>([&](auto step) {
+            constexpr int s = decltype(step)::value;
+            half8(&ca)[TI] = (s & 1) ? fa1 : fa0;
+            half8(&cb)[TJ] = (s & 1) ? fb1 : fb0;
+            half8(&na)[TI] = (s & 1) ? fa0 : fa1;
+            half8(&nb)[TJ] = (s & 1) ? fb0 : fb1;
+            if constexpr (s == KS - 1) {
+                // slice gs+1 landed (this wave's loads; later slices may stay in flight) and every read
+                // of slice gs done; after the barrier both hold for all waves
+                wait_vmcnt<(STAGES - 2) * LOADS>();
+                wait_lgkmcnt0();
+                __builtin_amdgcn_s_barrier();
+                issue(gs + STAGES);  // into stage gs % STAGES; may already be a later tile's slice
+                read_step(gs + 1, 0, na, nb);
+            } else {
+                read_step(gs, s + 1, na, nb);
+            }
+            static_for<0, TJ * TI>([&](auto ji) {
+                constexpr int j = decltype(ji)::value / TI, i = decltype(ji)::value % TI;
+                acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cb[j], ca[i], acc[j][i], 0, 0, 0);
+            });
+            // MFMA, read, MFMA, read, ...: this step's operands were read one step earlier, and the
+            // next step's reads issue while the matrix pipe works through this step
+            constexpr int RD = TI + TJ, MF = TI * TJ;
+            static_for<0, (RD < MF ? RD : MF)>([&](auto) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            });
+            if constexpr (MF > RD) __builtin_amdgcn_sched_group_barrier(0x008, MF - RD, 0);
+            if constexpr (RD > MF) __builtin_amdgcn_sched_group_barrier(0x100, RD - MF, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        wait_lgkmcnt0();  // next slice's first fragments (read before this slice's last MFMAs)
+        if (gs % nk == nk - 1) {
+            // ---- epilogue from registers (the next tile's first slices are already loading) ----
+            switch (act) {
+            case SOX_ACT_NONE: store_tile<SOX_ACT_NONE>(Y, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc); break;
+            case SOX_ACT_RELU: store_tile<SOX_ACT_RELU>(Y, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc); break;
+            case SOX_ACT_GELU: store_tile<SOX_ACT_GELU>(Y, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc); break;
+            default: store_tile<-1>(Y, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, act); break;
+            }
+            if (gs + 1 < total) {
+                tile_origin(vid + (gs + 1) / nk * G, bm_cur, bn_cur);
+                init_acc(gs + 1);  // published by this slice's barrier
+            }
+        }
     }
+    wait_vmcnt<0>();  // the trailing (unused) slices land before the workgroup's LDS is released
 }
 
-#define SOX_GEMM(NAME, BM, BN, BK, WM, WN, ST, GM)                                                  \
-    extern "C" __global__ void __launch_bounds__(256) NAME(sox_igemm_args p) {                    \
-        gemm_body<BM, BN, BK, WM, WN, ST, GM>(p);                                                 \
+#define SOX_GEMM(NAME, BM, BN, BK, WM, WN, ST, NW, OCC, GM)                                         \
+    extern "C" __global__ void __launch_bounds__(64 * NW, OCC) NAME(sox_igemm_args p) {           \
+        gemm_body<BM, BN, BK, WM, WN, ST, NW, GM>(p);                                             \
     }
 
-SOX_GEMM(sox_gemm_f16_256x128_s2, 256, 128, 64, 128, 64, 2, 4)
-SOX_GEMM(sox_gemm_f16_256x128_s3, 256, 128, 64, 128, 64, 3, 4)
-SOX_GEMM(sox_gemm_f16_128x128_s2, 128, 128, 64, 64, 64, 2, 4)
-SOX_GEMM(sox_gemm_f16_128x128_s3, 128, 128, 64, 64, 64, 3, 4)
-SOX_GEMM(sox_gemm_f16_128x256_s2, 128, 256, 64, 64, 128, 2, 4)
-SOX_GEMM(sox_gemm_f16_128x64_s3, 128, 64, 64, 64, 32, 3, 4)
-SOX_GEMM(sox_gemm_f16_64x64_s3, 64, 64, 64, 32, 32, 3, 4)
+// name: BMxBN tile, kBK slice depth, sSTAGES, wNW waves (4 when absent)
+SOX_GEMM(sox_gemm_f16_256x192_k32s5, 256, 192, 32, 128, 96, 5, 4, 1, 4)
+SOX_GEMM(sox_gemm_f16_256x192_k32s4, 256, 192, 32, 128, 96, 4, 4, 1, 4)
+SOX_GEMM(sox_gemm_f16_256x192_w8k64s2, 256, 192, 64, 64, 96, 2, 8, 1, 4)
+SOX_GEMM(sox_gemm_f16_256x256_w8k32s4, 256, 256, 32, 128, 64, 4, 8, 1, 4)
+SOX_GEMM(sox_gemm_f16_256x256_w8k64s2, 256, 256, 64, 128, 64, 2, 8, 1, 4)
+SOX_GEMM(sox_gemm_f16_256x128_k32s3, 256, 128, 32, 128, 64, 3, 4, 2, 4)
+SOX_GEMM(sox_gemm_f16_256x128_k32s5, 256, 128, 32, 128, 64, 5, 4, 1, 4)
+SOX_GEMM(sox_gemm_f16_256x128_w8k64s2, 256, 128, 64, 64, 64, 2, 8, 1, 4)
+SOX_GEMM(sox_gemm_f16_128x128_k64s2, 128, 128, 64, 64, 64, 2, 4, 2, 4)
+SOX_GEMM(sox_gemm_f16_128x128_k32s4, 128, 128, 32, 64, 64, 4, 4, 2, 4)
+SOX_GEMM(sox_gemm_f16_128x64_k64s2, 128, 64, 64, 64, 32, 2, 4, 3, 4)
+SOX_GEMM(sox_gemm_f16_64x64_k64s2, 64, 64, 64, 32, 32, 2, 4, 4, 4)

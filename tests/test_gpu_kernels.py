@@ -199,14 +199,21 @@ def test_replay_matches_direct(hip):
             assert np.array_equal(s.run(), direct)
 
 
-@pytest.mark.parametrize("kernel", ["sox_gemm_f16_256x128_s2", "sox_gemm_f16_256x128_s3", "sox_gemm_f16_128x128_s2",
-                                    "sox_gemm_f16_128x128_s3", "sox_gemm_f16_128x256_s2", "sox_gemm_f16_128x64_s3",
-                                    "sox_gemm_f16_64x64_s3"])
-@pytest.mark.parametrize("act", ["gelu", "relu", "none"])
-def test_pipelined_gemm_variants(hip, kernel, act, monkeypatch):
-    """Every LDS-DMA Gemm tiling against the oracle, with M and N tails (M=300, N=264) and K=192."""
+GEMM_KERNELS = ["sox_gemm_f16_256x192_k32s5", "sox_gemm_f16_256x128_w8k64s2", "sox_gemm_f16_128x128_k64s2",
+                "sox_gemm_f16_128x64_k64s2", "sox_gemm_f16_64x64_k64s2", "sox_gemm_f16_256x192_k32s4",
+                "sox_gemm_f16_256x192_w8k64s2", "sox_gemm_f16_256x256_w8k32s4", "sox_gemm_f16_256x256_w8k64s2",
+                "sox_gemm_f16_256x128_k32s3", "sox_gemm_f16_256x128_k32s5", "sox_gemm_f16_128x128_k32s4"]
+
+
+@pytest.mark.parametrize("kernel", GEMM_KERNELS)
+@pytest.mark.parametrize("act,shape", [("gelu", (4100, 192, 776)), ("relu", (4100, 192, 776)),
+                                       ("none", (16400, 64, 200)), ("hardswish", (16400, 128, 520))])
+def test_pipelined_gemm_variants(hip, kernel, act, shape, monkeypatch):
+    """Every LDS-DMA Gemm tiling against the oracle, with M and N tails. The M=16400 cases give every
+    tiling more tiles than resident workgroups, so one workgroup's K-slice ring crosses tile borders
+    (with K=64 a border every slice); hardswish takes the runtime-activation epilogue."""
     monkeypatch.setenv("SIMDONNX_HIP_GEMM", kernel)
-    m, k, n = 300, 192, 264
+    m, k, n = shape
     a = f16(synth.uniform(21, 1, (m, k), -1, 1))
     w = f16(synth.normal(21, 2, (k, n), 0.1))
     b = synth.uniform(21, 3, (n,), -0.1, 0.1)
