@@ -145,3 +145,34 @@ def test_round_f16_matches_ieee():
     x = np.concatenate([np.linspace(-70000, 70000, 10001), np.linspace(-1e-4, 1e-4, 10001)]).astype(np.float32)
     with np.errstate(over="ignore"):
         assert np.array_equal(O.round_f16(x), x.astype(np.float16).astype(np.float32))
+
+
+def test_elementwise_broadcast_concat_against_numpy():
+    """Elementwise Add/Sub/Mul/Div (+ReLU), per-channel broadcast both operand orders, channel concat and
+    HardSigmoid against numpy's own float32 arithmetic (one rounding per op, so bit-exact)."""
+    rng = np.random.default_rng(7)
+    a = rng.uniform(-2, 2, (3, 5, 7, 12)).astype(np.float32)
+    b = rng.uniform(0.5, 2, (3, 5, 7, 12)).astype(np.float32)
+    ops = [np.add, np.subtract, np.multiply, np.divide]
+    for op, fn in enumerate(ops):
+        assert np.array_equal(O.ew2(a, b, op=op), fn(a, b))
+        assert np.array_equal(O.ew2(a, b, op=op, act=1), np.maximum(fn(a, b), np.float32(0)))
+        v = b[0, 0, 0]
+        assert np.array_equal(O.channel_broadcast(a, v, op=op), fn(a, v))
+        assert np.array_equal(O.channel_broadcast(a, v, op=op, rev=True), fn(v, a))
+    parts = [a[..., :3], b[..., :5], a[..., 5:9]]
+    assert np.array_equal(O.concat_channels(parts), np.concatenate(parts, axis=-1))
+    hs = O.hard_sigmoid(a, 1 / 6, 0.5)
+    assert np.array_equal(hs, np.clip(a * np.float32(1 / 6) + np.float32(0.5), 0, 1))
+
+
+def test_activation_kinds_closed_forms():
+    """ActivationKind epilogues (Kernels/Nhwc.cs:83-99) against their float64 closed forms."""
+    x = np.linspace(-12, 12, 4801).astype(np.float32)
+    x64 = x.astype(np.float64)
+    sig = 1 / (1 + np.exp(-x64))
+    want = {"relu": np.maximum(x64, 0), "sigmoid": sig, "hardswish": x64 * np.clip(x64 / 6 + 0.5, 0, 1),
+            "swish": x64 * sig, "gelu": 0.5 * x64 * (1 + np.vectorize(math.erf)(x64 / math.sqrt(2)))}
+    for act, w in want.items():
+        got = O.activation(x, act).astype(np.float64)
+        assert np.max(np.abs(got - w)) <= 4e-6 * max(1.0, np.max(np.abs(w))), act
