@@ -91,9 +91,11 @@ typedef struct sox_gap_args {
 } sox_gap_args;
 
 /*
- * Squeeze-excitation gate (se_gate.comp; Kernels/Nhwc.Det.cs:287-314), one workgroup per image:
- *   mean = sum(part)/hw; hid = act1(b1 + W1 mean); z = b2 + W2 hid; s = gate(z) + offset  (out [n][c]).
- *   w1 is packed transposed [c][r], w2 transposed [r][c] (coalesced per-output columns).
+ * Squeeze-excitation gate (se_gate.comp; Kernels/Nhwc.Det.cs:287-314) in two passes, each one row
+ * per wave across many workgroups:
+ *   sox_se_fc1: mean = sum(part)/hw; hid = act1(b1 + W1 mean)        grid (ceil(r/4), n), 256 threads
+ *   sox_se_fc2: z = b2 + W2 hid; s = gate(z) + offset  (out [n][c])   grid (ceil(c/4), n), 256 threads
+ *   w1 [r][c] and w2 [c][r] keep their ONNX 1x1-conv layouts (fp32): one contiguous row per output.
  */
 typedef struct sox_se_args {
     const float* part;
@@ -101,7 +103,8 @@ typedef struct sox_se_args {
     const float* b1;
     const float* w2;
     const float* b2;
-    void* s; /* [n][c] in the graph's storage type */
+    void* s;    /* [n][c] in the graph's storage type */
+    float* hid; /* [n][r] fp32 (scratch) */
     int32_t c, r, chunks, hw;
     int32_t flags; /* bit0 b1, bit1 b2, bit2 act1 relu, bit3 hard */
     float alpha, beta, offset;
@@ -181,7 +184,7 @@ typedef struct sox_softmax_args {
     void* y;
     int64_t rows;
     int32_t len;
-    int32_t pad;
+    int32_t staged; /* 1: the row is kept in dynamic LDS (len floats, granted at launch) */
 } sox_softmax_args;
 
 /*

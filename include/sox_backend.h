@@ -105,7 +105,7 @@ typedef struct sox_bind { int32_t slot; int32_t pad_; uint64_t offset, size; } s
 enum { SOX_SLOT_ARENA = 0, SOX_SLOT_CONSTS = 1, SOX_SLOT_DUMMY = 2 };
 /* ConstKind (Engine/Extensions.cs:144-159) as an id. */
 enum { SOX_CK_RAW = 0, SOX_CK_F32 = 1, SOX_CK_CONVWT = 2, SOX_CK_GEMMNK = 3, SOX_CK_DWW = 4, SOX_CK_CONVTW = 5,
-       SOX_CK_F32T = 7 /* fp32, rank-2 view [a][b...] transposed to [b...][a] (SE weights) */ };
+       SOX_CK_F32T = 7 /* fp32, rank-2 view [a][b...] transposed to [b...][a] */ };
 typedef int (*sox_ext_emit_fn)(void* user, sox_graph* graph, int32_t node);
 typedef int (*sox_ext_consts_fn)(void* user, const sox_plan* plan, int32_t node, int32_t* values, int32_t* kinds,
                                  int32_t cap); /* GpuConsts: returns the count written */

@@ -32,6 +32,59 @@ SOX_DEV float wave_max(float v) {
     return v;
 }
 
+// f(i, x[i]) for i = start, start + step, ... < n, with U loads issued before the first is used.
+// A loop with a runtime trip count otherwise waits on every load in turn (one memory round trip per
+// element); here the U element numbers are clamped to the sequence's last element, so the loads
+// carry no branch and stay in bounds, and the surplus results are dropped.
+// The empty volatile asm after the loads keeps the compiler from sinking a load into the guarded
+// use below (where it would be issued and waited on alone).
+template <typename T> SOX_DEV void keep_in_vgprs(T& v) {
+    typedef unsigned u2v __attribute__((ext_vector_type(2)));
+    typedef unsigned u4v __attribute__((ext_vector_type(4)));
+    if constexpr (sizeof(T) == 2) {
+        unsigned u = __builtin_bit_cast(unsigned short, v);
+        asm volatile("" : "+v"(u));
+        v = __builtin_bit_cast(T, (unsigned short)u);
+    } else if constexpr (sizeof(T) == 4) {
+        unsigned u = __builtin_bit_cast(unsigned, v);
+        asm volatile("" : "+v"(u));
+        v = __builtin_bit_cast(T, u);
+    } else if constexpr (sizeof(T) == 8) {
+        u2v u = __builtin_bit_cast(u2v, v);
+        asm volatile("" : "+v"(u));
+        v = __builtin_bit_cast(T, u);
+    } else {
+        static_assert(sizeof(T) == 16, "2, 4, 8 or 16-byte elements");
+        u4v u = __builtin_bit_cast(u4v, v);
+        asm volatile("" : "+v"(u));
+        v = __builtin_bit_cast(T, u);
+    }
+}
+
+template <int U, typename T, typename F>
+SOX_DEV void strided_foreach(const T* __restrict__ x, long start, long n, long step, F&& f) {
+    if (start >= n) return;
+    const long cnt = (n - 1 - start) / step + 1;  // elements start, start + step, ... < n
+    for (long j0 = 0; j0 < cnt; j0 += U) {
+        T v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) v[u] = x[start + (j0 + u < cnt ? j0 + u : cnt - 1) * step];
+#pragma unroll
+        for (int u = 0; u < U; u++) keep_in_vgprs(v[u]);
+#pragma unroll
+        for (int u = 0; u < U; u++)
+            if (j0 + u < cnt) f(start + (j0 + u) * step, v[u]);
+    }
+}
+
+// Dot of a contiguous fp32 row with a vector, lanes striding the row, 8 loads in flight per lane.
+template <typename G>
+SOX_DEV float row_dot(const float* __restrict__ w, int len, int lane, G&& vec) {
+    float acc = 0.0f;
+    strided_foreach<8>(w, lane, len, 64, [&](long k, float wv) { acc = __builtin_fmaf(wv, vec((int)k), acc); });
+    return acc;
+}
+
 // ------------------------------------------------------------------------------------------
 // Depthwise k x k (Kernels/Nhwc.cs:496-631): acc = bias[c] + sum over taps (row-major) x*w,
 // + residual, act. One work item = CV channels of one output pixel; taps outside a
@@ -87,6 +140,65 @@ __device__ __forceinline__ void dw_body(const sox_dw_args& p) {
     *(Vec*)((T*)p.y + o) = out;
 }
 
+// K x K specialisation (3x3, 5x5): the taps unroll, every tap's x and w load is issued up front
+// (out-of-image taps read pixel 0 and are masked to the pad value), so a work item costs one memory
+// round trip instead of one per tap.
+template <typename T, int CV, int K>
+__device__ __forceinline__ void dw_body_k(const sox_dw_args& p) {
+    const int cvn = p.c / CV;
+    const long total = (long)p.n * p.oh * p.ow * cvn;
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const int cv = (int)(idx % cvn);
+    long pix = idx / cvn;
+    const int ox = (int)(pix % p.ow);
+    pix /= p.ow;
+    const int oy = (int)(pix % p.oh);
+    const int b = (int)(pix / p.oh);
+    const int c0 = cv * CV;
+    const bool reflect = (p.flags & SOX_F_REFLECT) != 0;
+    const T* __restrict__ x = (const T*)p.x + (long)b * p.ih * p.iw * p.c + c0;
+    const T* __restrict__ w = (const T*)p.w + c0;
+    typedef typename VecT<T, CV>::Vec Vec;
+    Vec xv[K * K], wv[K * K];
+    bool in[K * K];
+#pragma unroll
+    for (int ky = 0; ky < K; ky++) {
+        const int iy = sox_src_index(oy * p.sh + ky - p.pt, p.ih, reflect);
+#pragma unroll
+        for (int kx = 0; kx < K; kx++) {
+            const int ix = sox_src_index(ox * p.sw + kx - p.pl, p.iw, reflect);
+            const int t = ky * K + kx;
+            in[t] = iy >= 0 && ix >= 0;
+            xv[t] = *(const Vec*)(x + (in[t] ? ((long)iy * p.iw + ix) * p.c : 0));
+            wv[t] = *(const Vec*)(w + (long)t * p.c);
+        }
+    }
+    float acc[CV];
+#pragma unroll
+    for (int e = 0; e < CV; e++) acc[e] = (p.flags & SOX_F_BIAS) ? p.bias[c0 + e] : 0.0f;
+#pragma unroll
+    for (int t = 0; t < K * K; t++)
+#pragma unroll
+        for (int e = 0; e < CV; e++)  // taps in row-major order, as the reference accumulates them
+            acc[e] = __builtin_fmaf(in[t] ? to_f(xv[t][e]) : p.pad_value, to_f(wv[t][e]), acc[e]);
+    const int act = (p.flags & SOX_F_ACT_MASK) >> SOX_F_ACT_SHIFT;
+    const long o = (((long)b * p.oh + oy) * p.ow + ox) * p.c + c0;
+    if (p.flags & SOX_F_RESIDUAL) {
+        const Vec av = *(const Vec*)((const T*)p.add + o);
+#pragma unroll
+        for (int e = 0; e < CV; e++) acc[e] = acc[e] + to_f(av[e]);
+    }
+    Vec out;
+#pragma unroll
+    for (int e = 0; e < CV; e++) out[e] = (T)sox_act(acc[e], act);
+    *(Vec*)((T*)p.y + o) = out;
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_dw_f16_v3(sox_dw_args p) { dw_body_k<half_t, 8, 3>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_dw_f16_v5(sox_dw_args p) { dw_body_k<half_t, 8, 5>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_dw_f32_v3(sox_dw_args p) { dw_body_k<float, 4, 3>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_dw_f32_v5(sox_dw_args p) { dw_body_k<float, 4, 5>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_dw_f16_v(sox_dw_args p) { dw_body<half_t, 8>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_dw_f16_s(sox_dw_args p) { dw_body<half_t, 1>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_dw_f32_v(sox_dw_args p) { dw_body<float, 4>(p); }
@@ -160,13 +272,14 @@ __device__ __forceinline__ void gap_body(const sox_gap_args& p) {
     float acc[CV];
 #pragma unroll
     for (int e = 0; e < CV; e++) acc[e] = 0.0f;
-    if (ph < P && t < cg * P) {
-        const T* __restrict__ x = (const T*)p.x + (long)b * p.hw * p.c + g * CV;
-        for (long px = p0 + ph; px < p1; px += P) {
-            Vec v = *(const Vec*)(x + px * p.c);
+    if (ph < P && t < cg * P && p0 + ph < p1) {
+        // pixel px of this channel vector is Vec element px * (c / CV)
+        const Vec* __restrict__ x = (const Vec*)((const T*)p.x + (long)b * p.hw * p.c + g * CV);
+        const long stride = p.c / CV;
+        strided_foreach<4>(x, (p0 + ph) * stride, p1 * stride, P * stride, [&](long, Vec v) {
 #pragma unroll
             for (int e = 0; e < CV; e++) acc[e] += to_f(v[e]);
-        }
+        });
     }
 #pragma unroll
     for (int e = 0; e < CV; e++) red[t * CV + e] = acc[e];
@@ -185,41 +298,49 @@ extern "C" __global__ void __launch_bounds__(256) sox_gap_f32_v(sox_gap_args p) 
 extern "C" __global__ void __launch_bounds__(256) sox_gap_f32_s(sox_gap_args p) { gap_body<float, 1>(p); }
 
 // ------------------------------------------------------------------------------------------
-// SE gate (se_gate.comp; Kernels/Nhwc.Det.cs:287-314), one workgroup of 256 per image.
+// SE gate (se_gate.comp; Kernels/Nhwc.Det.cs:287-314) as two passes over many workgroups.
 // ------------------------------------------------------------------------------------------
-// w1 arrives transposed as [c][r] and w2 as [r][c] (SE weight packing of the HIP backend), so one
-// thread per output reads a coalesced column and no cross-lane reduction is needed.
-template <typename T>
-__device__ __forceinline__ void se_body(const sox_se_args& p) {
-    extern __shared__ float sm[];
-    float* mean = sm;          // [c]
-    float* hid = sm + p.c;     // [r]
-    const int b = blockIdx.x;
+// The SE weights are read once per inference, so they come from HBM/MALL: what costs is the number
+// of dependent memory round trips, not bytes. Each wave owns ONE output row (w1 [r][c] / w2 [c][r]
+// in their ONNX 1x1-conv layouts, contiguous), its lanes stride the row with independent loads and
+// a shuffle tree reduces: one round trip per pass. Four rows per 256-thread workgroup, as many
+// workgroups as rows.
+extern "C" __global__ void __launch_bounds__(256) sox_se_fc1(sox_se_args p) {
+    extern __shared__ float mean[];  // [c]
+    const int b = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const float inv = 1.0f / p.hw;
-    for (int c = threadIdx.x; c < p.c; c += blockDim.x) {
-        float s = 0.0f;
-        for (int k = 0; k < p.chunks; k++) s += p.part[((long)b * p.chunks + k) * p.c + c];
-        mean[c] = s * inv;
+    const float* part = p.part + (long)b * p.chunks * p.c;
+    for (int ch = t; ch < p.c; ch += blockDim.x) {
+        float acc = 0.0f;
+        strided_foreach<16>(part + ch, 0, (long)p.chunks * p.c, p.c, [&](long, float v) { acc += v; });
+        mean[ch] = acc * inv;
     }
     __syncthreads();
-    for (int j = threadIdx.x; j < p.r; j += blockDim.x) {
-        float s = 0.0f;
-        for (int k = 0; k < p.c; k++) s = __builtin_fmaf(p.w1[(long)k * p.r + j], mean[k], s);
+    const int j = blockIdx.x * (blockDim.x >> 6) + wave;
+    if (j >= p.r) return;
+    float s = wave_sum(row_dot(p.w1 + (long)j * p.c, p.c, lane, [&](int k) { return mean[k]; }));
+    if (lane == 0) {
         s += (p.flags & 1) ? p.b1[j] : 0.0f;
-        hid[j] = (p.flags & 4) ? fmaxf(s, 0.0f) : s;
-    }
-    __syncthreads();
-    for (int c = threadIdx.x; c < p.c; c += blockDim.x) {
-        float z = 0.0f;
-        for (int j = 0; j < p.r; j++) z = __builtin_fmaf(p.w2[(long)j * p.c + c], hid[j], z);
-        z += (p.flags & 2) ? p.b2[c] : 0.0f;
-        float g = (p.flags & 8) ? fminf(fmaxf(z * p.alpha + p.beta, 0.0f), 1.0f) : sox_sigmoid(z);
-        ((T*)p.s)[(long)b * p.c + c] = (T)(g + p.offset);
+        p.hid[(long)b * p.r + j] = (p.flags & 4) ? fmaxf(s, 0.0f) : s;
     }
 }
 
-extern "C" __global__ void __launch_bounds__(1024) sox_se_f16(sox_se_args p) { se_body<half_t>(p); }
-extern "C" __global__ void __launch_bounds__(1024) sox_se_f32(sox_se_args p) { se_body<float>(p); }
+template <typename T>
+__device__ __forceinline__ void se_fc2_body(const sox_se_args& p) {
+    const int b = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int ch = blockIdx.x * (blockDim.x >> 6) + wave;
+    if (ch >= p.c) return;
+    const float* hid = p.hid + (long)b * p.r;
+    float z = wave_sum(row_dot(p.w2 + (long)ch * p.r, p.r, lane, [&](int k) { return hid[k]; }));
+    if (lane == 0) {
+        z += (p.flags & 2) ? p.b2[ch] : 0.0f;
+        const float g = (p.flags & 8) ? fminf(fmaxf(z * p.alpha + p.beta, 0.0f), 1.0f) : sox_sigmoid(z);
+        ((T*)p.s)[(long)b * p.c + ch] = (T)(g + p.offset);
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_se_fc2_f16(sox_se_args p) { se_fc2_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_se_fc2_f32(sox_se_args p) { se_fc2_body<float>(p); }
 
 // ------------------------------------------------------------------------------------------
 // Per-channel broadcast y[p, c] = act(x[p, c] op v[img, c]) (ChannelBroadcast, Nhwc.Det.cs:317-351).
@@ -432,25 +553,41 @@ extern "C" __global__ void __launch_bounds__(256) sox_ln_f32(sox_ln_args p) { ln
 // ------------------------------------------------------------------------------------------
 template <typename T>
 __device__ __forceinline__ void softmax_body(const sox_softmax_args& p) {
+    // the row is read once (16 loads in flight per thread) into LDS as fp32 when it fits (dynamic
+    // LDS of len floats, granted by the host), then max, sum and the output come from LDS
+    extern __shared__ float rowbuf[];
     __shared__ float red[4];
     const long row = blockIdx.x;
     const T* x = (const T*)p.x + row * p.len;
     T* y = (T*)p.y + row * p.len;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const bool staged = p.staged != 0;
     float m = -INFINITY;
-    for (int i = threadIdx.x; i < p.len; i += 256) m = fmaxf(m, to_f(x[i]));
+    strided_foreach<16>(x, threadIdx.x, p.len, 256, [&](long i, T v) {
+        const float f = to_f(v);
+        m = fmaxf(m, f);
+        if (staged) rowbuf[i] = f;
+    });
     m = wave_max(m);
     if (lane == 0) red[wv] = m;
     __syncthreads();
     m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     __syncthreads();
     float s = 0.0f;
-    for (int i = threadIdx.x; i < p.len; i += 256) s += sox_exp(to_f(x[i]) - m);
+    if (staged) {
+        for (int i = threadIdx.x; i < p.len; i += 256) s += sox_exp(rowbuf[i] - m);
+    } else {
+        strided_foreach<16>(x, threadIdx.x, p.len, 256, [&](long, T v) { s += sox_exp(to_f(v) - m); });
+    }
     s = wave_sum(s);
     if (lane == 0) red[wv] = s;
     __syncthreads();
     const float inv = 1.0f / ((red[0] + red[1]) + (red[2] + red[3]));
-    for (int i = threadIdx.x; i < p.len; i += 256) y[i] = (T)(sox_exp(to_f(x[i]) - m) * inv);
+    if (staged) {
+        for (int i = threadIdx.x; i < p.len; i += 256) y[i] = (T)(sox_exp(rowbuf[i] - m) * inv);
+    } else {
+        strided_foreach<16>(x, threadIdx.x, p.len, 256, [&](long i, T v) { y[i] = (T)(sox_exp(to_f(v) - m) * inv); });
+    }
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_softmax_f16(sox_softmax_args p) { softmax_body<half_t>(p); }
