@@ -90,7 +90,16 @@ SOX_DEV void store_tile(half_t* __restrict__ Y, int ldy, int M, int N, int m0, i
                 const float v = acc[j][i][4 * q + e];
                 h[e] = (half_t)(ACT == SOX_ACT_GELU ? gelu_fast(v) : ACT >= 0 ? sox_act(v, ACT) : act_fast(v, act));
             });
-            if (m < M && n < N) *(half4*)(Y + (long)m * ldy + n) = h;
+            if (m < M && n < N) {
+                half_t* yp = Y + (long)m * ldy + n;
+                if (((ldy | N) & 3) == 0) {
+                    *(half4*)yp = h;  // 8-byte aligned rows, whole groups of 4
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        if (n + e < N) yp[e] = h[e];
+                }
+            }
         });
         __builtin_amdgcn_sched_barrier(0);  // one block at a time: bounded register pressure
     });
@@ -154,7 +163,8 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
     auto set_sources = [&](int t) {
         int bm, bn;
         tile_origin(t, bm, bn);
-        c_src = has_bias ? p.bias + min(bn + (wave * BIAS_LANES + lane) * 4, N - 4) : (const float*)A;
+        // the bias const is zero-padded to a multiple of 4 floats: the clamped float4 stays inside it
+        c_src = has_bias ? p.bias + min(bn + (wave * BIAS_LANES + lane) * 4, ((N + 3) & ~3) - 4) : (const float*)A;
 #pragma unroll
         for (int i = 0; i < A_IT; i++) {
             const int r = (wave * A_IT + i) * RPI + lane / CPR;

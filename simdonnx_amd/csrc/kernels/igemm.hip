@@ -138,35 +138,44 @@ __device__ __forceinline__ void igemm_body(const sox_igemm_args& p) {
                 ky = tap / p.kw;
                 kx = tap - ky * p.kw;
             }
+            // every load is issued unconditionally (masked lanes read element 0 of x) and the mask
+            // is applied afterwards, so all of a slice's loads are in flight together
+            bool ok[A_IT], inside[A_IT];
 #pragma unroll
             for (int i = 0; i < A_IT; i++) {
-                Vec v = (Vec)(T)0;
-                if (a_iy0[i] > -(1 << 28) && k < K) {
-                    if (AMODE == A_DENSE) {
-                        v = *(const Vec*)(x + a_base[i] + k);
-                    } else {
-                        int iy = sox_src_index(a_iy0[i] + ky, p.ih, reflect);
-                        int ix = sox_src_index(a_ix0[i] + kx, p.iw, reflect);
-                        if (iy >= 0 && ix >= 0)
-                            v = *(const Vec*)(x + a_base[i] + ((long)iy * p.iw + ix) * p.ic + c);
-                        else
-                            v = (Vec)(T)p.pad_value;
-                    }
+                ok[i] = a_iy0[i] > -(1 << 28) && k < K;
+                long off = 0;
+                inside[i] = true;
+                if (AMODE == A_DENSE) {
+                    off = a_base[i] + k;
+                } else {
+                    // rows past M carry a sentinel origin: give them pixel (0, 0) to fold
+                    const bool row = a_iy0[i] > -(1 << 28);
+                    const int iy = sox_src_index(row ? a_iy0[i] + ky : 0, p.ih, reflect);
+                    const int ix = sox_src_index(row ? a_ix0[i] + kx : 0, p.iw, reflect);
+                    inside[i] = iy >= 0 && ix >= 0;
+                    off = a_base[i] + ((long)iy * p.iw + ix) * p.ic + c;
                 }
-                a_reg[i] = v;
+                a_reg[i] = *(const Vec*)(x + (ok[i] && inside[i] ? off : 0));
             }
+#pragma unroll
+            for (int i = 0; i < A_IT; i++)
+                a_reg[i] = ok[i] ? (inside[i] ? a_reg[i] : (Vec)(T)p.pad_value) : (Vec)(T)0;
         }
     };
 
     auto load_b = [&](int k0) {
+        bool ok[B_IT];
 #pragma unroll
         for (int i = 0; i < B_IT; i++) {
             int chunk = tid + i * 256;
             int row = chunk / CPR, n = bn + row, k = k0 + (chunk % CPR) * LD;
-            Vec v = (Vec)(T)0;
-            if (chunk < B_CHUNKS && n < N && k < kpad) v = *(const Vec*)(w + (long)n * kpad + k);
-            b_reg[i] = v;
+            ok[i] = chunk < B_CHUNKS && n < N && k < kpad;
+            b_reg[i] = *(const Vec*)(w + (ok[i] ? (long)n * kpad + k : 0));
         }
+#pragma unroll
+        for (int i = 0; i < B_IT; i++)
+            if (!ok[i]) b_reg[i] = (Vec)(T)0;
     };
 
     auto store_tiles = [&](int buf) {
@@ -270,3 +279,9 @@ SOX_IGEMM(sox_igemm_f16_64x64_d, half_t, 64, 64, 32, 32, 32, A_DENSE)
 SOX_IGEMM(sox_igemm_f16_64x32_v, half_t, 64, 32, 32, 16, 32, A_IM2COL_VEC)
 SOX_IGEMM(sox_igemm_f16_64x32_s, half_t, 64, 32, 32, 16, 32, A_IM2COL_SCALAR)
 SOX_IGEMM(sox_igemm_f16_64x32_d, half_t, 64, 32, 32, 16, 32, A_DENSE)
+// long-K variants (K = kh*kw*ic >= 128, e.g. 3x3 convs over 96 channels): 128-deep slices, a quarter
+// of the load round trips of the 32-deep ones
+SOX_IGEMM(sox_igemm_f16_64x64_vk, half_t, 64, 64, 32, 32, 128, A_IM2COL_VEC)
+SOX_IGEMM(sox_igemm_f16_64x64_dk, half_t, 64, 64, 32, 32, 128, A_DENSE)
+SOX_IGEMM(sox_igemm_f16_64x32_vk, half_t, 64, 32, 32, 16, 128, A_IM2COL_VEC)
+SOX_IGEMM(sox_igemm_f16_64x32_dk, half_t, 64, 32, 32, 16, 128, A_DENSE)

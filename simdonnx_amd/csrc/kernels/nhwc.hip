@@ -237,6 +237,79 @@ __device__ __forceinline__ void convt_body(const sox_convt_args& p) {
 extern "C" __global__ void __launch_bounds__(256) sox_convt_f16(sox_convt_args p) { convt_body<half_t>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_convt_f32(sox_convt_args p) { convt_body<float>(p); }
 
+// Pixel-major ConvTranspose for kh*kw <= 4 taps (the 2x2 stride-2 DBNet head): one work item = one
+// input pixel x 8 output channels for ALL taps, so the pixel's ic channels are loaded once (8 at a
+// time, all in flight) and reused for every tap; the packed weights [tap][ic][oc] sit in LDS as
+// fp32 (host guarantees taps*ic*oc <= 16384) and are read as broadcasts. Output channels of one
+// tap are contiguous: 16-byte stores when oc % 8 == 0.
+template <typename T>
+__device__ __forceinline__ void convt_pix_body(const sox_convt_args& p) {
+    extern __shared__ float wl[];  // [tap][ic][oc]
+    const int taps = p.kh * p.kw, nw = taps * p.ic * p.oc;
+    for (int i = threadIdx.x; i < nw; i += blockDim.x) wl[i] = to_f(((const T*)p.w)[i]);
+    __syncthreads();
+    const int og_n = (p.oc + 7) / 8;
+    const long item = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (item >= (long)p.n * p.ih * p.iw * og_n) return;
+    const int og = (int)(item % og_n);
+    const long pix = item / og_n;
+    const int o0 = og * 8, on = min(8, p.oc - o0);
+    float acc[4][8];
+#pragma unroll
+    for (int o = 0; o < 8; o++) {
+        const float bv = (p.flags & SOX_F_BIAS) && o < on ? p.bias[o0 + o] : 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; t++) acc[t][o] = bv;
+    }
+    const T* __restrict__ xp = (const T*)p.x + pix * p.ic;
+    for (int c0 = 0; c0 < p.ic; c0 += 8) {
+        float xv[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) xv[e] = to_f(xp[min(c0 + e, p.ic - 1)]);
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            if (c0 + e >= p.ic) break;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                if (t >= taps) break;
+                const float* wr = wl + ((long)t * p.ic + c0 + e) * p.oc + o0;
+#pragma unroll
+                for (int o = 0; o < 8; o++) acc[t][o] = __builtin_fmaf(xv[e], wr[o < on ? o : 0], acc[t][o]);
+            }
+        }
+    }
+    const int act = (p.flags & SOX_F_ACT_MASK) >> SOX_F_ACT_SHIFT;
+    const int x = (int)(pix % p.iw);
+    const long q = pix / p.iw;
+    const int y = (int)(q % p.ih), b = (int)(q / p.ih);
+    const int ow = p.iw * p.kw, oh = p.ih * p.kh;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        if (t >= taps) break;
+        const int dy = t / p.kw, dx = t - dy * p.kw;
+        T* out = (T*)p.y + (((long)b * oh + (y * p.kh + dy)) * ow + (x * p.kw + dx)) * p.oc + o0;
+        if (on == 8 && (p.oc & 7) == 0) {
+            typedef typename VecT<T, 8>::Vec Vec8;
+            Vec8 v;
+#pragma unroll
+            for (int o = 0; o < 8; o++) v[o] = (T)sox_act(acc[t][o], act);
+            if (sizeof(T) == 2) {
+                *(Vec8*)out = v;
+            } else {
+#pragma unroll
+                for (int o = 0; o < 8; o++) out[o] = v[o];
+            }
+        } else {
+#pragma unroll
+            for (int o = 0; o < 8; o++)
+                if (o < on) out[o] = (T)sox_act(acc[t][o], act);
+        }
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_convt_pix_f16(sox_convt_args p) { convt_pix_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_convt_pix_f32(sox_convt_args p) { convt_pix_body<float>(p); }
+
 // ------------------------------------------------------------------------------------------
 // Global-average-pool partials (gap_part.comp): part[b][chunk][c] = sum over the chunk's pixels.
 // Grid (chunks, n); the 256 threads are (c / CV) channel vectors x P pixel phases, each thread

@@ -77,10 +77,12 @@ SOX_DEV float sox_ew(float a, float b, int op) {
 template <typename T> SOX_DEV float to_f(T v) { return (float)v; }
 template <typename T> SOX_DEV T from_f(float v) { return (T)v; }
 
+// Reflect padding (no edge repeat): the index folds with period 2*dim - 2, in O(1) for any i.
 SOX_DEV int sox_reflect(int i, int dim) {
     if (dim <= 1) return 0;
-    while (i < 0 || i >= dim) i = i < 0 ? -i : 2 * dim - 2 - i;
-    return i;
+    const int period = 2 * dim - 2;
+    i = abs(i) % period;
+    return i < dim ? i : period - i;
 }
 
 // Source index along one axis, -1 for a constant-pad position (Kernels/Nhwc.cs:72-80).

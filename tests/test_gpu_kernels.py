@@ -207,11 +207,13 @@ GEMM_KERNELS = ["sox_gemm_f16_256x192_k32s5", "sox_gemm_f16_256x128_w8k64s2", "s
 
 @pytest.mark.parametrize("kernel", GEMM_KERNELS)
 @pytest.mark.parametrize("act,shape", [("gelu", (4100, 192, 776)), ("relu", (4100, 192, 776)),
-                                       ("none", (16400, 64, 200)), ("hardswish", (16400, 128, 520))])
+                                       ("none", (16400, 64, 200)), ("hardswish", (16400, 128, 520)),
+                                       ("none", (2560, 192, 6625)), ("relu", (300, 64, 13))])
 def test_pipelined_gemm_variants(hip, kernel, act, shape, monkeypatch):
     """Every LDS-DMA Gemm tiling against the oracle, with M and N tails. The M=16400 cases give every
     tiling more tiles than resident workgroups, so one workgroup's K-slice ring crosses tile borders
-    (with K=64 a border every slice); hardswish takes the runtime-activation epilogue."""
+    (with K=64 a border every slice); hardswish takes the runtime-activation epilogue; N=6625 (the
+    recognizer head) and N=13 take the unaligned-row store path and the zero-padded bias groups."""
     monkeypatch.setenv("SIMDONNX_HIP_GEMM", kernel)
     m, k, n = shape
     a = f16(synth.uniform(21, 1, (m, k), -1, 1))
