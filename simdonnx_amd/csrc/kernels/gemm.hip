@@ -1,7 +1,7 @@
 // Large fp16 Gemm with fused bias + activation on CDNA4 matrix cores (the conv_cm.comp Gemm route,
 // Backends/Vulkan/VkGraph.cs:760-773, rebuilt for gfx950):
-//   Y[M,N] = act(A[M,K] . W[N,K]^T + bias[N]),  A dense rows (lda), W packed [N][kpad] k-fastest,
-//   fp16 storage, fp32 accumulation, fp16 output.
+//   Y[M,N] = act(A[M,K] . W[N,K]^T + bias[N] (+ R[M,N])),  A dense rows (lda), W packed [N][kpad]
+//   k-fastest, R an optional same-shape residual, fp16 storage, fp32 accumulation, fp16 output.
 //
 // Structure (NW waves, BM x BN output tile, BK-deep K slices):
 //  * v_mfma_f32_32x32x16_f16 (the gfx950 instruction that sustains the dense fp16 rate with one wave
@@ -73,26 +73,43 @@ SOX_DEV float act_fast(float v, int act) { return act == SOX_ACT_GELU ? gelu_fas
 // elements 4q .. 4q+3 (the bias is already in the accumulators): activation on a float4, one 8-byte
 // store each.
 template <int ACT, int TJ, int TI>
-SOX_DEV void store_tile(half_t* __restrict__ Y, int ldy, int M, int N, int m0, int n0, const float16v (&acc)[TJ][TI],
-                        int act = 0) {
+SOX_DEV void store_tile(half_t* __restrict__ Y, const half_t* __restrict__ R, int ldy, int M, int N, int m0, int n0,
+                        const float16v (&acc)[TJ][TI], int act = 0) {
     const int lane = threadIdx.x & 63, l32 = lane & 31, hl = lane >> 5;
+    const bool aligned = ((ldy | N) & 3) == 0;
     // static_for, not #pragma unroll: the accumulators must only ever be indexed by constants, or they
     // leave registers
     static_for<0, TJ * TI>([&](auto ji) {
         constexpr int j = decltype(ji)::value / TI, i = decltype(ji)::value % TI;
         const int m = m0 + i * 32 + l32;
+        // residual (the next node's Add, fused): the block's four 8-byte groups load together
+        half4 rv[4];
+        if (R) {
+            static_for<0, 4>([&](auto qq) {
+                constexpr int q = decltype(qq)::value;
+                const int n = n0 + j * 32 + 8 * q + 4 * hl;
+                const long o = (m < M && n < N) ? (long)m * ldy + n : 0;
+                if (aligned) {
+                    rv[q] = *(const half4*)(R + o);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) rv[q][e] = R[o + (n + e < N ? e : 0)];
+                }
+            });
+        }
         static_for<0, 4>([&](auto qq) {
             constexpr int q = decltype(qq)::value;
             const int n = n0 + j * 32 + 8 * q + 4 * hl;
             half4 h;
             static_for<0, 4>([&](auto ee) {
                 constexpr int e = decltype(ee)::value;
-                const float v = acc[j][i][4 * q + e];
+                float v = acc[j][i][4 * q + e];
+                if (R) v += (float)rv[q][e];
                 h[e] = (half_t)(ACT == SOX_ACT_GELU ? gelu_fast(v) : ACT >= 0 ? sox_act(v, ACT) : act_fast(v, act));
             });
             if (m < M && n < N) {
                 half_t* yp = Y + (long)m * ldy + n;
-                if (((ldy | N) & 3) == 0) {
+                if (aligned) {
                     *(half4*)yp = h;  // 8-byte aligned rows, whole groups of 4
                 } else {
 #pragma unroll
@@ -136,6 +153,7 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
     const half_t* __restrict__ A = (const half_t*)p.x;
     const half_t* __restrict__ W = (const half_t*)p.w;
     half_t* __restrict__ Y = (half_t*)p.y;
+    const half_t* __restrict__ R = (p.flags & SOX_F_RESIDUAL) ? (const half_t*)p.add : nullptr;  // [M][ldy]
     const int act = (p.flags & SOX_F_ACT_MASK) >> SOX_F_ACT_SHIFT;
     const bool has_bias = (p.flags & SOX_F_BIAS) != 0;
     const int nk = K / BK;
@@ -285,10 +303,10 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
         if (gs % nk == nk - 1) {
             // ---- epilogue from registers (the next tile's first slices are already loading) ----
             switch (act) {
-            case SOX_ACT_NONE: store_tile<SOX_ACT_NONE>(Y, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc); break;
-            case SOX_ACT_RELU: store_tile<SOX_ACT_RELU>(Y, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc); break;
-            case SOX_ACT_GELU: store_tile<SOX_ACT_GELU>(Y, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc); break;
-            default: store_tile<-1>(Y, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, act); break;
+            case SOX_ACT_NONE: store_tile<SOX_ACT_NONE>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc); break;
+            case SOX_ACT_RELU: store_tile<SOX_ACT_RELU>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc); break;
+            case SOX_ACT_GELU: store_tile<SOX_ACT_GELU>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc); break;
+            default: store_tile<-1>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, act); break;
             }
             if (gs + 1 < total) {
                 tile_origin(vid + (gs + 1) / nk * G, bm_cur, bn_cur);
@@ -317,3 +335,6 @@ SOX_GEMM(sox_gemm_f16_128x128_k64s2, 128, 128, 64, 64, 64, 2, 4, 2, 4)
 SOX_GEMM(sox_gemm_f16_128x128_k32s4, 128, 128, 32, 64, 64, 4, 4, 2, 4)
 SOX_GEMM(sox_gemm_f16_128x64_k64s2, 128, 64, 64, 64, 32, 2, 4, 3, 4)
 SOX_GEMM(sox_gemm_f16_64x64_k64s2, 64, 64, 64, 32, 32, 2, 4, 4, 4)
+// short K (a few slices): every slice of a tile in flight from the start
+SOX_GEMM(sox_gemm_f16_64x64_k64s4, 64, 64, 64, 32, 32, 4, 4, 2, 4)
+SOX_GEMM(sox_gemm_f16_128x64_k64s4, 128, 64, 64, 64, 32, 4, 4, 1, 4)

@@ -603,18 +603,46 @@ __device__ __forceinline__ void ln_body(const sox_ln_args& p) {
     if (row >= p.rows) return;
     const T* x = (const T*)p.x + row * p.len;
     T* y = (T*)p.y + row * p.len;
+    // rows up to 512 stay in registers (8 per lane, loaded together); longer rows are re-read
+    constexpr int R = 8;
+    float xr[R];
     float s = 0.0f, ss = 0.0f;
-    for (int i = lane; i < p.len; i += 64) {
-        float v = to_f(x[i]);
-        s += v;
-        ss = __builtin_fmaf(v, v, ss);
+    if (p.len <= 64 * R) {
+#pragma unroll
+        for (int u = 0; u < R; u++) xr[u] = to_f(x[min(lane + 64 * u, p.len - 1)]);
+#pragma unroll
+        for (int u = 0; u < R; u++)
+            if (lane + 64 * u < p.len) {
+                s += xr[u];
+                ss = __builtin_fmaf(xr[u], xr[u], ss);
+            }
+    } else {
+        strided_foreach<8>(x, lane, p.len, 64, [&](long, T v) {
+            const float f = to_f(v);
+            s += f;
+            ss = __builtin_fmaf(f, f, ss);
+        });
     }
     s = wave_sum(s);
     ss = wave_sum(ss);
     const float mean = s / p.len;
     const float inv = 1.0f / sqrtf(fmaxf(ss / p.len - mean * mean, 0.0f) + p.eps);
-    for (int i = lane; i < p.len; i += 64)
-        y[i] = (T)__builtin_fmaf(to_f(x[i]) - mean, inv * p.gamma[i], p.beta[i]);
+    if (p.len <= 64 * R) {
+        float g[R], bt[R];
+#pragma unroll
+        for (int u = 0; u < R; u++) {
+            const int i = min(lane + 64 * u, p.len - 1);
+            g[u] = p.gamma[i];
+            bt[u] = p.beta[i];
+        }
+#pragma unroll
+        for (int u = 0; u < R; u++)
+            if (lane + 64 * u < p.len) y[lane + 64 * u] = (T)__builtin_fmaf(xr[u] - mean, inv * g[u], bt[u]);
+    } else {
+        strided_foreach<8>(x, lane, p.len, 64, [&](long i, T v) {
+            y[i] = (T)__builtin_fmaf(to_f(v) - mean, inv * p.gamma[i], p.beta[i]);
+        });
+    }
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_ln_f16(sox_ln_args p) { ln_body<half_t>(p); }
@@ -646,9 +674,16 @@ __device__ __forceinline__ void softmax_body(const sox_softmax_args& p) {
     __syncthreads();
     m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     __syncthreads();
+    // fp16 outputs take the hardware exp2 (~1 ulp of fp32, far below the fp16 rounding); fp32
+    // outputs keep the shared Cephes-style exp core
+    auto ex = [](float v) { return sizeof(T) == 2 ? __builtin_amdgcn_exp2f(v * 1.4426950408889634f) : sox_exp(v); };
     float s = 0.0f;
-    if (staged) {
-        for (int i = threadIdx.x; i < p.len; i += 256) s += sox_exp(rowbuf[i] - m);
+    if (staged) {  // each exp once: kept in the row buffer for the output pass
+        for (int i = threadIdx.x; i < p.len; i += 256) {
+            const float e = ex(rowbuf[i] - m);
+            rowbuf[i] = e;
+            s += e;
+        }
     } else {
         strided_foreach<16>(x, threadIdx.x, p.len, 256, [&](long, T v) { s += sox_exp(to_f(v) - m); });
     }
@@ -657,7 +692,7 @@ __device__ __forceinline__ void softmax_body(const sox_softmax_args& p) {
     __syncthreads();
     const float inv = 1.0f / ((red[0] + red[1]) + (red[2] + red[3]));
     if (staged) {
-        for (int i = threadIdx.x; i < p.len; i += 256) y[i] = (T)(sox_exp(rowbuf[i] - m) * inv);
+        for (int i = threadIdx.x; i < p.len; i += 256) y[i] = (T)(rowbuf[i] * inv);
     } else {
         strided_foreach<16>(x, threadIdx.x, p.len, 256, [&](long i, T v) { y[i] = (T)(sox_exp(to_f(v) - m) * inv); });
     }
@@ -916,5 +951,66 @@ __device__ __forceinline__ void conv_direct_body(const sox_igemm_args& p) {
     *(Vec*)((T*)p.y + o) = out;
 }
 
+// 3x3 taps over 3 channels (the RGB stems): all 27 input values of a pixel are loaded up front
+// (out-of-image taps read pixel 0 and take the pad value) instead of one dependent load per term.
+template <typename T, int OCV>
+__device__ __forceinline__ void conv_direct_333_body(const sox_igemm_args& p) {
+    constexpr int KH = 3, KW = 3, IC = 3, K = KH * KW * IC;
+    extern __shared__ float wl[];  // [oc][K]
+    for (int i = threadIdx.x; i < p.n * K; i += blockDim.x) {
+        const int o = i / K, kk = i - o * K;
+        wl[i] = to_f(((const T*)p.w)[(long)o * p.kpad + kk]);
+    }
+    __syncthreads();
+    const int ocg = p.n / OCV;
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long)p.m * ocg) return;
+    const int og = (int)(idx % ocg);
+    const long m = idx / ocg;
+    const int ohw = p.oh * p.ow;
+    const int b = (int)(m / ohw), r = (int)(m - (long)b * ohw);
+    const int oy = r / p.ow, ox = r - oy * p.ow;
+    const bool reflect = (p.flags & SOX_F_REFLECT) != 0;
+    const T* __restrict__ x = (const T*)p.x + (long)b * p.ih * p.iw * IC;
+    float xv[K];
+#pragma unroll
+    for (int ky = 0; ky < KH; ky++) {
+        const int iy = sox_src_index(oy * p.sh + ky - p.pt, p.ih, reflect);
+#pragma unroll
+        for (int kx = 0; kx < KW; kx++) {
+            const int ix = sox_src_index(ox * p.sw + kx - p.pl, p.iw, reflect);
+            const bool in = iy >= 0 && ix >= 0;
+            const T* px = x + (in ? ((long)iy * p.iw + ix) * IC : 0);
+#pragma unroll
+            for (int c = 0; c < IC; c++) {
+                const float v = to_f(px[c]);  // always a valid address: issued with the others
+                xv[(ky * KW + kx) * IC + c] = in ? v : p.pad_value;
+            }
+        }
+    }
+    float acc[OCV];
+#pragma unroll
+    for (int e = 0; e < OCV; e++) acc[e] = (p.flags & SOX_F_BIAS) ? p.bias[og * OCV + e] : 0.0f;
+    const float* w0 = wl + (long)og * OCV * K;
+#pragma unroll
+    for (int kk = 0; kk < K; kk++)
+#pragma unroll
+        for (int e = 0; e < OCV; e++) acc[e] = __builtin_fmaf(xv[kk], w0[e * K + kk], acc[e]);
+    const int act = (p.flags & SOX_F_ACT_MASK) >> SOX_F_ACT_SHIFT;
+    typedef typename VecT<T, OCV>::Vec Vec;
+    const long o = m * p.ldy + og * OCV;
+    if (p.flags & SOX_F_RESIDUAL) {
+        const Vec av = *(const Vec*)((const T*)p.add + o);
+#pragma unroll
+        for (int e = 0; e < OCV; e++) acc[e] = acc[e] + to_f(av[e]);
+    }
+    Vec out;
+#pragma unroll
+    for (int e = 0; e < OCV; e++) out[e] = (T)sox_act(acc[e], act);
+    *(Vec*)((T*)p.y + o) = out;
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_333_f16(sox_igemm_args p) { conv_direct_333_body<half_t, 8>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_333_f32(sox_igemm_args p) { conv_direct_333_body<float, 4>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_f16(sox_igemm_args p) { conv_direct_body<half_t, 8>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_f32(sox_igemm_args p) { conv_direct_body<float, 4>(p); }

@@ -202,7 +202,8 @@ def test_replay_matches_direct(hip):
 GEMM_KERNELS = ["sox_gemm_f16_256x192_k32s5", "sox_gemm_f16_256x128_w8k64s2", "sox_gemm_f16_128x128_k64s2",
                 "sox_gemm_f16_128x64_k64s2", "sox_gemm_f16_64x64_k64s2", "sox_gemm_f16_256x192_k32s4",
                 "sox_gemm_f16_256x192_w8k64s2", "sox_gemm_f16_256x256_w8k32s4", "sox_gemm_f16_256x256_w8k64s2",
-                "sox_gemm_f16_256x128_k32s3", "sox_gemm_f16_256x128_k32s5", "sox_gemm_f16_128x128_k32s4"]
+                "sox_gemm_f16_256x128_k32s3", "sox_gemm_f16_256x128_k32s5", "sox_gemm_f16_128x128_k32s4",
+                "sox_gemm_f16_64x64_k64s4", "sox_gemm_f16_128x64_k64s4"]
 
 
 @pytest.mark.parametrize("kernel", GEMM_KERNELS)
@@ -230,3 +231,27 @@ def test_pipelined_gemm_variants(hip, kernel, act, shape, monkeypatch):
         got = s.run().copy()
     want = O.gemm(a, w, b, act=act)
     assert max_rel(got, want) < TOL[True]
+
+
+@pytest.mark.parametrize("half", [False, True], ids=["f32", "f16"])
+@pytest.mark.parametrize("m,k,n,act", [(2560, 192, 576, "none"), (2560, 768, 192, "relu"), (300, 40, 24, "none")])
+def test_gemm_residual_add_fused(hip, m, k, n, act, half):
+    """Gemm followed by Add(gemm, residual) [+ReLU] runs as one dispatch (the Add in the epilogue) through
+    the LDS-DMA kernel (fp16, K % 64 == 0) or the implicit-GEMM kernel, against the unfused oracle."""
+    cv = f16 if half else (lambda v: v)
+    a = cv(synth.uniform(31, 1, (m, k), -1, 1))
+    r = cv(synth.uniform(31, 2, (m, n), -1, 1))
+    w = cv(synth.normal(31, 3, (k, n), 0.1))
+    b = synth.uniform(31, 4, (n,), -0.1, 0.1)
+    pb = PlanBuilder()
+    av = pb.input((m, k), None, "a")
+    rv = pb.input((m, n), None, "r")
+    y = pb.gemm(av, w, b, name="gemm")
+    z = pb.add(y, rv, act=act, name="res")
+    plan = pb.build(z)
+    g = hip.graph(plan, half)
+    assert [d[0] for d in g.dispatches] == ["gemm"]
+    got = run(hip, plan, [a, r], half)
+    g1 = O.gemm(a, w, b)
+    want = O.ew2(O.round_f16(g1) if half else g1, r, op=0, act=1 if act == "relu" else 0)
+    assert max_rel(got, want) < (2e-2 if half else 1e-4)
