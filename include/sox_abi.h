@@ -29,6 +29,8 @@ enum sox_act { SOX_ACT_NONE = 0, SOX_ACT_RELU = 1, SOX_ACT_SIGMOID = 2, SOX_ACT_
 #define SOX_F_ACT_SHIFT 4
 #define SOX_F_ACT_MASK 0xF0
 #define SOX_F_DENSE_A 0x100 /* A is a plain row-major [M][lda] matrix (Gemm), not an NHWC image */
+#define SOX_F_CONVT 0x200   /* LDS-DMA conv kernels: column n = tap * ct_oc + o of input pixel m is
+                               ConvTranspose output (y * ct_kh + dy, x * ct_kw + dx, o), tap = dy * ct_kw + dx */
 
 /*
  * Implicit-GEMM convolution / Gemm with fused epilogue (conv_cm.comp, gemm.comp).
@@ -43,6 +45,7 @@ typedef struct sox_igemm_args {
     const float* bias;
     const void* add;
     void* y;
+    const void* zeros; /* >= 16 zero bytes: the source of padding taps for LDS-DMA conv kernels */
     int32_t m, n, k, kpad;
     int32_t ih, iw, ic, oh, ow;
     int32_t kh, kw, sh, sw, pt, pl;
@@ -51,6 +54,7 @@ typedef struct sox_igemm_args {
     int32_t ldy;  /* output / residual row stride in elements (n, or a concat channel total) */
     int32_t lda;  /* SOX_F_DENSE_A: A row stride in elements */
     int32_t tiles_n; /* ceil(N/BN): tile-order remap of the 1-D grid */
+    int32_t ct_kh, ct_kw, ct_oc; /* SOX_F_CONVT: the ConvTranspose kernel (stride == kernel) and its channels */
 } sox_igemm_args;
 
 /*
@@ -91,22 +95,30 @@ typedef struct sox_gap_args {
 } sox_gap_args;
 
 /*
- * Squeeze-excitation gate (se_gate.comp; Kernels/Nhwc.Det.cs:287-314) in two passes, each one row
- * per wave across many workgroups:
- *   sox_se_fc1: mean = sum(part)/hw; hid = act1(b1 + W1 mean)        grid (ceil(r/4), n), 256 threads
- *   sox_se_fc2: z = b2 + W2 hid; s = gate(z) + offset  (out [n][c])   grid (ceil(c/4), n), 256 threads
+ * Squeeze-excitation gate (se_gate.comp; Kernels/Nhwc.Det.cs:287-314) in two passes:
+ *   sox_se_fc1: grid (groups, n), groups = ceil(c / 64). Workgroup g averages channels
+ *               [64 g, 64 g + 64) over the GAP partials and writes its share of fc1,
+ *               hid[b][g][j] = sum_{ch in group} W1[j][ch] mean[ch]                      256 threads
+ *   sox_se_fc2: grid (ceil(c/4), n). h = act1(b1 + sum_g hid[b][g]); one wave per channel:
+ *               z = b2 + W2 h; gate = sigmoid(z) or hard-sigmoid, + offset              256 threads
+ *               and either s[b][ch] = gate, or (SOX_SE_FOLD, one image) column ch of the consumer
+ *               1x1 conv's packed weights scaled by it: wdst[n][ch] = wsrc[n][ch] * gate.
  *   w1 [r][c] and w2 [c][r] keep their ONNX 1x1-conv layouts (fp32): one contiguous row per output.
  */
+#define SOX_SE_FOLD 16
 typedef struct sox_se_args {
     const float* part;
     const float* w1;
     const float* b1;
     const float* w2;
     const float* b2;
-    void* s;    /* [n][c] in the graph's storage type */
-    float* hid; /* [n][r] fp32 (scratch) */
-    int32_t c, r, chunks, hw;
-    int32_t flags; /* bit0 b1, bit1 b2, bit2 act1 relu, bit3 hard */
+    void* s;           /* [n][c] in the graph's storage type */
+    float* hid;        /* [n][groups][r] fp32 (scratch) */
+    const void* wsrc;  /* SOX_SE_FOLD: the consumer's weights [wn][wk] (storage type) */
+    void* wdst;        /* SOX_SE_FOLD: their gated copy (scratch) */
+    int32_t c, r, chunks, hw, groups;
+    int32_t wn, wk;
+    int32_t flags; /* bit0 b1, bit1 b2, bit2 act1 relu, bit3 hard, SOX_SE_FOLD */
     float alpha, beta, offset;
 } sox_se_args;
 

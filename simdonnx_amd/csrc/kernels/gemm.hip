@@ -1,326 +1,5 @@
-// Large fp16 Gemm with fused bias + activation on CDNA4 matrix cores (the conv_cm.comp Gemm route,
-// Backends/Vulkan/VkGraph.cs:760-773, rebuilt for gfx950):
-//   Y[M,N] = act(A[M,K] . W[N,K]^T + bias[N] (+ R[M,N])),  A dense rows (lda), W packed [N][kpad]
-//   k-fastest, R an optional same-shape residual, fp16 storage, fp32 accumulation, fp16 output.
-//
-// Structure (NW waves, BM x BN output tile, BK-deep K slices):
-//  * v_mfma_f32_32x32x16_f16 (the gfx950 instruction that sustains the dense fp16 rate with one wave
-//    per SIMD; the 16x16x32 form needs two waves per SIMD and still tops out lower). W is the row
-//    operand and A the column operand, so lane l holds Y^T[n = 8(q/4) + 4(l/32) + q%4][m = l%32]:
-//    4 runs of 4 consecutive output channels of one row, i.e. float4 bias/activation and 8-byte stores
-//    straight from the accumulators.
-//  * K slices move global -> LDS with global_load_lds_dwordx4 (no register staging), STAGES deep.
-//    LDS rows are BK fp16 (CPR 16-byte chunks) stored XOR-swizzled (slot = chunk ^ f(row),
-//    f(r) = (r / (16 / CPR)) % CPR), so the 16 lanes that one ds_read_b128 cycle serves (16 consecutive
-//    rows, same chunk) hit 16 distinct 16-byte bank groups. The swizzle is applied on the load side.
-//  * Register pipeline: k-step s+1's fragments are read while k-step s multiplies; the last k-step of
-//    a slice reads the NEXT slice's first step. One s_barrier per slice, placed there: it publishes
-//    slice g+1 (explicit vmcnt, loads complete in order) and retires slice g's stage, which is
-//    refilled at once with slice g+STAGES.
-//  * The bias never passes through vector registers on its own: each stage carries the tile's BN bias
-//    floats (loaded by the same DMA), and a tile's accumulators start from them, so the epilogue is
-//    activation + store only and no global load result is waited on outside the slice protocol.
-//  * Persistent: each workgroup walks its tiles as ONE ring of K-slices, so the next tile's slices load
-//    while the current tile's epilogue runs. Workgroups are numbered XCD-major (consecutive dispatch
-//    ids land on different XCDs), so the tiles in flight on one XCD are a compact group of GM M-tiles
-//    x some N-tiles and share A rows and W columns in that XCD's L2.
-#include <type_traits>
-
-#include "sox_device.h"
-
-#define LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
-
-// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
-template <int N> SOX_DEV void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-SOX_DEV void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
-
-template <int I, int N, class F> SOX_DEV void static_for(F&& f) {
-    if constexpr (I < N) {
-        f(std::integral_constant<int, I>{});
-        static_for<I + 1, N>(f);
-    }
-}
-
-// LDS chunk swizzle for rows of CPR 16-byte chunks: rows sharing a 256-byte bank window get distinct
-// slots, so 16 consecutive rows read at one chunk hit 16 distinct 16-byte bank groups.
-template <int CPR> SOX_DEV int swz(int r) { return (r / (16 / CPR)) % CPR; }
-
-// erf-GELU with the A&S 7.1.26 erf, rearranged for few instructions:
-//   gelu(x) = x Phi(x) = max(x, 0) - 0.5 |x| (1 - erf(|x| / sqrt2)),
-//   1 - erf(z) = t P(t) exp(-z^2),  t = 1 / (1 + 0.3275911 z)   (z >= 0),
-// with the 0.5 folded into P's coefficients, the hardware reciprocal and exp2 (fp16 outputs: their
-// ~1e-7 relative error is far below the output rounding). |x| is capped at 16 inside the erf term
-// (where that term is < 1e-50) so x = +-inf gives +inf / 0.
-SOX_DEV float gelu_fast(float x) {
-    const float ax = fminf(fabsf(x), 16.0f);
-    const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f * 0.70710678118654752f, ax, 1.0f));
-    float p = 0.5f * 1.061405429f;
-    p = __builtin_fmaf(p, t, 0.5f * -1.453152027f);
-    p = __builtin_fmaf(p, t, 0.5f * 1.421413741f);
-    p = __builtin_fmaf(p, t, 0.5f * -0.284496736f);
-    p = __builtin_fmaf(p, t, 0.5f * 0.254829592f);
-    const float e = __builtin_amdgcn_exp2f((ax * -0.72134752044448170f) * ax);  // exp(-x^2 / 2)
-    return __builtin_fmaf(-(ax * (p * t)), e, fmaxf(x, 0.0f));
-}
-
-SOX_DEV float act_fast(float v, int act) { return act == SOX_ACT_GELU ? gelu_fast(v) : sox_act(v, act); }
-
-// Epilogue of one wave's WM x WN block: lane l (l32 = l % 32, hl = l / 32) of 32x32 block (j, i) holds
-// output row m0 + 32 i + l32 and, for q = 0..3, channels n0 + 32 j + 8 q + 4 hl .. +3 in accumulator
-// elements 4q .. 4q+3 (the bias is already in the accumulators): activation on a float4, one 8-byte
-// store each.
-template <int ACT, int TJ, int TI>
-SOX_DEV void store_tile(half_t* __restrict__ Y, const half_t* __restrict__ R, int ldy, int M, int N, int m0, int n0,
-                        const float16v (&acc)[TJ][TI], int act = 0) {
-    const int lane = threadIdx.x & 63, l32 = lane & 31, hl = lane >> 5;
-    const bool aligned = ((ldy | N) & 3) == 0;
-    // static_for, not #pragma unroll: the accumulators must only ever be indexed by constants, or they
-    // leave registers
-    static_for<0, TJ * TI>([&](auto ji) {
-        constexpr int j = decltype(ji)::value / TI, i = decltype(ji)::value % TI;
-        const int m = m0 + i * 32 + l32;
-        // residual (the next node's Add, fused): the block's four 8-byte groups load together
-        half4 rv[4];
-        if (R) {
-            static_for<0, 4>([&](auto qq) {
-                constexpr int q = decltype(qq)::value;
-                const int n = n0 + j * 32 + 8 * q + 4 * hl;
-                const long o = (m < M && n < N) ? (long)m * ldy + n : 0;
-                if (aligned) {
-                    rv[q] = *(const half4*)(R + o);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; e++) rv[q][e] = R[o + (n + e < N ? e : 0)];
-                }
-            });
-        }
-        static_for<0, 4>([&](auto qq) {
-            constexpr int q = decltype(qq)::value;
-            const int n = n0 + j * 32 + 8 * q + 4 * hl;
-            half4 h;
-            static_for<0, 4>([&](auto ee) {
-                constexpr int e = decltype(ee)::value;
-                float v = acc[j][i][4 * q + e];
-                if (R) v += (float)rv[q][e];
-                h[e] = (half_t)(ACT == SOX_ACT_GELU ? gelu_fast(v) : ACT >= 0 ? sox_act(v, ACT) : act_fast(v, act));
-            });
-            if (m < M && n < N) {
-                half_t* yp = Y + (long)m * ldy + n;
-                if (aligned) {
-                    *(half4*)yp = h;  // 8-byte aligned rows, whole groups of 4
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; e++)
-                        if (n + e < N) yp[e] = h[e];
-                }
-            }
-        });
-        __builtin_amdgcn_sched_barrier(0);  // one block at a time: bounded register pressure
-    });
-}
-
-template <int BM, int BN, int BK, int WM, int WN, int STAGES, int NW, int GM>
-__device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
-    constexpr int CPR = BK / 8;                 // 16-byte chunks per LDS row
-    constexpr int ROWB = BK * 2;                // LDS row bytes
-    constexpr int KS = BK / 16;                 // MFMA k-steps per slice
-    constexpr int A_BYTES = BM * ROWB, B_BYTES = BN * ROWB, BIAS_BYTES = BN * 4;
-    constexpr int STAGE_BYTES = A_BYTES + B_BYTES + BIAS_BYTES;
-    constexpr int BIAS_LANES = BIAS_BYTES / 16 / NW;  // lanes of each wave's bias DMA (16 B each)
-    constexpr int A_IT = A_BYTES / 1024 / NW;   // DMA instructions per wave per slice (1 KiB each)
-    constexpr int B_IT = B_BYTES / 1024 / NW;
-    constexpr int LOADS = A_IT + B_IT + 1;      // + the bias DMA
-    constexpr int TI = WM / 32, TJ = WN / 32;   // 32x32 MFMA blocks: m (columns) x n (rows)
-    constexpr int WAVES_N = BN / WN;
-    constexpr int RPI = 1024 / ROWB;            // rows per 1 KiB DMA instruction
-    static_assert(CPR == 4 || CPR == 8, "BK = 32 or 64");
-    static_assert(KS % 2 == 0, "fragment sets alternate per k-step and must realign per slice");
-    static_assert((BM / WM) * (BN / WN) == NW && WM % 32 == 0 && WN % 32 == 0, "tiling");
-    static_assert(A_IT * 1024 * NW == A_BYTES && B_IT * 1024 * NW == B_BYTES, "DMA split");
-    static_assert(BIAS_LANES * 16 * NW == BIAS_BYTES && BIAS_LANES <= 64 && STAGE_BYTES % 16 == 0, "bias DMA split");
-    static_assert(STAGES >= 2 && (STAGES - 1) * LOADS < 64, "vmcnt range");
-
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[STAGE_BYTES * STAGES];
-
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int l32 = lane & 31, hl = lane >> 5;
-    const int M = p.m, N = p.n, K = p.k;
-    const int tiles_n = p.tiles_n, tiles_m = (M + BM - 1) / BM, ntiles = tiles_m * tiles_n;
-    const int wm0 = (wave / WAVES_N) * WM, wn0 = (wave % WAVES_N) * WN;
-    const half_t* __restrict__ A = (const half_t*)p.x;
-    const half_t* __restrict__ W = (const half_t*)p.w;
-    half_t* __restrict__ Y = (half_t*)p.y;
-    const half_t* __restrict__ R = (p.flags & SOX_F_RESIDUAL) ? (const half_t*)p.add : nullptr;  // [M][ldy]
-    const int act = (p.flags & SOX_F_ACT_MASK) >> SOX_F_ACT_SHIFT;
-    const bool has_bias = (p.flags & SOX_F_BIAS) != 0;
-    const int nk = K / BK;
-
-    // XCD-major workgroup number: dispatch id b runs on XCD b % 8, so XCD x gets the contiguous
-    // numbers [x G/8, (x+1) G/8) and with them consecutive tiles of every round
-    const int G = gridDim.x;
-    const int vid = (G % 8 == 0) ? (blockIdx.x % 8) * (G / 8) + blockIdx.x / 8 : blockIdx.x;
-    const int my_tiles = vid < ntiles ? (ntiles - 1 - vid) / G + 1 : 0;
-    const int total = my_tiles * nk;  // this workgroup's ring of K-slices
-    auto tile_origin = [&](int t, int& bm, int& bn) {  // M-tiles walked in groups of GM
-        const int group = t / (GM * tiles_n), first_m = group * GM;
-        const int gsize = min(tiles_m - first_m, GM);
-        const int in_group = t - group * GM * tiles_n;
-        bm = (first_m + in_group % gsize) * BM;
-        bn = (in_group / gsize) * BN;
-    };
-
-    // DMA sources of the tile being issued: lane l of instruction i of this wave fills LDS slot l of the
-    // 1 KiB block (wave * IT + i), i.e. row (wave * IT + i) * RPI + l / CPR, slot l % CPR, which holds
-    // global chunk slot ^ swz(row). Rows past M / N re-read the last row (never stored).
-    const half_t* a_src[A_IT];
-    const half_t* b_src[B_IT];
-    const float* c_src;  // this lane's 4 bias floats (a duplicate A chunk when there is no bias)
-    auto set_sources = [&](int t) {
-        int bm, bn;
-        tile_origin(t, bm, bn);
-        // the bias const is zero-padded to a multiple of 4 floats: the clamped float4 stays inside it
-        c_src = has_bias ? p.bias + min(bn + (wave * BIAS_LANES + lane) * 4, ((N + 3) & ~3) - 4) : (const float*)A;
-#pragma unroll
-        for (int i = 0; i < A_IT; i++) {
-            const int r = (wave * A_IT + i) * RPI + lane / CPR;
-            const int c = (lane % CPR) ^ swz<CPR>(r);
-            a_src[i] = A + (long)min(bm + r, M - 1) * p.lda + c * 8;
-        }
-#pragma unroll
-        for (int i = 0; i < B_IT; i++) {
-            const int r = (wave * B_IT + i) * RPI + lane / CPR;
-            const int c = (lane % CPR) ^ swz<CPR>(r);
-            b_src[i] = W + (long)min(bn + r, N - 1) * p.kpad + c * 8;
-        }
-    };
-    // ring slice gs = (index in this workgroup's tile list) * nk + k-slice. Slices past the end are
-    // still issued (re-reading the last tile's rows into a stage nobody reads again), so every slice
-    // has the same number of loads in flight and one static vmcnt covers them all.
-    auto issue = [&](int gs) {
-        const int kt = gs % nk;
-        if (kt == 0 && gs < total) set_sources(vid + (gs / nk) * G);
-        unsigned char* st = smem + (gs % STAGES) * STAGE_BYTES;
-        const int k0 = kt * BK;
-#pragma unroll
-        for (int i = 0; i < A_IT; i++)
-            __builtin_amdgcn_global_load_lds(a_src[i] + k0, LDS_PTR(st + (wave * A_IT + i) * 1024), 16, 0, 0);
-#pragma unroll
-        for (int i = 0; i < B_IT; i++)
-            __builtin_amdgcn_global_load_lds(b_src[i] + k0, LDS_PTR(st + A_BYTES + (wave * B_IT + i) * 1024), 16, 0, 0);
-        // the tile's bias rides along with every slice (same bytes each time) so every slice has the
-        // same load count; the accumulators of a new tile start from it
-        if (lane < BIAS_LANES)
-            __builtin_amdgcn_global_load_lds(c_src, LDS_PTR(st + A_BYTES + B_BYTES + wave * BIAS_LANES * 16), 16, 0, 0);
-    };
-
-    // fragment offsets: k-step s of a lane covers chunk 2s + l/32 of rows (row0 + l%32)
-    int a_off[KS][TI], b_off[KS][TJ];
-#pragma unroll
-    for (int s = 0; s < KS; s++) {
-#pragma unroll
-        for (int i = 0; i < TI; i++) {
-            const int r = wm0 + i * 32 + l32;
-            a_off[s][i] = r * ROWB + (((2 * s + hl) ^ swz<CPR>(r)) << 4);
-        }
-#pragma unroll
-        for (int j = 0; j < TJ; j++) {
-            const int r = wn0 + j * 32 + l32;
-            b_off[s][j] = A_BYTES + r * ROWB + (((2 * s + hl) ^ swz<CPR>(r)) << 4);
-        }
-    }
-
-    if (total == 0) return;
-    int bm_cur, bn_cur;  // origin of the tile being multiplied
-    tile_origin(vid, bm_cur, bn_cur);
-
-    float16v acc[TJ][TI];
-    half8 fa0[TI], fb0[TJ], fa1[TI], fb1[TJ];
-    auto read_step = [&](int gs, int s, half8 (&fa)[TI], half8 (&fb)[TJ]) {
-        const unsigned char* st = smem + (gs % STAGES) * STAGE_BYTES;
-#pragma unroll
-        for (int j = 0; j < TJ; j++) fb[j] = *(const half8*)(st + b_off[s][j]);
-#pragma unroll
-        for (int i = 0; i < TI; i++) fa[i] = *(const half8*)(st + a_off[s][i]);
-    };
-    // accumulators of a new tile = its bias (from the LDS stage of the tile's first slice)
-    auto init_acc = [&](int gs) {
-        const float* bl = (const float*)(smem + (gs % STAGES) * STAGE_BYTES + A_BYTES + B_BYTES);
-        static_for<0, TJ>([&](auto jj) {
-            constexpr int j = decltype(jj)::value;
-            float4v b4[4];
-#pragma unroll
-            for (int q = 0; q < 4; q++)
-                b4[q] = has_bias ? *(const float4v*)(bl + wn0 + j * 32 + 8 * q + 4 * hl) : (float4v)0.0f;
-            float16v v;
-            static_for<0, 16>([&](auto qe) { v[decltype(qe)::value] = b4[decltype(qe)::value / 4][decltype(qe)::value % 4]; });
-            static_for<0, TI>([&](auto ii) { acc[j][decltype(ii)::value] = v; });
-        });
-    };
-
-#pragma unroll
-    for (int s = 0; s < STAGES; s++) issue(s);
-    wait_vmcnt<(STAGES - 1) * LOADS>();  // slice 0
-    __builtin_amdgcn_s_barrier();
-    init_acc(0);
-    read_step(0, 0, fa0, fb0);
-    for (int gs = 0; gs < total; gs++) {
-        static_for<0, KS>([&](auto step) {
-            constexpr int s = decltype(step)::value;
-            half8(&ca)[TI] = (s & 1) ? fa1 : fa0;
-            half8(&cb)[TJ] = (s & 1) ? fb1 : fb0;
-            half8(&na)[TI] = (s & 1) ? fa0 : fa1;
-            half8(&nb)[TJ] = (s & 1) ? fb0 : fb1;
-            if constexpr (s == KS - 1) {
-                // slice gs+1 landed (this wave's loads; later slices may stay in flight) and every read
-                // of slice gs done; after the barrier both hold for all waves
-                wait_vmcnt<(STAGES - 2) * LOADS>();
-                wait_lgkmcnt0();
-                __builtin_amdgcn_s_barrier();
-                issue(gs + STAGES);  // into stage gs % STAGES; may already be a later tile's slice
-                read_step(gs + 1, 0, na, nb);
-            } else {
-                read_step(gs, s + 1, na, nb);
-            }
-            static_for<0, TJ * TI>([&](auto ji) {
-                constexpr int j = decltype(ji)::value / TI, i = decltype(ji)::value % TI;
-                acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cb[j], ca[i], acc[j][i], 0, 0, 0);
-            });
-            // MFMA, read, MFMA, read, ...: this step's operands were read one step earlier, and the
-            // next step's reads issue while the matrix pipe works through this step
-            constexpr int RD = TI + TJ, MF = TI * TJ;
-            static_for<0, (RD < MF ? RD : MF)>([&](auto) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            });
-            if constexpr (MF > RD) __builtin_amdgcn_sched_group_barrier(0x008, MF - RD, 0);
-            if constexpr (RD > MF) __builtin_amdgcn_sched_group_barrier(0x100, RD - MF, 0);
-            __builtin_amdgcn_sched_barrier(0);
-        });
-        wait_lgkmcnt0();  // next slice's first fragments (read before this slice's last MFMAs)
-        if (gs % nk == nk - 1) {
-            // ---- epilogue from registers (the next tile's first slices are already loading) ----
-            switch (act) {
-            case SOX_ACT_NONE: store_tile<SOX_ACT_NONE>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc); break;
-            case SOX_ACT_RELU: store_tile<SOX_ACT_RELU>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc); break;
-            case SOX_ACT_GELU: store_tile<SOX_ACT_GELU>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc); break;
-            default: store_tile<-1>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, act); break;
-            }
-            if (gs + 1 < total) {
-                tile_origin(vid + (gs + 1) / nk * G, bm_cur, bn_cur);
-                init_acc(gs + 1);  // published by this slice's barrier
-            }
-        }
-    }
-    wait_vmcnt<0>();  // the trailing (unused) slices land before the workgroup's LDS is released
-}
-
-#define SOX_GEMM(NAME, BM, BN, BK, WM, WN, ST, NW, OCC, GM)                                         \
-    extern "C" __global__ void __launch_bounds__(64 * NW, OCC) NAME(sox_igemm_args p) {           \
-        gemm_body<BM, BN, BK, WM, WN, ST, NW, GM>(p);                                             \
-    }
+// Dense fp16 Gemm instances of the LDS-DMA persistent ring (gemm_ring.h).
+#include "gemm_ring.h"
 
 // name: BMxBN tile, kBK slice depth, sSTAGES, wNW waves (4 when absent)
 SOX_GEMM(sox_gemm_f16_256x192_k32s5, 256, 192, 32, 128, 96, 5, 4, 1, 4)
@@ -338,3 +17,4 @@ SOX_GEMM(sox_gemm_f16_64x64_k64s2, 64, 64, 64, 32, 32, 2, 4, 4, 4)
 // short K (a few slices): every slice of a tile in flight from the start
 SOX_GEMM(sox_gemm_f16_64x64_k64s4, 64, 64, 64, 32, 32, 4, 4, 2, 4)
 SOX_GEMM(sox_gemm_f16_128x64_k64s4, 128, 64, 64, 64, 32, 4, 4, 1, 4)
+

@@ -1,0 +1,514 @@
+// The LDS-DMA persistent ring (instantiated by gemm.hip for dense Gemm and conv_ring.hip for Conv2d /
+// ConvTranspose): fp16 Gemm with fused bias + activation on CDNA4 matrix cores (the conv_cm.comp Gemm
+// route, Backends/Vulkan/VkGraph.cs:760-773, rebuilt for gfx950):
+//   Y[M,N] = act(A[M,K] . W[N,K]^T + bias[N] (+ R[M,N])),  A dense rows (lda), W packed [N][kpad]
+//   k-fastest, R an optional same-shape residual, fp16 storage, fp32 accumulation, fp16 output.
+//
+// Structure (NW waves, BM x BN output tile, BK-deep K slices):
+//  * v_mfma_f32_32x32x16_f16 (the gfx950 instruction that sustains the dense fp16 rate with one wave
+//    per SIMD; the 16x16x32 form needs two waves per SIMD and still tops out lower). W is the row
+//    operand and A the column operand, so lane l holds Y^T[n = 8(q/4) + 4(l/32) + q%4][m = l%32]:
+//    4 runs of 4 consecutive output channels of one row, i.e. float4 bias/activation and 8-byte stores
+//    straight from the accumulators.
+//  * K slices move global -> LDS with global_load_lds_dwordx4 (no register staging), STAGES deep.
+//    LDS rows are BK fp16 (CPR 16-byte chunks) stored XOR-swizzled (slot = chunk ^ f(row),
+//    f(r) = (r / (16 / CPR)) % CPR), so the 16 lanes that one ds_read_b128 cycle serves (16 consecutive
+//    rows, same chunk) hit 16 distinct 16-byte bank groups. The swizzle is applied on the load side.
+//  * Register pipeline: k-step s+1's fragments are read while k-step s multiplies; the last k-step of
+//    a slice reads the NEXT slice's first step. One s_barrier per slice, placed there: it publishes
+//    slice g+1 (explicit vmcnt, loads complete in order) and retires slice g's stage, which is
+//    refilled at once with slice g+STAGES.
+//  * The bias never passes through vector registers on its own: each stage carries the tile's BN bias
+//    floats (loaded by the same DMA), and a tile's accumulators start from them, so the epilogue is
+//    activation + store only and no global load result is waited on outside the slice protocol.
+//  * Persistent: each workgroup walks its tiles as ONE ring of K-slices, so the next tile's slices load
+//    while the current tile's epilogue runs. Workgroups are numbered XCD-major (consecutive dispatch
+//    ids land on different XCDs), so the tiles in flight on one XCD are a compact group of GM M-tiles
+//    x some N-tiles and share A rows and W columns in that XCD's L2.
+#pragma once
+#include <type_traits>
+
+#include "sox_device.h"
+
+#define LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
+template <int N> SOX_DEV void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+SOX_DEV void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
+
+template <int I, int N, class F> SOX_DEV void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
+// LDS chunk swizzle for rows of CPR 16-byte chunks: rows sharing a 256-byte bank window get distinct
+// slots, so 16 consecutive rows read at one chunk hit 16 distinct 16-byte bank groups.
+template <int CPR> SOX_DEV int swz(int r) { return (r / (16 / CPR)) % CPR; }
+
+// erf-GELU with the A&S 7.1.26 erf, rearranged for few instructions:
+//   gelu(x) = x Phi(x) = max(x, 0) - 0.5 |x| (1 - erf(|x| / sqrt2)),
+//   1 - erf(z) = t P(t) exp(-z^2),  t = 1 / (1 + 0.3275911 z)   (z >= 0),
+// with the 0.5 folded into P's coefficients, the hardware reciprocal and exp2 (fp16 outputs: their
+// ~1e-7 relative error is far below the output rounding). |x| is capped at 16 inside the erf term
+// (where that term is < 1e-50) so x = +-inf gives +inf / 0.
+SOX_DEV float gelu_fast(float x) {
+    const float ax = fminf(fabsf(x), 16.0f);
+    const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f * 0.70710678118654752f, ax, 1.0f));
+    float p = 0.5f * 1.061405429f;
+    p = __builtin_fmaf(p, t, 0.5f * -1.453152027f);
+    p = __builtin_fmaf(p, t, 0.5f * 1.421413741f);
+    p = __builtin_fmaf(p, t, 0.5f * -0.284496736f);
+    p = __builtin_fmaf(p, t, 0.5f * 0.254829592f);
+    const float e = __builtin_amdgcn_exp2f((ax * -0.72134752044448170f) * ax);  // exp(-x^2 / 2)
+    return __builtin_fmaf(-(ax * (p * t)), e, fmaxf(x, 0.0f));
+}
+
+SOX_DEV float act_fast(float v, int act) { return act == SOX_ACT_GELU ? gelu_fast(v) : sox_act(v, act); }
+
+// Epilogue of one wave's WM x WN block: lane l (l32 = l % 32, hl = l / 32) of 32x32 block (j, i) holds
+// output row m0 + 32 i + l32 and, for q = 0..3, channels n0 + 32 j + 8 q + 4 hl .. +3 in accumulator
+// elements 4q .. 4q+3 (the bias is already in the accumulators): activation on a float4, one 8-byte
+// store each.
+// ConvTranspose scatter (SOX_F_CONVT): output row m = (b, y, x) of the ih x iw input and column
+// n = tap * oc + o land at pixel (y * kh + dy, x * kw + dx) of the output, tap = dy * kw + dx; the
+// per-channel bias (bias[o], the same for every tap) is added here, before the activation.
+struct ConvtOut {
+    int ih, iw, kh, kw, oc;
+    const float* bias;
+};
+
+template <int ACT, int TJ, int TI>
+SOX_DEV void store_tile(half_t* __restrict__ Y, const half_t* __restrict__ R, int ldy, int M, int N, int m0, int n0,
+                        const float16v (&acc)[TJ][TI], int act = 0, bool convt = false, ConvtOut ctv = {}) {
+    const int lane = threadIdx.x & 63, l32 = lane & 31, hl = lane >> 5;
+    const bool aligned = ((ldy | N) & 3) == 0;
+    if (convt) {  // uniform: ConvTranspose output, no residual
+        const ConvtOut* ct = &ctv;
+        auto fin = [&](float a) { return ACT == SOX_ACT_GELU ? gelu_fast(a) : ACT >= 0 ? sox_act(a, ACT) : act_fast(a, act); };
+        static_for<0, TJ * TI>([&](auto ji) {
+            constexpr int j = decltype(ji)::value / TI, i = decltype(ji)::value % TI;
+            const int m = m0 + i * 32 + l32;
+            const int x = m % ct->iw, yb = m / ct->iw, y = yb % ct->ih, b = yb / ct->ih;
+            const long ow = (long)ct->iw * ct->kw, base = ((long)b * ct->ih * ct->kh + (long)y * ct->kh) * ow + (long)x * ct->kw;
+            static_for<0, 4>([&](auto qq) {
+                constexpr int q = decltype(qq)::value;
+                const int n = n0 + j * 32 + 8 * q + 4 * hl;
+                if (m < M) {
+                    if (ct->oc % 4 == 0) {  // the group's four channels share one tap
+                        if (n < N) {
+                            const int t = n / ct->oc, o = n - t * ct->oc, dy = t / ct->kw, dx = t - dy * ct->kw;
+                            half4 h;
+                            static_for<0, 4>([&](auto ee) {
+                                constexpr int e = decltype(ee)::value;
+                                h[e] = (half_t)fin(acc[j][i][4 * q + e] + (ct->bias ? ct->bias[o + e] : 0.0f));
+                            });
+                            *(half4*)(Y + (base + (long)dy * ow + dx) * ct->oc + o) = h;
+                        }
+                    } else {
+                        static_for<0, 4>([&](auto ee) {
+                            constexpr int e = decltype(ee)::value;
+                            if (n + e < N) {
+                                const int t = (n + e) / ct->oc, o = n + e - t * ct->oc, dy = t / ct->kw, dx = t - dy * ct->kw;
+                                Y[(base + (long)dy * ow + dx) * ct->oc + o] =
+                                    (half_t)fin(acc[j][i][4 * q + e] + (ct->bias ? ct->bias[o] : 0.0f));
+                            }
+                        });
+                    }
+                }
+            });
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        return;
+    }
+    // static_for, not #pragma unroll: the accumulators must only ever be indexed by constants, or they
+    // leave registers
+    static_for<0, TJ * TI>([&](auto ji) {
+        constexpr int j = decltype(ji)::value / TI, i = decltype(ji)::value % TI;
+        const int m = m0 + i * 32 + l32;
+        // residual (the next node's Add, fused): the block's four 8-byte groups load together
+        half4 rv[4];
+        if (R) {
+            static_for<0, 4>([&](auto qq) {
+                constexpr int q = decltype(qq)::value;
+                const int n = n0 + j * 32 + 8 * q + 4 * hl;
+                const long o = (m < M && n < N) ? (long)m * ldy + n : 0;
+                if (aligned) {
+                    rv[q] = *(const half4*)(R + o);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) rv[q][e] = R[o + (n + e < N ? e : 0)];
+                }
+            });
+            // vmcnt counts in order, so these wait behind every DMA in flight anyway; waiting here, on
+            // every path that loaded, keeps the compiler from carrying them into the K loop as pending
+            // writes (which costs a full vmcnt(0) drain per slice)
+            wait_vmcnt<0>();
+        }
+        static_for<0, 4>([&](auto qq) {
+            constexpr int q = decltype(qq)::value;
+            const int n = n0 + j * 32 + 8 * q + 4 * hl;
+            half4 h;
+            static_for<0, 4>([&](auto ee) {
+                constexpr int e = decltype(ee)::value;
+                float v = acc[j][i][4 * q + e];
+                if (R) v += (float)rv[q][e];
+                h[e] = (half_t)(ACT == SOX_ACT_GELU ? gelu_fast(v) : ACT >= 0 ? sox_act(v, ACT) : act_fast(v, act));
+            });
+            if (m < M && n < N) {
+                half_t* yp = Y + (long)m * ldy + n;
+                if (aligned) {
+                    *(half4*)yp = h;  // 8-byte aligned rows, whole groups of 4
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        if (n + e < N) yp[e] = h[e];
+                }
+            }
+        });
+        __builtin_amdgcn_sched_barrier(0);  // one block at a time: bounded register pressure
+    });
+}
+
+// CONV = false: A is a dense [M][lda] matrix (Gemm). CONV = true: A is the implicit im2col matrix of
+// an NHWC image, A[m][k] = x[b][oy*sh - pt + ky][ox*sw - pl + kx][c] for m = (b, oy, ox) and
+// k = (ky*kw + kx)*ic + c (tap-major, the packed weights' order). The K loop walks taps x channel
+// blocks of BK, so a slice never straddles a tap: its tap is uniform (scalar math) and a lane's source
+// is its row's offset + the tap's offset + its channel. Channels past ic (the last block of a tap
+// when BK does not divide ic) and zero-padding taps are fetched from p.zeros; ic % 8 == 0. Rows past
+// M re-read row M - 1 (never stored).
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int NW, int GM, bool CONV = false, bool PF = false>
+__device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
+    constexpr int CPR = BK / 8;                 // 16-byte chunks per LDS row
+    constexpr int ROWB = BK * 2;                // LDS row bytes
+    constexpr int KS = BK / 16;                 // MFMA k-steps per slice
+    constexpr int A_BYTES = BM * ROWB, B_BYTES = BN * ROWB, BIAS_BYTES = BN * 4;
+    constexpr int STAGE_BYTES = A_BYTES + B_BYTES + BIAS_BYTES;
+    constexpr int BIAS_LANES = BIAS_BYTES / 16 / NW;  // lanes of each wave's bias DMA (16 B each)
+    // DMA instructions per wave per slice; each fills CH contiguous LDS bytes (<= 1 KiB: lanes past
+    // CH / 16 are idle when a wave's share is smaller)
+    constexpr int CH_A = A_BYTES / NW < 1024 ? A_BYTES / NW : 1024, A_IT = A_BYTES / NW / CH_A;
+    constexpr int CH_B = B_BYTES / NW < 1024 ? B_BYTES / NW : 1024, B_IT = B_BYTES / NW / CH_B;
+    constexpr int LOADS = A_IT + B_IT + 1;      // + the bias DMA
+    constexpr int TI = WM / 32, TJ = WN / 32;   // 32x32 MFMA blocks: m (columns) x n (rows)
+    constexpr int WAVES_N = BN / WN;
+    static_assert(CPR == 4 || CPR == 8, "BK = 32 or 64");
+    static_assert(KS % 2 == 0, "fragment sets alternate per k-step and must realign per slice");
+    static_assert((BM / WM) * (BN / WN) == NW && WM % 32 == 0 && WN % 32 == 0, "tiling");
+    static_assert(A_IT * CH_A * NW == A_BYTES && B_IT * CH_B * NW == B_BYTES && CH_A % 16 == 0 && CH_B % 16 == 0,
+                  "DMA split");
+    static_assert(BIAS_LANES * 16 * NW == BIAS_BYTES && BIAS_LANES <= 64 && STAGE_BYTES % 16 == 0, "bias DMA split");
+    static_assert(STAGES >= 2 && (STAGES - 1) * LOADS < 64, "vmcnt range");
+
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[STAGE_BYTES * STAGES];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int l32 = lane & 31, hl = lane >> 5;
+    const int M = p.m, N = p.n, K = p.k;
+    const int tiles_n = p.tiles_n, tiles_m = (M + BM - 1) / BM, ntiles = tiles_m * tiles_n;
+    const int wm0 = (wave / WAVES_N) * WM, wn0 = (wave % WAVES_N) * WN;
+    const half_t* __restrict__ A = (const half_t*)p.x;
+    const half_t* __restrict__ W = (const half_t*)p.w;
+    const half_t* __restrict__ Z = (const half_t*)p.zeros;
+    half_t* __restrict__ Y = (half_t*)p.y;
+    const half_t* __restrict__ R = (p.flags & SOX_F_RESIDUAL) ? (const half_t*)p.add : nullptr;  // [M][ldy]
+    const int act = (p.flags & SOX_F_ACT_MASK) >> SOX_F_ACT_SHIFT;
+    // a ConvTranspose's bias is per output channel, added in its scatter epilogue, not per column
+    const bool has_bias = (p.flags & SOX_F_BIAS) != 0 && !(CONV && (p.flags & SOX_F_CONVT));
+    const int cblocks = CONV ? (p.ic + BK - 1) / BK : 1;  // channel blocks per tap
+    const int nk = CONV ? p.kh * p.kw * cblocks : K / BK;
+    const bool reflect = (p.flags & SOX_F_REFLECT) != 0;
+
+    // XCD-major workgroup number: dispatch id b runs on XCD b % 8, so XCD x gets the contiguous
+    // numbers [x G/8, (x+1) G/8) and with them consecutive tiles of every round
+    const int G = gridDim.x;
+    const int vid = (G % 8 == 0) ? (blockIdx.x % 8) * (G / 8) + blockIdx.x / 8 : blockIdx.x;
+    const int my_tiles = vid < ntiles ? (ntiles - 1 - vid) / G + 1 : 0;
+    const int total = my_tiles * nk;  // this workgroup's ring of K-slices
+    auto tile_origin = [&](int t, int& bm, int& bn) __attribute__((always_inline)) {  // M-tiles walked in groups of GM
+        const int group = t / (GM * tiles_n), first_m = group * GM;
+        const int gsize = min(tiles_m - first_m, GM);
+        const int in_group = t - group * GM * tiles_n;
+        bm = (first_m + in_group % gsize) * BM;
+        bn = (in_group / gsize) * BN;
+    };
+
+    // DMA sources of the tile being issued: lane l of instruction i of this wave fills the 16 LDS bytes
+    // at (wave * IT + i) * CH + 16 l, i.e. row r = that offset / ROWB, slot (offset % ROWB) / 16, which
+    // holds global chunk slot ^ swz(r). Rows past M / N re-read the last row (never stored).
+    const bool a_lane = lane * 16 < CH_A, b_lane = lane * 16 < CH_B;
+    int a_chunk[A_IT], b_chunk[B_IT];  // global chunk (k / 8 within the slice) of each instruction
+    const half_t* a_src[A_IT];         // dense A: row base + chunk; conv: image base of the row's batch
+    int a_iy0[A_IT], a_ix0[A_IT];      // conv: the row's receptive-field origin
+    int a_off0[A_IT];                  // conv: (iy0 * iw + ix0) * ic, the origin's offset in its image
+    const half_t* b_src[B_IT];
+    const float* c_src;  // this lane's 4 bias floats (a duplicate A chunk when there is no bias)
+#pragma unroll
+    for (int i = 0; i < A_IT; i++) {
+        const int off = (wave * A_IT + i) * CH_A + lane * 16, r = off / ROWB;
+        a_chunk[i] = ((off % ROWB) / 16) ^ swz<CPR>(r);
+    }
+#pragma unroll
+    for (int i = 0; i < B_IT; i++) {
+        const int off = (wave * B_IT + i) * CH_B + lane * 16, r = off / ROWB;
+        b_chunk[i] = ((off % ROWB) / 16) ^ swz<CPR>(r);
+    }
+    auto set_sources = [&](int t) __attribute__((always_inline)) {
+        int bm, bn;
+        tile_origin(t, bm, bn);
+        // the bias const is zero-padded to a multiple of 4 floats: the clamped float4 stays inside it
+        c_src = has_bias ? p.bias + min(bn + (wave * BIAS_LANES + lane) * 4, ((N + 3) & ~3) - 4) : (const float*)A;
+#pragma unroll
+        for (int i = 0; i < A_IT; i++) {
+            const int r = ((wave * A_IT + i) * CH_A + lane * 16) / ROWB;
+            if constexpr (CONV) {
+                const int m = min(bm + r, M - 1);
+                const int ohw = p.oh * p.ow, b = m / ohw, rem = m - b * ohw;
+                const int oy = rem / p.ow, ox = rem - oy * p.ow;
+                a_iy0[i] = oy * p.sh - p.pt;
+                a_ix0[i] = ox * p.sw - p.pl;
+                a_off0[i] = (a_iy0[i] * p.iw + a_ix0[i]) * p.ic;
+                a_src[i] = A + (long)b * p.ih * p.iw * p.ic;
+            } else {
+                a_src[i] = A + (long)min(bm + r, M - 1) * p.lda + a_chunk[i] * 8;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < B_IT; i++) {
+            const int r = ((wave * B_IT + i) * CH_B + lane * 16) / ROWB;
+            b_src[i] = W + (long)min(bn + r, N - 1) * p.kpad + b_chunk[i] * 8;
+        }
+    };
+    // ring slice gs = (index in this workgroup's tile list) * nk + k-slice. Slices past the end are
+    // still issued (re-reading the last tile's rows into a stage nobody reads again), so every slice
+    // has the same number of loads in flight and one static vmcnt covers them all.
+    // prep computes a slice's DMA sources (calling set_sources at a tile's first slice), fire issues
+    // the DMAs; the small-tile loop runs prep a slice early, under the MFMAs.
+    struct Src {
+        const half_t* a[A_IT];
+        const half_t* b[B_IT];
+        const float* c;
+    };
+    auto prep = [&](int gs, Src& q) __attribute__((always_inline)) {
+        const int kt = gs % nk;
+        if (kt == 0 && gs < total) set_sources(vid + (gs / nk) * G);
+        if constexpr (CONV) {
+            // uniform: the slice's tap (ky, kx) and first channel c0
+            const int tap = kt / cblocks, c0 = (kt - tap * cblocks) * BK;
+            const int ky = tap / p.kw, kx = tap - ky * p.kw;
+            const int tap_off = (ky * p.iw + kx) * p.ic;
+#pragma unroll
+            for (int i = 0; i < A_IT; i++) {
+                const int ch = c0 + a_chunk[i] * 8;
+                const int iy = a_iy0[i] + ky, ix = a_ix0[i] + kx;
+                bool ok = (unsigned)iy < (unsigned)p.ih && (unsigned)ix < (unsigned)p.iw;
+                int off = a_off0[i] + tap_off + ch;
+                if (reflect) {  // uniform; folds once: the launcher only routes pads < the image size here
+                    const int ry = iy < 0 ? -iy : iy >= p.ih ? 2 * p.ih - 2 - iy : iy;
+                    const int rx = ix < 0 ? -ix : ix >= p.iw ? 2 * p.iw - 2 - ix : ix;
+                    off = (ry * p.iw + rx) * p.ic + ch;
+                    ok = true;
+                }
+                ok = ok && ch < p.ic;
+                q.a[i] = ok ? a_src[i] + off : Z;  // one image < 2^31 elements
+            }
+#pragma unroll
+            for (int i = 0; i < B_IT; i++) {
+                const int ch = c0 + b_chunk[i] * 8;
+                q.b[i] = ch < p.ic ? b_src[i] + tap * p.ic + c0 : Z;  // b_src includes the chunk
+            }
+        } else {
+            const int k0 = kt * BK;
+#pragma unroll
+            for (int i = 0; i < A_IT; i++) q.a[i] = a_src[i] + k0;
+#pragma unroll
+            for (int i = 0; i < B_IT; i++) q.b[i] = b_src[i] + k0;
+        }
+        q.c = c_src;
+    };
+    auto fire = [&](int gs, const Src& q) __attribute__((always_inline)) {
+        unsigned char* st = smem + (gs % STAGES) * STAGE_BYTES;
+#pragma unroll
+        for (int i = 0; i < A_IT; i++)
+            if (a_lane) __builtin_amdgcn_global_load_lds(q.a[i], LDS_PTR(st + (wave * A_IT + i) * CH_A), 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < B_IT; i++)
+            if (b_lane)
+                __builtin_amdgcn_global_load_lds(q.b[i], LDS_PTR(st + A_BYTES + (wave * B_IT + i) * CH_B), 16, 0, 0);
+        // the tile's bias rides along with every slice (same bytes each time) so every slice has the
+        // same load count; the accumulators of a new tile start from it
+        if (lane < BIAS_LANES)
+            __builtin_amdgcn_global_load_lds(q.c, LDS_PTR(st + A_BYTES + B_BYTES + wave * BIAS_LANES * 16), 16, 0, 0);
+    };
+    auto issue = [&](int gs) __attribute__((always_inline)) {
+        Src q;
+        prep(gs, q);
+        fire(gs, q);
+    };
+
+    // fragment offsets: k-step s of a lane covers chunk 2s + l/32 of rows (row0 + l%32)
+    int a_off[KS][TI], b_off[KS][TJ];
+#pragma unroll
+    for (int s = 0; s < KS; s++) {
+#pragma unroll
+        for (int i = 0; i < TI; i++) {
+            const int r = wm0 + i * 32 + l32;
+            a_off[s][i] = r * ROWB + (((2 * s + hl) ^ swz<CPR>(r)) << 4);
+        }
+#pragma unroll
+        for (int j = 0; j < TJ; j++) {
+            const int r = wn0 + j * 32 + l32;
+            b_off[s][j] = A_BYTES + r * ROWB + (((2 * s + hl) ^ swz<CPR>(r)) << 4);
+        }
+    }
+
+    if (total == 0) return;
+    int bm_cur, bn_cur;  // origin of the tile being multiplied
+    tile_origin(vid, bm_cur, bn_cur);
+
+    float16v acc[TJ][TI];
+    half8 fa0[TI], fb0[TJ], fa1[TI], fb1[TJ];
+    auto read_step = [&](int gs, int s, half8 (&fa)[TI], half8 (&fb)[TJ]) __attribute__((always_inline)) {
+        const unsigned char* st = smem + (gs % STAGES) * STAGE_BYTES;
+#pragma unroll
+        for (int j = 0; j < TJ; j++) fb[j] = *(const half8*)(st + b_off[s][j]);
+#pragma unroll
+        for (int i = 0; i < TI; i++) fa[i] = *(const half8*)(st + a_off[s][i]);
+    };
+    // accumulators of a new tile = its bias (from the LDS stage of the tile's first slice)
+    auto init_acc = [&](int gs) __attribute__((always_inline)) {
+        const float* bl = (const float*)(smem + (gs % STAGES) * STAGE_BYTES + A_BYTES + B_BYTES);
+        static_for<0, TJ>([&](auto jj) {
+            constexpr int j = decltype(jj)::value;
+            float4v b4[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                b4[q] = has_bias ? *(const float4v*)(bl + wn0 + j * 32 + 8 * q + 4 * hl) : (float4v)0.0f;
+            float16v v;
+            static_for<0, 16>([&](auto qe) { v[decltype(qe)::value] = b4[decltype(qe)::value / 4][decltype(qe)::value % 4]; });
+            static_for<0, TI>([&](auto ii) { acc[j][decltype(ii)::value] = v; });
+        });
+    };
+
+    const ConvtOut cto{p.ih, p.iw, p.ct_kh, p.ct_kw, p.ct_oc, (p.flags & SOX_F_BIAS) ? p.bias : nullptr};
+    const bool ctp = CONV && (p.flags & SOX_F_CONVT);
+    auto epilogue = [&](int gs) __attribute__((always_inline)) {
+        // ---- epilogue from registers (the next tile's first slices are already loading) ----
+        switch (act) {
+        case SOX_ACT_NONE: store_tile<SOX_ACT_NONE>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, ctp, cto); break;
+        case SOX_ACT_RELU: store_tile<SOX_ACT_RELU>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, ctp, cto); break;
+        case SOX_ACT_GELU: store_tile<SOX_ACT_GELU>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, ctp, cto); break;
+        default: store_tile<-1>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, act, ctp, cto); break;
+        }
+        if (gs + 1 < total) {
+            tile_origin(vid + (gs + 1) / nk * G, bm_cur, bn_cur);
+            init_acc(gs + 1);  // published by this slice's barrier
+        }
+    };
+
+#pragma unroll
+    for (int s = 0; s < STAGES; s++) issue(s);
+    if constexpr (PF) {
+        // Small tiles (a few MFMAs per k-step): a k-step's MFMAs cannot cover an LDS read, so every
+        // fragment of the next slice is read right after the barrier that publishes it, in flight
+        // under this slice's MFMAs, and the DMA sources of the slice after that are computed there
+        // too. Fragments double-buffer by slice parity (two slices per loop trip, constant indices).
+        half8 sa[2][KS][TI], sb[2][KS][TJ];
+        auto read_slice = [&](int gs, half8 (&fa)[KS][TI], half8 (&fb)[KS][TJ]) __attribute__((always_inline)) {
+            const unsigned char* st = smem + (gs % STAGES) * STAGE_BYTES;
+            static_for<0, KS>([&](auto ss) {
+                constexpr int k = decltype(ss)::value;
+                static_for<0, TJ>([&](auto jj) { fb[k][decltype(jj)::value] = *(const half8*)(st + b_off[k][decltype(jj)::value]); });
+                static_for<0, TI>([&](auto ii) { fa[k][decltype(ii)::value] = *(const half8*)(st + a_off[k][decltype(ii)::value]); });
+            });
+        };
+        Src nxt;
+        prep(STAGES, nxt);
+        wait_vmcnt<(STAGES - 1) * LOADS>();  // slice 0
+        __builtin_amdgcn_s_barrier();
+        init_acc(0);
+        read_slice(0, sa[0], sb[0]);
+        auto slice = [&](int gs, auto cc) __attribute__((always_inline)) {
+            constexpr int C = decltype(cc)::value, X = 1 - C;
+            // slice gs+1 landed and every read of slice gs is in registers, for all waves
+            wait_vmcnt<(STAGES - 2) * LOADS>();
+            wait_lgkmcnt0();
+            __builtin_amdgcn_s_barrier();
+            fire(gs + STAGES, nxt);  // into stage gs % STAGES
+            read_slice(gs + 1, sa[X], sb[X]);
+            __builtin_amdgcn_sched_barrier(0);
+            static_for<0, KS * TJ * TI>([&](auto kji) {
+                constexpr int k = decltype(kji)::value / (TJ * TI), j = (decltype(kji)::value / TI) % TJ,
+                              i = decltype(kji)::value % TI;
+                acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sb[C][k][j], sa[C][k][i], acc[j][i], 0, 0, 0);
+            });
+            prep(gs + STAGES + 1, nxt);
+            __builtin_amdgcn_sched_barrier(0);
+            if (gs % nk == nk - 1) {
+                wait_lgkmcnt0();  // init_acc reads LDS too
+                epilogue(gs);
+            }
+        };
+        for (int gs = 0; gs < total; gs += 2) {
+            slice(gs, std::integral_constant<int, 0>{});
+            if (gs + 1 < total) slice(gs + 1, std::integral_constant<int, 1>{});
+        }
+        wait_vmcnt<0>();
+        return;
+    }
+    wait_vmcnt<(STAGES - 1) * LOADS>();  // slice 0
+    __builtin_amdgcn_s_barrier();
+    init_acc(0);
+    read_step(0, 0, fa0, fb0);
+    for (int gs = 0; gs < total; gs++) {
+        static_for<0, KS>([&](auto step) {
+            constexpr int s = decltype(step)::value;
+            half8(&ca)[TI] = (s & 1) ? fa1 : fa0;
+            half8(&cb)[TJ] = (s & 1) ? fb1 : fb0;
+            half8(&na)[TI] = (s & 1) ? fa0 : fa1;
+            half8(&nb)[TJ] = (s & 1) ? fb0 : fb1;
+            if constexpr (s == KS - 1) {
+                // slice gs+1 landed (this wave's loads; later slices may stay in flight) and every read
+                // of slice gs done; after the barrier both hold for all waves
+                wait_vmcnt<(STAGES - 2) * LOADS>();
+                wait_lgkmcnt0();
+                __builtin_amdgcn_s_barrier();
+                issue(gs + STAGES);  // into stage gs % STAGES; may already be a later tile's slice
+                read_step(gs + 1, 0, na, nb);
+            } else {
+                read_step(gs, s + 1, na, nb);
+            }
+            static_for<0, TJ * TI>([&](auto ji) {
+                constexpr int j = decltype(ji)::value / TI, i = decltype(ji)::value % TI;
+                acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cb[j], ca[i], acc[j][i], 0, 0, 0);
+            });
+            // MFMA, read, MFMA, read, ...: this step's operands were read one step earlier, and the
+            // next step's reads issue while the matrix pipe works through this step
+            constexpr int RD = TI + TJ, MF = TI * TJ;
+            static_for<0, (RD < MF ? RD : MF)>([&](auto) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            });
+            if constexpr (MF > RD) __builtin_amdgcn_sched_group_barrier(0x008, MF - RD, 0);
+            if constexpr (RD > MF) __builtin_amdgcn_sched_group_barrier(0x100, RD - MF, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        wait_lgkmcnt0();  // next slice's first fragments (read before this slice's last MFMAs)
+        if (gs % nk == nk - 1) epilogue(gs);
+    }
+    wait_vmcnt<0>();  // the trailing (unused) slices land before the workgroup's LDS is released
+}
+
+#define SOX_GEMM(NAME, BM, BN, BK, WM, WN, ST, NW, OCC, GM)                                         \
+    extern "C" __global__ void __launch_bounds__(64 * NW, OCC) NAME(sox_igemm_args p) {           \
+        gemm_body<BM, BN, BK, WM, WN, ST, NW, GM>(p);                                             \
+    }
+#define SOX_CONV(NAME, BM, BN, BK, WM, WN, ST, NW, OCC, GM)                                         \
+    extern "C" __global__ void __launch_bounds__(64 * NW, OCC) NAME(sox_igemm_args p) {           \
+        gemm_body<BM, BN, BK, WM, WN, ST, NW, GM, true>(p);                                       \
+    }
+

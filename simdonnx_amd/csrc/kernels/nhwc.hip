@@ -238,43 +238,78 @@ extern "C" __global__ void __launch_bounds__(256) sox_convt_f16(sox_convt_args p
 extern "C" __global__ void __launch_bounds__(256) sox_convt_f32(sox_convt_args p) { convt_body<float>(p); }
 
 // Pixel-major ConvTranspose for kh*kw <= 4 taps (the 2x2 stride-2 DBNet head): one work item = one
-// input pixel x 8 output channels for ALL taps, so the pixel's ic channels are loaded once (8 at a
-// time, all in flight) and reused for every tap; the packed weights [tap][ic][oc] sit in LDS as
-// fp32 (host guarantees taps*ic*oc <= 16384) and are read as broadcasts. Output channels of one
-// tap are contiguous: 16-byte stores when oc % 8 == 0.
+// input pixel x 8 output channels for ALL taps, so the pixel's ic channels are loaded once and reused
+// for every tap; the packed weights [tap][ic][oc] sit in LDS as fp32 (host guarantees
+// taps*ic*oc <= 16384) and are read as broadcasts. When ic is a multiple of the 16-byte vector and
+// at most 8 vectors, the pixel's loads (and its bias) are all issued before the weights are staged,
+// so the kernel waits on memory once. Output channels of one tap are contiguous: 16-byte stores
+// when oc % 8 == 0.
 template <typename T>
 __device__ __forceinline__ void convt_pix_body(const sox_convt_args& p) {
     extern __shared__ float wl[];  // [tap][ic][oc]
+    typedef typename V16<T>::Vec Vec;
+    constexpr int VE = V16<T>::N;
     const int taps = p.kh * p.kw, nw = taps * p.ic * p.oc;
-    for (int i = threadIdx.x; i < nw; i += blockDim.x) wl[i] = to_f(((const T*)p.w)[i]);
-    __syncthreads();
     const int og_n = (p.oc + 7) / 8;
-    const long item = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (item >= (long)p.n * p.ih * p.iw * og_n) return;
+    const long items = (long)p.n * p.ih * p.iw * og_n;
+    const long item_raw = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long item = min(item_raw, items - 1);  // threads past the end still stage weights
     const int og = (int)(item % og_n);
     const long pix = item / og_n;
     const int o0 = og * 8, on = min(8, p.oc - o0);
+    const int nv = p.ic / VE;
+    const bool vec = p.ic % VE == 0 && nv <= 8;  // uniform
+    Vec xv[8];
+    if (vec) {
+        const Vec* __restrict__ xp = (const Vec*)((const T*)p.x + pix * p.ic);
+#pragma unroll
+        for (int u = 0; u < 8; u++) xv[u] = xp[min(u, nv - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; u++) keep_in_vgprs(xv[u]);
+    }
     float acc[4][8];
 #pragma unroll
     for (int o = 0; o < 8; o++) {
-        const float bv = (p.flags & SOX_F_BIAS) && o < on ? p.bias[o0 + o] : 0.0f;
+        const float bv = (p.flags & SOX_F_BIAS) ? p.bias[o0 + min(o, on - 1)] : 0.0f;
 #pragma unroll
-        for (int t = 0; t < 4; t++) acc[t][o] = bv;
+        for (int t = 0; t < 4; t++) acc[t][o] = o < on ? bv : 0.0f;
     }
-    const T* __restrict__ xp = (const T*)p.x + pix * p.ic;
-    for (int c0 = 0; c0 < p.ic; c0 += 8) {
-        float xv[8];
+    strided_foreach<8>((const T*)p.w, (long)threadIdx.x, (long)nw, (long)blockDim.x,
+                       [&](long i, T v) { wl[i] = to_f(v); });
+    __syncthreads();
+    if (item_raw >= items) return;
+    if (vec) {
 #pragma unroll
-        for (int e = 0; e < 8; e++) xv[e] = to_f(xp[min(c0 + e, p.ic - 1)]);
+        for (int u = 0; u < 8; u++) {
+            if (u >= nv) break;
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            if (c0 + e >= p.ic) break;
+            for (int e = 0; e < VE; e++) {
+                const float xe = to_f(xv[u][e]);
 #pragma unroll
-            for (int t = 0; t < 4; t++) {
-                if (t >= taps) break;
-                const float* wr = wl + ((long)t * p.ic + c0 + e) * p.oc + o0;
+                for (int t = 0; t < 4; t++) {
+                    if (t >= taps) break;
+                    const float* wr = wl + ((long)t * p.ic + u * VE + e) * p.oc + o0;
 #pragma unroll
-                for (int o = 0; o < 8; o++) acc[t][o] = __builtin_fmaf(xv[e], wr[o < on ? o : 0], acc[t][o]);
+                    for (int o = 0; o < 8; o++) acc[t][o] = __builtin_fmaf(xe, wr[o < on ? o : 0], acc[t][o]);
+                }
+            }
+        }
+    } else {
+        const T* __restrict__ xp = (const T*)p.x + pix * p.ic;
+        for (int c0 = 0; c0 < p.ic; c0 += 8) {
+            float xs[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) xs[e] = to_f(xp[min(c0 + e, p.ic - 1)]);
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                if (c0 + e >= p.ic) break;
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    if (t >= taps) break;
+                    const float* wr = wl + ((long)t * p.ic + c0 + e) * p.oc + o0;
+#pragma unroll
+                    for (int o = 0; o < 8; o++) acc[t][o] = __builtin_fmaf(xs[e], wr[o < on ? o : 0], acc[t][o]);
+                }
             }
         }
     }
@@ -373,42 +408,85 @@ extern "C" __global__ void __launch_bounds__(256) sox_gap_f32_s(sox_gap_args p) 
 // ------------------------------------------------------------------------------------------
 // SE gate (se_gate.comp; Kernels/Nhwc.Det.cs:287-314) as two passes over many workgroups.
 // ------------------------------------------------------------------------------------------
-// The SE weights are read once per inference, so they come from HBM/MALL: what costs is the number
-// of dependent memory round trips, not bytes. Each wave owns ONE output row (w1 [r][c] / w2 [c][r]
-// in their ONNX 1x1-conv layouts, contiguous), its lanes stride the row with independent loads and
-// a shuffle tree reduces: one round trip per pass. Four rows per 256-thread workgroup, as many
-// workgroups as rows.
+// The SE weights are read once per inference, so what costs is the number of dependent memory
+// round trips, not bytes. fc1 is split by channel groups so every GAP partial is read once: group g
+// reduces its 64 channels' partials (4 chunk phases per channel, one batch of loads each), then
+// 16 lanes x 4 channels cover the group's slice of four W1 rows per wave instruction, and a 16-lane
+// shuffle reduces each row.
+constexpr int SE_CG = 64;
 extern "C" __global__ void __launch_bounds__(256) sox_se_fc1(sox_se_args p) {
-    extern __shared__ float mean[];  // [c]
-    const int b = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const float inv = 1.0f / p.hw;
-    const float* part = p.part + (long)b * p.chunks * p.c;
-    for (int ch = t; ch < p.c; ch += blockDim.x) {
+    __shared__ float red[256];
+    __shared__ float mean[SE_CG];
+    const int g = blockIdx.x, b = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int c0 = g * SE_CG, cn = min(SE_CG, p.c - c0);
+    {
+        const int ch = t % SE_CG, ph = t / SE_CG;
         float acc = 0.0f;
-        strided_foreach<16>(part + ch, 0, (long)p.chunks * p.c, p.c, [&](long, float v) { acc += v; });
-        mean[ch] = acc * inv;
+        if (ch < cn)
+            strided_foreach<16>(p.part + (long)b * p.chunks * p.c + c0 + ch, (long)ph * p.c, (long)p.chunks * p.c,
+                                4L * p.c, [&](long, float v) { acc += v; });
+        red[t] = acc;
     }
     __syncthreads();
-    const int j = blockIdx.x * (blockDim.x >> 6) + wave;
-    if (j >= p.r) return;
-    float s = wave_sum(row_dot(p.w1 + (long)j * p.c, p.c, lane, [&](int k) { return mean[k]; }));
-    if (lane == 0) {
-        s += (p.flags & 1) ? p.b1[j] : 0.0f;
-        p.hid[(long)b * p.r + j] = (p.flags & 4) ? fmaxf(s, 0.0f) : s;
+    if (t < SE_CG) mean[t] = ((red[t] + red[t + 64]) + (red[t + 128] + red[t + 192])) * (1.0f / p.hw);
+    __syncthreads();
+    const int sub = lane & 15, rq = lane >> 4;  // channel quad, row within the wave's four
+    float m4[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) m4[e] = 4 * sub + e < cn ? mean[4 * sub + e] : 0.0f;  // 0: lane past the group
+    const bool vec = (p.c & 3) == 0;  // rows and groups start 16-byte aligned, cn % 4 == 0
+    float* hid = p.hid + ((long)b * p.groups + g) * p.r;
+    // four rows per wave instruction, four instructions' loads in flight (clamped, branch-free)
+    for (int j0 = wave * 4; j0 < p.r; j0 += 64) {
+        float s[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int j = min(j0 + 16 * u + rq, p.r - 1);
+            const float* w = p.w1 + (long)j * p.c + c0;
+            if (vec) {
+                const float4v v = *(const float4v*)(w + min(4 * sub, cn - 4));
+                s[u] = v[0] * m4[0] + v[1] * m4[1] + v[2] * m4[2] + v[3] * m4[3];
+            } else {
+                s[u] = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 4; e++) s[u] += w[min(4 * sub + e, cn - 1)] * m4[e];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1) s[u] += __shfl_xor(s[u], o, 64);
+            const int j = j0 + 16 * u + rq;
+            if (sub == 0 && j < p.r) hid[j] = s[u];
+        }
     }
 }
 
+// fc2: the workgroup rebuilds h from the groups' partials in LDS (fixed summation order), then one
+// wave per output channel.
 template <typename T>
 __device__ __forceinline__ void se_fc2_body(const sox_se_args& p) {
-    const int b = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    extern __shared__ float h[];  // [r]
+    const int b = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const float* part = p.hid + (long)b * p.groups * p.r;
+    for (int k = t; k < p.r; k += blockDim.x) {
+        float s = (p.flags & 1) ? p.b1[k] : 0.0f;
+        strided_foreach<16>(part + k, 0, (long)p.groups * p.r, p.r, [&](long, float v) { s += v; });
+        h[k] = (p.flags & 4) ? fmaxf(s, 0.0f) : s;
+    }
+    __syncthreads();
     const int ch = blockIdx.x * (blockDim.x >> 6) + wave;
     if (ch >= p.c) return;
-    const float* hid = p.hid + (long)b * p.r;
-    float z = wave_sum(row_dot(p.w2 + (long)ch * p.r, p.r, lane, [&](int k) { return hid[k]; }));
-    if (lane == 0) {
-        z += (p.flags & 2) ? p.b2[ch] : 0.0f;
-        const float g = (p.flags & 8) ? fminf(fmaxf(z * p.alpha + p.beta, 0.0f), 1.0f) : sox_sigmoid(z);
-        ((T*)p.s)[(long)b * p.c + ch] = (T)(g + p.offset);
+    float z = wave_sum(row_dot(p.w2 + (long)ch * p.r, p.r, lane, [&](int k) { return h[k]; }));
+    z += (p.flags & 2) ? p.b2[ch] : 0.0f;
+    const float gate = ((p.flags & 8) ? fminf(fmaxf(z * p.alpha + p.beta, 0.0f), 1.0f) : sox_sigmoid(z)) + p.offset;
+    if (p.flags & SOX_SE_FOLD) {
+        const T* __restrict__ ws = (const T*)p.wsrc;
+        T* __restrict__ wd = (T*)p.wdst;
+        strided_foreach<4>(ws + ch, (long)lane * p.wk, (long)p.wn * p.wk, 64L * p.wk,
+                           [&](long i, T v) { wd[ch + i] = (T)(to_f(v) * gate); });
+    } else if (lane == 0) {
+        ((T*)p.s)[(long)b * p.c + ch] = (T)gate;
     }
 }
 

@@ -52,9 +52,14 @@ def conv_plan(x, w, b, add, stride, pads, act, pad_mode, pad_value, group=1):
     return pb.build(y), ins
 
 
-@pytest.mark.parametrize("half", [False, True], ids=["f32", "f16"])
+@pytest.mark.parametrize("half,path", [(False, "default"), (True, "default"), (True, "igemm")],
+                         ids=["f32", "f16", "f16-igemm"])
 @pytest.mark.parametrize("i", range(int(G["conv_n"][0])))
-def test_conv_matches_oracle(hip, i, half):
+def test_conv_matches_oracle(hip, i, half, path, monkeypatch):
+    """Every golden conv case; fp16 through the default route (the LDS-DMA implicit-GEMM ring when
+    ic % 8 == 0) and through the register-staged implicit-GEMM kernel."""
+    if path == "igemm":
+        monkeypatch.setenv("SIMDONNX_HIP_IGEMM", "1")
     ic, oc, k, s, h, w, mode, act, res = [int(v) for v in G[f"conv{i}_meta"]]
     pv = float(G[f"conv{i}_pv"][0])
     cv = f16 if half else (lambda a: a)
@@ -69,7 +74,7 @@ def test_conv_matches_oracle(hip, i, half):
 
 @pytest.mark.parametrize("half", [False, True], ids=["f32", "f16"])
 @pytest.mark.parametrize("case", [(3, 16, 2, 64, 40), (64, 128, 1, 33, 29), (32, 96, 2, 30, 22), (8, 64, 2, 21, 17),
-                                  (128, 256, 1, 16, 16), (16, 160, 1, 24, 20)])
+                                  (128, 256, 1, 16, 16), (16, 160, 1, 24, 20), (64, 128, 1, 96, 96)])
 def test_conv_shapes_batch(hip, case, half):
     """conv_cm route coverage (VkKernelTests.ConvCm_MatchesCpu shapes): stems, stride 2, wide oc, batch 2."""
     ic, oc, s, h, w = case
@@ -109,9 +114,12 @@ def test_depthwise_matches_oracle(hip, i, half):
     assert max_rel(got, want) < TOL[half]
 
 
-@pytest.mark.parametrize("half", [False, True], ids=["f32", "f16"])
+@pytest.mark.parametrize("half,path", [(False, "direct"), (True, "gemm"), (True, "direct")],
+                         ids=["f32", "f16-gemm", "f16-direct"])
 @pytest.mark.parametrize("i", range(int(G["ct_n"][0])))
-def test_conv_transpose_matches_oracle(hip, i, half):
+def test_conv_transpose_matches_oracle(hip, i, half, path, monkeypatch):
+    if path == "direct":
+        monkeypatch.setenv("SIMDONNX_HIP_CONVT_DIRECT", "1")
     ic, oc, k, h, w, act = [int(v) for v in G[f"ct{i}_meta"]]
     cv = f16 if half else (lambda a: a)
     x, wt, b = cv(G[f"ct{i}_x"]), cv(G[f"ct{i}_w"]), G[f"ct{i}_b"]
@@ -120,6 +128,47 @@ def test_conv_transpose_matches_oracle(hip, i, half):
     y = pb.conv_transpose(xv, wt, b, act=ACTS[act], name="convt")
     got = run(hip, pb.build(y), [x], half)
     want = O.conv_transpose(x, wt, b, act=ACTS[act])
+    assert max_rel(got, want) < TOL[half]
+
+
+# (batch, ic, oc, k, h, w, act): ConvTranspose (stride == kernel) shapes beyond the fixtures
+CONVT_SHAPES = [(2, 32, 16, 3, 7, 5, "relu"), (1, 16, 5, 2, 33, 17, "sigmoid"), (1, 64, 96, 2, 13, 11, "none")]
+
+
+@pytest.mark.parametrize("half", [False, True], ids=["f32", "f16"])
+@pytest.mark.parametrize("case", CONVT_SHAPES, ids=lambda c: "x".join(str(v) for v in c))
+def test_conv_transpose_shapes(hip, case, half):
+    n, ic, oc, k, h, w, act = case
+    cv = f16 if half else (lambda a: a)
+    x = cv(synth.uniform(12, 1, (n, h, w, ic), -1, 1))
+    wt = cv(synth.normal(12, 2, (ic, oc, k, k), 0.2))
+    b = synth.uniform(12, 3, (oc,), -0.2, 0.2)
+    pb = PlanBuilder()
+    xv = pb.input((n, ic, h, w), NHWC, "x")
+    y = pb.conv_transpose(xv, wt, b, act=act, name="convt")
+    got = run(hip, pb.build(y), [x], half)
+    assert max_rel(got, O.conv_transpose(x, wt, b, act=act)) < TOL[half]
+
+
+@pytest.mark.parametrize("half", [False, True], ids=["f32", "f16"])
+def test_conv_transpose_then_channel_affine(hip, half):
+    """ConvTranspose -> per-channel Mul -> per-channel Add + ReLU (an unfolded BatchNormalization)."""
+    cv = f16 if half else (lambda a: a)
+    ic, oc, h, w = 24, 24, 15, 13
+    x = cv(synth.uniform(13, 1, (1, h, w, ic), -1, 1))
+    wt = cv(synth.normal(13, 2, (ic, oc, 2, 2), 0.2))
+    b = synth.uniform(13, 3, (oc,), -0.2, 0.2)
+    s_, t_ = synth.uniform(13, 4, (oc, 1, 1), 0.5, 1.5), synth.uniform(13, 5, (oc, 1, 1), -0.3, 0.3)
+    pb = PlanBuilder()
+    xv = pb.input((1, ic, h, w), NHWC, "x")
+    hv = pb.conv_transpose(xv, wt, b, name="convt")
+    hv = pb.ew(hv, pb.const(s_, "bn_scale"), 2, name="bn_mul")
+    y = pb.ew(hv, pb.const(t_, "bn_shift"), 0, act="relu", name="bn_add")
+    got = run(hip, pb.build(y), [x], half)
+    ref = O.conv_transpose(x, wt, b)
+    if half:
+        ref = f16(ref)
+    want = np.maximum(ref * s_.reshape(-1) + t_.reshape(-1), 0.0)
     assert max_rel(got, want) < TOL[half]
 
 
@@ -136,6 +185,38 @@ def test_se_block_matches_oracle(hip, half):
     got = run(hip, pb.build(y), [x], half)
     s = O.channel_gate(x, G["se_w1"], G["se_b1"], G["se_w2"], G["se_b2"])
     want = x * s[:, None, None, :]
+    assert max_rel(got, want) < TOL[half]
+
+
+# (batch, c, r, h, w, out, residual): one image with c % 8 == 0 folds the gate into the projection's
+# weights; two images, or c % 8 != 0, keep the broadcast multiply
+SE_PROJ = [(1, 96, 24, 9, 11, 40, False), (1, 576, 144, 5, 7, 96, True), (1, 16, 8, 33, 31, 16, True),
+           (2, 96, 24, 9, 11, 40, False), (1, 36, 12, 6, 5, 24, False)]
+
+
+@pytest.mark.parametrize("half", [False, True], ids=["f32", "f16"])
+@pytest.mark.parametrize("case", SE_PROJ, ids=lambda c: "x".join(str(int(v)) for v in c))
+def test_se_then_projection(hip, case, half):
+    """ChannelGate -> x * gate -> 1x1 conv (+ residual), the MobileNetV3 block tail."""
+    n, c, r, h, w, out, res = case
+    cv = f16 if half else (lambda a: a)
+    x = cv(synth.uniform(11, c, (n, h, w, c), -1, 1))
+    w1 = synth.normal(11, 2, (r, c, 1, 1), 0.2)
+    w2 = synth.normal(11, 3, (c, r, 1, 1), 0.2)
+    b1, b2 = synth.uniform(11, 4, (r,), -0.1, 0.1), synth.uniform(11, 5, (c,), -0.1, 0.1)
+    wp = cv(synth.normal(11, 6, (out, c, 1, 1), 0.1))
+    bp = synth.uniform(11, 7, (out,), -0.1, 0.1)
+    add = cv(synth.uniform(11, 8, (n, h, w, out), -1, 1)) if res else None
+    pb = PlanBuilder()
+    xv = pb.input((n, c, h, w), NHWC, "x")
+    av = pb.input((n, out, h, w), NHWC, "add") if res else None
+    gate = pb.channel_gate(xv, w1, b1, w2, b2, act1="relu", hard=True, alpha=1.0 / 6.0, beta=0.5, name="se")
+    hv = pb.mul(xv, gate, name="se_scale")
+    y = pb.conv(hv, wp, bp, stride=1, pad=0, add=av, name="project")
+    got = run(hip, pb.build(y), [x, add] if res else [x], half)
+    s = O.channel_gate(x, w1.reshape(r, c), b1, w2.reshape(c, r), b2)
+    scaled = cv(x * s[:, None, None, :])
+    want = O.conv(scaled, wp, bp, add)
     assert max_rel(got, want) < TOL[half]
 
 
