@@ -1,0 +1,151 @@
+// Direct KH x KW convolution (stride SH x SW, zero padding) from an LDS halo tile on CDNA4 matrix
+// cores: the fp16 Conv2d route (conv_cm.comp, Backends/Vulkan/VkGraph.cs:555-703) for convs with few
+// output channels, whose implicit-GEMM form would fetch every input pixel kh*kw times.
+//  * A workgroup owns a TH x TW tile of output pixels x 32 output channels. Per block of CB input
+//    channels it copies the tile's input halo ((TH-1)SH+KH x (TW-1)SW+KW pixels) and the block's
+//    weights [tap][32 n] into LDS with global_load_lds (padding pixels, channel tails and absent
+//    output channels read p.zeros), double-buffered: block c+1 loads while block c multiplies.
+//  * Halo pixels and weight rows are PITCH = 5 sixteen-byte slots apart (4 channel chunks + 1 pad
+//    slot): 8 consecutive pixels then fall on 8 distinct 16-byte bank groups with no swizzle, so a
+//    tap's fragment is the lane's base address + a compile-time offset.
+//  * Each wave takes 2 output rows (32 pixels) x 32 channels: per tap and 16-channel k-step one
+//    v_mfma_f32_32x32x16_f16 (weights as the row operand, pixels as the column operand: lane l ends
+//    with pixel l % 32 and channels 8q + 4(l/32) + e in accumulator 4q + e, as in the Gemm ring).
+//  * Epilogue: bias (in the accumulators from the start), residual, activation, 8-byte stores with
+//    row stride ldy (a concat slice works).
+// Every DMA lane writes a slot (the regions are padded to whole instructions), so every wave issues
+// the same number of loads per block and one static vmcnt covers them.
+#include "gemm_ring.h"
+
+template <int KH, int KW, int SH, int SW>
+__device__ __forceinline__ void halo_body(const sox_igemm_args& p) {
+    constexpr int TW = 16, TH = 8, CB = 32, PITCH = 5;
+    constexpr int HW = (TW - 1) * SW + KW, HH = (TH - 1) * SH + KH, HP = HH * HW, TAPS = KH * KW;
+    constexpr int HALO_IT = (HP * PITCH + 255) / 256, W_IT = (TAPS * 32 * PITCH + 255) / 256;
+    constexpr int HALO_SLOTS = HALO_IT * 256, W_SLOTS = W_IT * 256, STAGE = HALO_SLOTS + W_SLOTS;
+    constexpr int LOADS = HALO_IT + W_IT;
+    static_assert(2 * STAGE * 16 <= 160 * 1024, "two stages fit the LDS");
+    static_assert(LOADS < 32, "vmcnt range");
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * STAGE * 16];
+
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, l32 = lane & 31, hl = lane >> 5;
+    const int M = p.m, N = p.n;
+    const int tiles_x = (p.ow + TW - 1) / TW, tiles_y = (p.oh + TH - 1) / TH;
+    const int tx = blockIdx.x % tiles_x, tyb = blockIdx.x / tiles_x;
+    const int ty = tyb % tiles_y, b = tyb / tiles_y;
+    const int n0 = blockIdx.y * 32;
+    const int oy0 = ty * TH, ox0 = tx * TW;
+    const int iy0 = oy0 * SH - p.pt, ix0 = ox0 * SW - p.pl;
+    const half_t* __restrict__ X = (const half_t*)p.x + (long)b * p.ih * p.iw * p.ic;
+    const half_t* __restrict__ W = (const half_t*)p.w;
+    const half_t* __restrict__ Z = (const half_t*)p.zeros;
+    const int ncb = (p.ic + CB - 1) / CB;
+
+    // this thread's DMA sources in channel block 0 (nullptr: the slot is padding and reads zeros);
+    // block c adds c * CB channels, and a chunk past ic reads zeros too
+    const half_t* hsrc[HALO_IT];
+    int hch[HALO_IT];
+#pragma unroll
+    for (int i = 0; i < HALO_IT; i++) {
+        const int q = i * 256 + t, hp = q / PITCH, sub = q - hp * PITCH;
+        const int hy = hp / HW, hx = hp - hy * HW, iy = iy0 + hy, ix = ix0 + hx;
+        const bool ok = q < HP * PITCH && sub < 4 && (unsigned)iy < (unsigned)p.ih && (unsigned)ix < (unsigned)p.iw;
+        hsrc[i] = ok ? X + ((long)iy * p.iw + ix) * p.ic + sub * 8 : nullptr;
+        hch[i] = sub * 8;
+    }
+    const half_t* wsrc[W_IT];
+    int wch[W_IT];
+#pragma unroll
+    for (int i = 0; i < W_IT; i++) {
+        const int q = i * 256 + t, row = q / PITCH, sub = q - row * PITCH;
+        const int tap = row / 32, n = row - tap * 32;
+        const bool ok = q < TAPS * 32 * PITCH && sub < 4 && n0 + n < N;
+        wsrc[i] = ok ? W + (long)(n0 + n) * p.kpad + tap * p.ic + sub * 8 : nullptr;
+        wch[i] = sub * 8;
+    }
+    auto issue = [&](int cb, int stage) __attribute__((always_inline)) {
+        unsigned char* st = smem + stage * STAGE * 16 + wave * 64 * 16;
+        const int c0 = cb * CB;
+#pragma unroll
+        for (int i = 0; i < HALO_IT; i++) {
+            const half_t* src = hsrc[i] && c0 + hch[i] < p.ic ? hsrc[i] + c0 : Z;
+            __builtin_amdgcn_global_load_lds(src, LDS_PTR(st + i * 256 * 16), 16, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < W_IT; i++) {
+            const half_t* src = wsrc[i] && c0 + wch[i] < p.ic ? wsrc[i] + c0 : Z;
+            __builtin_amdgcn_global_load_lds(src, LDS_PTR(st + (HALO_SLOTS + i * 256) * 16), 16, 0, 0);
+        }
+    };
+
+    // lane's output pixel (row 2 wave + l32 / 16, column l32 % 16 of the tile) and fragment bases
+    const int py = 2 * wave + (l32 >> 4), px = l32 & 15;
+    const int a_base = ((py * SH * HW + px * SW) * PITCH + hl) * 16;
+    const int b_base = (HALO_SLOTS + l32 * PITCH + hl) * 16;
+
+    float16v acc;
+    const bool has_bias = (p.flags & SOX_F_BIAS) != 0;
+    static_for<0, 16>([&](auto qe) {
+        constexpr int q = decltype(qe)::value / 4, e = decltype(qe)::value % 4;
+        const int n = n0 + 8 * q + 4 * hl + e;
+        acc[decltype(qe)::value] = has_bias && n < N ? p.bias[n] : 0.0f;
+    });
+
+    issue(0, 0);
+    for (int cb = 0; cb < ncb; cb++) {
+        issue(cb + 1, (cb + 1) & 1);  // past the last block: zeros into the idle stage, never read
+        wait_vmcnt<LOADS>();          // this wave's block cb landed
+        __builtin_amdgcn_s_barrier();  // ... and every wave's
+        const unsigned char* st = smem + (cb & 1) * STAGE * 16;
+        static_for<0, TAPS * 2>([&](auto ts) {
+            constexpr int tap = decltype(ts)::value / 2, s = decltype(ts)::value % 2;
+            constexpr int a_off = (((tap / KW) * HW + tap % KW) * PITCH + 2 * s) * 16;
+            constexpr int b_off = (tap * 32 * PITCH + 2 * s) * 16;
+            const half8 wf = *(const half8*)(st + b_base + b_off);
+            const half8 af = *(const half8*)(st + a_base + a_off);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf, af, acc, 0, 0, 0);
+        });
+        wait_lgkmcnt0();
+        __builtin_amdgcn_s_barrier();  // stage cb & 1 is refilled by the next iteration's issue
+    }
+    wait_vmcnt<0>();
+
+    const int oy = oy0 + py, ox = ox0 + px;
+    if (oy >= p.oh || ox >= p.ow) return;
+    const long m = ((long)b * p.oh + oy) * p.ow + ox;
+    if (m >= M) return;
+    const int act = (p.flags & SOX_F_ACT_MASK) >> SOX_F_ACT_SHIFT;
+    const half_t* __restrict__ R = (p.flags & SOX_F_RESIDUAL) ? (const half_t*)p.add : nullptr;
+    half_t* __restrict__ Y = (half_t*)p.y + m * p.ldy;
+    const bool aligned = ((p.ldy | N) & 3) == 0;
+    static_for<0, 4>([&](auto qq) {
+        constexpr int q = decltype(qq)::value;
+        const int n = n0 + 8 * q + 4 * hl;
+        if (n >= N) return;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            v[e] = acc[4 * q + e];
+            if (R && n + e < N) v[e] += (float)R[m * p.ldy + n + e];
+            v[e] = act_fast(v[e], act);
+        }
+        if (aligned) {
+            half4 h;
+#pragma unroll
+            for (int e = 0; e < 4; e++) h[e] = (half_t)v[e];
+            *(half4*)(Y + n) = h;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (n + e < N) Y[n + e] = (half_t)v[e];
+        }
+    });
+}
+
+#define SOX_HALO(NAME, KH, KW, SH, SW, OCC)                                                       \
+    extern "C" __global__ void __launch_bounds__(256, OCC) NAME(sox_igemm_args p) {            \
+        halo_body<KH, KW, SH, SW>(p);                                                          \
+    }
+
+SOX_HALO(sox_conv_halo_f16_3x3s1, 3, 3, 1, 1, 2)
+SOX_HALO(sox_conv_halo_f16_3x3s2, 3, 3, 2, 2, 1)

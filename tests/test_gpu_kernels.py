@@ -52,14 +52,17 @@ def conv_plan(x, w, b, add, stride, pads, act, pad_mode, pad_value, group=1):
     return pb.build(y), ins
 
 
-@pytest.mark.parametrize("half,path", [(False, "default"), (True, "default"), (True, "igemm")],
-                         ids=["f32", "f16", "f16-igemm"])
+@pytest.mark.parametrize("half,path", [(False, "default"), (True, "default"), (True, "ring"), (True, "igemm")],
+                         ids=["f32", "f16", "f16-ring", "f16-igemm"])
 @pytest.mark.parametrize("i", range(int(G["conv_n"][0])))
 def test_conv_matches_oracle(hip, i, half, path, monkeypatch):
-    """Every golden conv case; fp16 through the default route (the LDS-DMA implicit-GEMM ring when
-    ic % 8 == 0) and through the register-staged implicit-GEMM kernel."""
+    """Every golden conv case; fp16 through the default route (the LDS halo kernel for 3x3 convs with
+    few output channels, else the LDS-DMA implicit-GEMM ring when ic % 8 == 0), through the ring
+    alone and through the register-staged implicit-GEMM kernel."""
     if path == "igemm":
         monkeypatch.setenv("SIMDONNX_HIP_IGEMM", "1")
+    if path == "ring":
+        monkeypatch.setenv("SIMDONNX_HIP_NOHALO", "1")
     ic, oc, k, s, h, w, mode, act, res = [int(v) for v in G[f"conv{i}_meta"]]
     pv = float(G[f"conv{i}_pv"][0])
     cv = f16 if half else (lambda a: a)
@@ -186,6 +189,27 @@ def test_se_block_matches_oracle(hip, half):
     s = O.channel_gate(x, G["se_w1"], G["se_b1"], G["se_w2"], G["se_b2"])
     want = x * s[:, None, None, :]
     assert max_rel(got, want) < TOL[half]
+
+
+# (batch, ic, oc, stride, h, w, act, residual): 3x3 zero-padded convs on the halo route, with tile,
+# output-channel and input-channel-block tails
+HALO_CASES = [(1, 96, 24, 1, 30, 30, "none", False), (2, 40, 40, 1, 17, 35, "relu", True),
+              (1, 32, 64, 2, 33, 47, "hardswish", False), (1, 8, 16, 1, 9, 8, "gelu", True),
+              (1, 64, 72, 1, 12, 20, "none", False)]
+
+
+@pytest.mark.parametrize("case", HALO_CASES, ids=lambda c: "x".join(str(v) for v in c))
+def test_conv_halo_route(hip, case):
+    n, ic, oc, s, h, w, act, res = case
+    x = f16(synth.uniform(14, 1, (n, h, w, ic), -1, 1))
+    wt = f16(synth.normal(14, 2, (oc, ic, 3, 3), 0.1))
+    b = synth.uniform(14, 3, (oc,), -0.2, 0.2)
+    oh, ow = (h + 2 - 3) // s + 1, (w + 2 - 3) // s + 1
+    add = f16(synth.uniform(14, 4, (n, oh, ow, oc), -1, 1)) if res else None
+    plan, ins = conv_plan(x, wt, b, add, (s, s), (1, 1, 1, 1), act, 0, 0.0)
+    got = run(hip, plan, ins, True)
+    want = O.conv(x, wt, b, add, stride=(s, s), pads=(1, 1, 1, 1), act=act)
+    assert max_rel(got, want) < TOL[True]
 
 
 # (batch, c, r, h, w, out, residual): one image with c % 8 == 0 folds the gate into the projection's
