@@ -414,11 +414,27 @@ extern "C" __global__ void __launch_bounds__(256) sox_gap_f32_s(sox_gap_args p) 
 // 16 lanes x 4 channels cover the group's slice of four W1 rows per wave instruction, and a 16-lane
 // shuffle reduces each row.
 constexpr int SE_CG = 64;
+constexpr int SE_FC1_U = 16;  // W1 rows prefetched per lane: r <= 16 * SE_FC1_U takes the one-round-trip path
 extern "C" __global__ void __launch_bounds__(256) sox_se_fc1(sox_se_args p) {
     __shared__ float red[256];
     __shared__ float mean[SE_CG];
     const int g = blockIdx.x, b = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int c0 = g * SE_CG, cn = min(SE_CG, p.c - c0);
+    const int sub = lane & 15, rq = lane >> 4;  // channel quad, row within the wave's four
+    const bool vec = (p.c & 3) == 0;            // rows and groups start 16-byte aligned, cn % 4 == 0
+    const bool pre = vec && p.r <= 16 * SE_FC1_U;
+    // the group's W1 slice does not depend on the mean: its loads go out first, with the partials'
+    // (rows wave*4 + rq + 16u, clamped; this lane's quad of channels)
+    float4v wv[SE_FC1_U];
+    if (pre) {
+#pragma unroll
+        for (int u = 0; u < SE_FC1_U; u++) {
+            const int j = min(wave * 4 + rq + 16 * u, p.r - 1);
+            wv[u] = *(const float4v*)(p.w1 + (long)j * p.c + c0 + min(4 * sub, cn - 4));
+        }
+#pragma unroll
+        for (int u = 0; u < SE_FC1_U; u++) keep_in_vgprs(wv[u]);
+    }
     {
         const int ch = t % SE_CG, ph = t / SE_CG;
         float acc = 0.0f;
@@ -430,12 +446,22 @@ extern "C" __global__ void __launch_bounds__(256) sox_se_fc1(sox_se_args p) {
     __syncthreads();
     if (t < SE_CG) mean[t] = ((red[t] + red[t + 64]) + (red[t + 128] + red[t + 192])) * (1.0f / p.hw);
     __syncthreads();
-    const int sub = lane & 15, rq = lane >> 4;  // channel quad, row within the wave's four
     float m4[4];
 #pragma unroll
     for (int e = 0; e < 4; e++) m4[e] = 4 * sub + e < cn ? mean[4 * sub + e] : 0.0f;  // 0: lane past the group
-    const bool vec = (p.c & 3) == 0;  // rows and groups start 16-byte aligned, cn % 4 == 0
     float* hid = p.hid + ((long)b * p.groups + g) * p.r;
+    if (pre) {
+#pragma unroll
+        for (int u = 0; u < SE_FC1_U; u++) {
+            const int j = wave * 4 + rq + 16 * u;
+            if (wave * 4 + 16 * u >= p.r) break;  // uniform
+            float s = wv[u][0] * m4[0] + wv[u][1] * m4[1] + wv[u][2] * m4[2] + wv[u][3] * m4[3];
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+            if (sub == 0 && j < p.r) hid[j] = s;
+        }
+        return;
+    }
     // four rows per wave instruction, four instructions' loads in flight (clamped, branch-free)
     for (int j0 = wave * 4; j0 < p.r; j0 += 64) {
         float s[4];
@@ -463,11 +489,30 @@ extern "C" __global__ void __launch_bounds__(256) sox_se_fc1(sox_se_args p) {
 }
 
 // fc2: the workgroup rebuilds h from the groups' partials in LDS (fixed summation order), then one
-// wave per output channel.
+// wave per output channel. The wave's W2 row and, when folding, its column of the consumer's weights
+// (r, wn <= 256: four per lane) are loaded before h is gathered, so the kernel waits on memory once.
 template <typename T>
 __device__ __forceinline__ void se_fc2_body(const sox_se_args& p) {
     extern __shared__ float h[];  // [r]
     const int b = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int ch = blockIdx.x * (blockDim.x >> 6) + wave, chc = min(ch, p.c - 1);
+    const bool fold = (p.flags & SOX_SE_FOLD) != 0;
+    const bool pre = p.r <= 256 && (!fold || p.wn <= 256);
+    const T* __restrict__ ws = (const T*)p.wsrc;
+    float w2v[4];
+    T wsv[4];
+    if (pre) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) w2v[u] = p.w2[(long)chc * p.r + min(lane + 64 * u, p.r - 1)];
+        if (fold) {
+#pragma unroll
+            for (int u = 0; u < 4; u++) wsv[u] = ws[(long)min(lane + 64 * u, p.wn - 1) * p.wk + chc];
+#pragma unroll
+            for (int u = 0; u < 4; u++) keep_in_vgprs(wsv[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) keep_in_vgprs(w2v[u]);
+    }
     const float* part = p.hid + (long)b * p.groups * p.r;
     for (int k = t; k < p.r; k += blockDim.x) {
         float s = (p.flags & 1) ? p.b1[k] : 0.0f;
@@ -475,16 +520,31 @@ __device__ __forceinline__ void se_fc2_body(const sox_se_args& p) {
         h[k] = (p.flags & 4) ? fmaxf(s, 0.0f) : s;
     }
     __syncthreads();
-    const int ch = blockIdx.x * (blockDim.x >> 6) + wave;
     if (ch >= p.c) return;
-    float z = wave_sum(row_dot(p.w2 + (long)ch * p.r, p.r, lane, [&](int k) { return h[k]; }));
+    float z;
+    if (pre) {
+        z = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            if (lane + 64 * u < p.r) z = __builtin_fmaf(w2v[u], h[lane + 64 * u], z);
+        z = wave_sum(z);
+    } else {
+        z = wave_sum(row_dot(p.w2 + (long)ch * p.r, p.r, lane, [&](int k) { return h[k]; }));
+    }
     z += (p.flags & 2) ? p.b2[ch] : 0.0f;
     const float gate = ((p.flags & 8) ? fminf(fmaxf(z * p.alpha + p.beta, 0.0f), 1.0f) : sox_sigmoid(z)) + p.offset;
-    if (p.flags & SOX_SE_FOLD) {
-        const T* __restrict__ ws = (const T*)p.wsrc;
+    if (fold) {
         T* __restrict__ wd = (T*)p.wdst;
-        strided_foreach<4>(ws + ch, (long)lane * p.wk, (long)p.wn * p.wk, 64L * p.wk,
-                           [&](long i, T v) { wd[ch + i] = (T)(to_f(v) * gate); });
+        if (pre) {
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int n = lane + 64 * u;
+                if (n < p.wn) wd[(long)n * p.wk + ch] = (T)(to_f(wsv[u]) * gate);
+            }
+        } else {
+            strided_foreach<4>(ws + ch, (long)lane * p.wk, (long)p.wn * p.wk, 64L * p.wk,
+                               [&](long i, T v) { wd[ch + i] = (T)(to_f(v) * gate); });
+        }
     } else if (lane == 0) {
         ((T*)p.s)[(long)b * p.c + ch] = (T)gate;
     }
