@@ -391,13 +391,17 @@ __device__ __forceinline__ void gap_body(const sox_gap_args& p) {
     }
 #pragma unroll
     for (int e = 0; e < CV; e++) red[t * CV + e] = acc[e];
-    __syncthreads();
-    for (int ch = t; ch < p.c; ch += 256) {
-        int gg = ch / CV, e = ch - gg * CV;
-        float s = 0.0f;
-        for (int q = 0; q < P && q * cg + gg < 256; q++) s += red[(q * cg + gg) * CV + e];
-        p.part[((long)b * p.chunks + chunk) * p.c + ch] = s;
+    // the P phases of each channel vector fold in a fixed binary tree (log2 P steps; a serial loop
+    // over P = 256 / cg phases is long for few channels)
+    for (int st = 1; st < P; st *= 2) {
+        __syncthreads();
+        if (t < cg * P && ph % (2 * st) == 0 && ph + st < P) {
+#pragma unroll
+            for (int e = 0; e < CV; e++) red[t * CV + e] += red[(t + st * cg) * CV + e];
+        }
     }
+    __syncthreads();
+    for (int ch = t; ch < p.c; ch += 256) p.part[((long)b * p.chunks + chunk) * p.c + ch] = red[ch];
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_gap_f16_v(sox_gap_args p) { gap_body<half_t, 8>(p); }
