@@ -148,4 +148,3 @@ __device__ __forceinline__ void halo_body(const sox_igemm_args& p) {
     }
 
 SOX_HALO(sox_conv_halo_f16_3x3s1, 3, 3, 1, 1, 2)
-SOX_HALO(sox_conv_halo_f16_3x3s2, 3, 3, 2, 2, 1)

@@ -191,8 +191,8 @@ def test_se_block_matches_oracle(hip, half):
     assert max_rel(got, want) < TOL[half]
 
 
-# (batch, ic, oc, stride, h, w, act, residual): 3x3 zero-padded convs on the halo route, with tile,
-# output-channel and input-channel-block tails
+# (batch, ic, oc, stride, h, w, act, residual): 3x3 zero-padded convs on the halo route (stride 1),
+# with tile, output-channel and input-channel-block tails; the stride-2 case takes the ring
 HALO_CASES = [(1, 96, 24, 1, 30, 30, "none", False), (2, 40, 40, 1, 17, 35, "relu", True),
               (1, 32, 64, 2, 33, 47, "hardswish", False), (1, 8, 16, 1, 9, 8, "gelu", True),
               (1, 64, 72, 1, 12, 20, "none", False)]
