@@ -64,3 +64,47 @@ def test_code_objects_embedded_for_gfx950():
     syms = subprocess.run(["nm", "-D", N.BACKEND_PATH], capture_output=True, text=True).stdout
     for s in srcs:
         assert f"sox_res_{s}_start" in syms
+
+
+def _kernel_descriptors(path):
+    """(name, 64-byte kernel descriptor) of every `<kernel>.kd` symbol in a gfx950 code object (ELF64)."""
+    import struct
+    data = open(path, "rb").read()
+    shoff = struct.unpack_from("<Q", data, 0x28)[0]
+    shentsize, shnum = struct.unpack_from("<HH", data, 0x3A)
+    secs = [struct.unpack_from("<IIQQQQIIQQ", data, shoff + i * shentsize) for i in range(shnum)]
+    out = {}
+    for sec in secs:
+        if sec[1] != 2:  # SHT_SYMTAB
+            continue
+        strtab = secs[sec[6]]
+        for i in range(sec[5] // 24):
+            st_name, _, _, st_shndx, st_value, _ = struct.unpack_from("<IBBHQQ", data, sec[4] + i * 24)
+            end = data.index(b"\0", strtab[4] + st_name)
+            name = data[strtab[4] + st_name:end].decode()
+            if name.endswith(".kd") and st_shndx < len(secs):
+                home = secs[st_shndx]
+                off = home[4] + (st_value - home[3])
+                out[name[:-3]] = data[off:off + 64]
+    return out
+
+
+def test_kernels_use_no_scratch():
+    """No built kernel spills to scratch (private segment 0): the ring kernels index their accumulators
+    with constants only, and a spill there costs ~15% (it happened once when a lambda was not inlined)."""
+    import glob
+    import struct
+    build = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "simdonnx_amd", "_build")
+    objs = sorted(glob.glob(os.path.join(build, "*.hsaco")))
+    if not objs:
+        pytest.skip("code objects not built")
+    spills = {}
+    count = 0
+    for path in objs:
+        for name, kd in _kernel_descriptors(path).items():
+            count += 1
+            private = struct.unpack_from("<I", kd, 4)[0]  # private_segment_fixed_size
+            if private:
+                spills[name] = private
+    assert count > 50
+    assert not spills, spills
