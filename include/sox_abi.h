@@ -29,6 +29,8 @@ enum sox_act { SOX_ACT_NONE = 0, SOX_ACT_RELU = 1, SOX_ACT_SIGMOID = 2, SOX_ACT_
 #define SOX_F_ACT_SHIFT 4
 #define SOX_F_ACT_MASK 0xF0
 #define SOX_F_DENSE_A 0x100 /* A is a plain row-major [M][lda] matrix (Gemm), not an NHWC image */
+#define SOX_F_PAD_ROWS 0x400 /* LDS-DMA Gemm: output rows are padded to ldy >= N rounded up to 4, so the N tail
+                                 is stored as whole 4-element groups (the pad columns take junk) */
 #define SOX_F_CONVT 0x200   /* LDS-DMA conv kernels: column n = tap * ct_oc + o of input pixel m is
                                ConvTranspose output (y * ct_kh + dy, x * ct_kw + dx, o), tap = dy * ct_kw + dx */
 
@@ -197,6 +199,8 @@ typedef struct sox_softmax_args {
     int64_t rows;
     int32_t len;
     int32_t staged; /* 1: the row is kept in dynamic LDS (len floats, granted at launch) */
+    int32_t ldx;    /* input row stride in elements (>= len; the output rows are dense) */
+    int32_t pad_;
 } sox_softmax_args;
 
 /*

@@ -84,9 +84,11 @@ struct ConvtOut {
 
 template <int ACT, int TJ, int TI>
 SOX_DEV void store_tile(half_t* __restrict__ Y, const half_t* __restrict__ R, int ldy, int M, int N, int m0, int n0,
-                        const float16v (&acc)[TJ][TI], int act = 0, bool convt = false, ConvtOut ctv = {}) {
+                        const float16v (&acc)[TJ][TI], int act = 0, bool convt = false, ConvtOut ctv = {},
+                        bool pad_rows = false) {
     const int lane = threadIdx.x & 63, l32 = lane & 31, hl = lane >> 5;
-    const bool aligned = ((ldy | N) & 3) == 0;
+    // whole 4-element groups: rows of a multiple of 4 elements, or rows padded past the N tail
+    const bool aligned = pad_rows ? (ldy & 3) == 0 : ((ldy | N) & 3) == 0;
     if (convt) {  // uniform: ConvTranspose output, no residual
         const ConvtOut* ct = &ctv;
         auto fin = [&](float a) { return ACT == SOX_ACT_GELU ? gelu_fast(a) : ACT >= 0 ? sox_act(a, ACT) : act_fast(a, act); };
@@ -396,13 +398,14 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
 
     const ConvtOut cto{p.ih, p.iw, p.ct_kh, p.ct_kw, p.ct_oc, (p.flags & SOX_F_BIAS) ? p.bias : nullptr};
     const bool ctp = CONV && (p.flags & SOX_F_CONVT);
+    const bool pad_rows = (p.flags & SOX_F_PAD_ROWS) != 0;
     auto epilogue = [&](int gs) __attribute__((always_inline)) {
         // ---- epilogue from registers (the next tile's first slices are already loading) ----
         switch (act) {
-        case SOX_ACT_NONE: store_tile<SOX_ACT_NONE>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, ctp, cto); break;
-        case SOX_ACT_RELU: store_tile<SOX_ACT_RELU>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, ctp, cto); break;
-        case SOX_ACT_GELU: store_tile<SOX_ACT_GELU>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, ctp, cto); break;
-        default: store_tile<-1>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, act, ctp, cto); break;
+        case SOX_ACT_NONE: store_tile<SOX_ACT_NONE>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, ctp, cto, pad_rows); break;
+        case SOX_ACT_RELU: store_tile<SOX_ACT_RELU>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, ctp, cto, pad_rows); break;
+        case SOX_ACT_GELU: store_tile<SOX_ACT_GELU>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, ctp, cto, pad_rows); break;
+        default: store_tile<-1>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, act, ctp, cto, pad_rows); break;
         }
         if (gs + 1 < total) {
             tile_origin(vid + (gs + 1) / nk * G, bm_cur, bn_cur);

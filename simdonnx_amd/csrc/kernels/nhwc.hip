@@ -801,16 +801,33 @@ __device__ __forceinline__ void softmax_body(const sox_softmax_args& p) {
     extern __shared__ float rowbuf[];
     __shared__ float red[4];
     const long row = blockIdx.x;
-    const T* x = (const T*)p.x + row * p.len;
+    const T* x = (const T*)p.x + row * p.ldx;
     T* y = (T*)p.y + row * p.len;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const bool staged = p.staged != 0;
     float m = -INFINITY;
-    strided_foreach<16>(x, threadIdx.x, p.len, 256, [&](long i, T v) {
-        const float f = to_f(v);
-        m = fmaxf(m, f);
-        if (staged) rowbuf[i] = f;
-    });
+    typedef typename V16<T>::Vec Vec;
+    constexpr int VE = V16<T>::N;
+    if (staged && p.ldx % VE == 0) {
+        // 16-byte aligned rows (a padded stride): vector loads, the last vector clipped at len
+        const int nv = (p.len + VE - 1) / VE;
+        strided_foreach<8>((const Vec*)x, threadIdx.x, nv, 256, [&](long j, Vec v) {
+#pragma unroll
+            for (int e = 0; e < VE; e++) {
+                if (j * VE + e < p.len) {
+                    const float f = to_f(v[e]);
+                    m = fmaxf(m, f);
+                    rowbuf[j * VE + e] = f;
+                }
+            }
+        });
+    } else {
+        strided_foreach<16>(x, threadIdx.x, p.len, 256, [&](long i, T v) {
+            const float f = to_f(v);
+            m = fmaxf(m, f);
+            if (staged) rowbuf[i] = f;
+        });
+    }
     m = wave_max(m);
     if (lane == 0) red[wv] = m;
     __syncthreads();

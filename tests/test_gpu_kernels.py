@@ -191,6 +191,25 @@ def test_se_block_matches_oracle(hip, half):
     assert max_rel(got, want) < TOL[half]
 
 
+# (m, k, n): Gemm -> Softmax over rows whose N is not a multiple of 4 (the class head): the Gemm runs
+# on the LDS-DMA ring into rows padded to a multiple of 8, the Softmax reads that stride
+HEAD_CASES = [(300, 128, 1001), (2560, 192, 6625), (77, 64, 13)]
+
+
+@pytest.mark.parametrize("case", HEAD_CASES, ids=lambda c: "x".join(str(v) for v in c))
+def test_gemm_softmax_padded_rows(hip, case):
+    m, k, n = case
+    a = f16(synth.uniform(15, 1, (m, k), -1, 1))
+    w = f16(synth.normal(15, 2, (k, n), 0.1))
+    b = synth.uniform(15, 3, (n,), -0.5, 0.5)
+    pb = PlanBuilder()
+    av = pb.input((m, k), None, "a")
+    y = pb.softmax(pb.gemm(av, w, b, name="head"), name="softmax")
+    got = run(hip, pb.build(y), [a], True)
+    want = O.softmax(f16(O.gemm(a, w, b)))
+    assert max_rel(got, want) < TOL[True]
+
+
 # (batch, ic, oc, stride, h, w, act, residual): 3x3 zero-padded convs on the halo route (stride 1),
 # with tile, output-channel and input-channel-block tails; the stride-2 case takes the ring
 HALO_CASES = [(1, 96, 24, 1, 30, 30, "none", False), (2, 40, 40, 1, 17, 35, "relu", True),
