@@ -176,6 +176,12 @@ SOX_DEV void store_tile(half_t* __restrict__ Y, const half_t* __restrict__ R, in
     });
 }
 
+// Bytes one wave's DMA instruction fills: its whole share when that is at most 1 KiB (64 lanes x 16 B),
+// else the largest of 1024 / 768 / 512 / 256 that divides the share (e.g. 1.5 KiB -> 2 x 768).
+constexpr int dma_chunk(int share) {
+    return share <= 1024 ? share : share % 1024 == 0 ? 1024 : share % 768 == 0 ? 768 : share % 512 == 0 ? 512 : 256;
+}
+
 // CONV = false: A is a dense [M][lda] matrix (Gemm). CONV = true: A is the implicit im2col matrix of
 // an NHWC image, A[m][k] = x[b][oy*sh - pt + ky][ox*sw - pl + kx][c] for m = (b, oy, ox) and
 // k = (ky*kw + kx)*ic + c (tap-major, the packed weights' order). The K loop walks taps x channel
@@ -193,8 +199,8 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
     constexpr int BIAS_LANES = BIAS_BYTES / 16 / NW;  // lanes of each wave's bias DMA (16 B each)
     // DMA instructions per wave per slice; each fills CH contiguous LDS bytes (<= 1 KiB: lanes past
     // CH / 16 are idle when a wave's share is smaller)
-    constexpr int CH_A = A_BYTES / NW < 1024 ? A_BYTES / NW : 1024, A_IT = A_BYTES / NW / CH_A;
-    constexpr int CH_B = B_BYTES / NW < 1024 ? B_BYTES / NW : 1024, B_IT = B_BYTES / NW / CH_B;
+    constexpr int CH_A = dma_chunk(A_BYTES / NW), A_IT = A_BYTES / NW / CH_A;
+    constexpr int CH_B = dma_chunk(B_BYTES / NW), B_IT = B_BYTES / NW / CH_B;
     constexpr int LOADS = A_IT + B_IT + 1;      // + the bias DMA
     constexpr int TI = WM / 32, TJ = WN / 32;   // 32x32 MFMA blocks: m (columns) x n (rows)
     constexpr int WAVES_N = BN / WN;
