@@ -9,7 +9,8 @@
 //    per SIMD; the 16x16x32 form needs two waves per SIMD and still tops out lower). W is the row
 //    operand and A the column operand, so lane l holds Y^T[n = 8(q/4) + 4(l/32) + q%4][m = l%32]:
 //    4 runs of 4 consecutive output channels of one row, i.e. float4 bias/activation and 8-byte stores
-//    straight from the accumulators.
+//    straight from the accumulators, or (EPI_LDS instances) staged through LDS into 16-byte stores of
+//    whole 128-byte row segments.
 //  * K slices move global -> LDS with global_load_lds_dwordx4 (no register staging), STAGES deep.
 //    LDS rows are BK fp16 (CPR 16-byte chunks) stored XOR-swizzled (slot = chunk ^ f(row),
 //    f(r) = (r / (16 / CPR)) % CPR), so the 16 lanes that one ds_read_b128 cycle serves (16 consecutive
@@ -176,6 +177,43 @@ SOX_DEV void store_tile(half_t* __restrict__ Y, const half_t* __restrict__ R, in
     });
 }
 
+// Epilogue through LDS (no residual, no scatter, rows of whole 8-element groups): each wave stages
+// 32 rows x 64 channels (two 32x32 blocks; 32 when it has one) of fp16 results in its own 4 KiB
+// (2 KiB) of LDS and stores them back as 16-byte chunks, 8 (4) lanes per row, so every store
+// instruction writes 8 whole 128-byte row segments (16 of 64 bytes) instead of 32 scattered 16-byte
+// pieces. The staged rows hold 16-byte chunks XOR-swizzled
+// by row (slot = chunk ^ row % chunks), which spreads both the 8-byte writes (one row per lane) and
+// the 16-byte reads (one row per 8 lanes) evenly over the banks.
+template <int ACT, int TJ, int TI>
+SOX_DEV void store_tile_lds(half_t* __restrict__ Y, int ldy, int M, int N, int m0, int n0,
+                            const float16v (&acc)[TJ][TI], int act, unsigned char* stg) {
+    const int lane = threadIdx.x & 63, l32 = lane & 31, hl = lane >> 5;
+    auto fin = [&](float a) { return ACT == SOX_ACT_GELU ? gelu_fast(a) : ACT >= 0 ? sox_act(a, ACT) : act_fast(a, act); };
+    static_for<0, TI * ((TJ + 1) / 2)>([&](auto ip) {
+        constexpr int i = decltype(ip)::value / ((TJ + 1) / 2), j0 = 2 * (decltype(ip)::value % ((TJ + 1) / 2));
+        constexpr int JG = j0 + 1 < TJ ? 2 : 1, CH = JG * 4;  // blocks staged together, 16-byte chunks per row
+        static_for<0, CH>([&](auto cc) {
+            constexpr int c = decltype(cc)::value, j = j0 + c / 4, q = c % 4;
+            half4 h;
+            static_for<0, 4>([&](auto ee) { h[decltype(ee)::value] = (half_t)fin(acc[j][i][4 * q + decltype(ee)::value]); });
+            *(half4*)(stg + l32 * CH * 16 + ((c ^ (l32 % CH)) << 4) + hl * 8) = h;
+        });
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // other lanes' rows are read back
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        static_for<0, CH / 2>([&](auto tt) {
+            const int idx = decltype(tt)::value * 64 + lane, r = idx / CH, c = idx % CH;
+            const half8 v = *(const half8*)(stg + r * CH * 16 + ((c ^ (r % CH)) << 4));
+            const int m = m0 + i * 32 + r, n = n0 + j0 * 32 + c * 8;
+            if (m < M && n < N) *(half8*)(Y + (long)m * ldy + n) = v;
+        });
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the next group overwrites the stage
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        __builtin_amdgcn_sched_barrier(0);
+    });
+}
+
 // Bytes one wave's DMA instruction fills: its whole share when that is at most 1 KiB (64 lanes x 16 B),
 // else the largest of 1024 / 768 / 512 / 256 that divides the share (e.g. 1.5 KiB -> 2 x 768).
 constexpr int dma_chunk(int share) {
@@ -189,7 +227,7 @@ constexpr int dma_chunk(int share) {
 // is its row's offset + the tap's offset + its channel. Channels past ic (the last block of a tap
 // when BK does not divide ic) and zero-padding taps are fetched from p.zeros; ic % 8 == 0. Rows past
 // M re-read row M - 1 (never stored).
-template <int BM, int BN, int BK, int WM, int WN, int STAGES, int NW, int GM, bool CONV = false, bool PF = false>
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int NW, int GM, bool CONV = false, bool EPI_LDS = false>
 __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
     constexpr int CPR = BK / 8;                 // 16-byte chunks per LDS row
     constexpr int ROWB = BK * 2;                // LDS row bytes
@@ -212,7 +250,9 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
     static_assert(BIAS_LANES * 16 * NW == BIAS_BYTES && BIAS_LANES <= 64 && STAGE_BYTES % 16 == 0, "bias DMA split");
     static_assert(STAGES >= 2 && (STAGES - 1) * LOADS < 64, "vmcnt range");
 
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[STAGE_BYTES * STAGES];
+    constexpr int EPI_WAVE = 32 * 32 * (TJ < 2 ? TJ : 2) * 2;  // store_tile_lds staging per wave (2 or 4 KiB)
+    constexpr int EPI_BYTES = EPI_LDS ? NW * EPI_WAVE : 0;
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[STAGE_BYTES * STAGES + EPI_BYTES];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int l32 = lane & 31, hl = lane >> 5;
@@ -295,7 +335,7 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
     // still issued (re-reading the last tile's rows into a stage nobody reads again), so every slice
     // has the same number of loads in flight and one static vmcnt covers them all.
     // prep computes a slice's DMA sources (calling set_sources at a tile's first slice), fire issues
-    // the DMAs; the small-tile loop runs prep a slice early, under the MFMAs.
+    // the DMAs.
     struct Src {
         const half_t* a[A_IT];
         const half_t* b[B_IT];
@@ -358,20 +398,19 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
         fire(gs, q);
     };
 
-    // fragment offsets: k-step s of a lane covers chunk 2s + l/32 of rows (row0 + l%32)
-    int a_off[KS][TI], b_off[KS][TJ];
+    // fragment offsets: k-step s of a lane covers chunk 2s + l/32 of rows (row0 + l%32), stored at slot
+    // (2s + l/32) ^ swz(row) = 2s ^ (l/32 ^ swz(row)): the offset of step 0 with bit 5 flipped by s
+    // (the row's byte offset has no bits below ROWB >= 64)
+    int a_off[TI], b_off[TJ];
 #pragma unroll
-    for (int s = 0; s < KS; s++) {
+    for (int i = 0; i < TI; i++) {
+        const int r = wm0 + i * 32 + l32;
+        a_off[i] = r * ROWB + ((hl ^ swz<CPR>(r)) << 4);
+    }
 #pragma unroll
-        for (int i = 0; i < TI; i++) {
-            const int r = wm0 + i * 32 + l32;
-            a_off[s][i] = r * ROWB + (((2 * s + hl) ^ swz<CPR>(r)) << 4);
-        }
-#pragma unroll
-        for (int j = 0; j < TJ; j++) {
-            const int r = wn0 + j * 32 + l32;
-            b_off[s][j] = A_BYTES + r * ROWB + (((2 * s + hl) ^ swz<CPR>(r)) << 4);
-        }
+    for (int j = 0; j < TJ; j++) {
+        const int r = wn0 + j * 32 + l32;
+        b_off[j] = A_BYTES + r * ROWB + ((hl ^ swz<CPR>(r)) << 4);
     }
 
     if (total == 0) return;
@@ -383,9 +422,9 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
     auto read_step = [&](int gs, int s, half8 (&fa)[TI], half8 (&fb)[TJ]) __attribute__((always_inline)) {
         const unsigned char* st = smem + (gs % STAGES) * STAGE_BYTES;
 #pragma unroll
-        for (int j = 0; j < TJ; j++) fb[j] = *(const half8*)(st + b_off[s][j]);
+        for (int j = 0; j < TJ; j++) fb[j] = *(const half8*)(st + (b_off[j] ^ (s << 5)));
 #pragma unroll
-        for (int i = 0; i < TI; i++) fa[i] = *(const half8*)(st + a_off[s][i]);
+        for (int i = 0; i < TI; i++) fa[i] = *(const half8*)(st + (a_off[i] ^ (s << 5)));
     };
     // accumulators of a new tile = its bias (from the LDS stage of the tile's first slice)
     auto init_acc = [&](int gs) __attribute__((always_inline)) {
@@ -405,8 +444,25 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
     const ConvtOut cto{p.ih, p.iw, p.ct_kh, p.ct_kw, p.ct_oc, (p.flags & SOX_F_BIAS) ? p.bias : nullptr};
     const bool ctp = CONV && (p.flags & SOX_F_CONVT);
     const bool pad_rows = (p.flags & SOX_F_PAD_ROWS) != 0;
+    // whole 16-byte chunks of every stored row (pad_rows: the row pitch covers N rounded up to 8)
+    const bool lds_ok = EPI_LDS && !R && !ctp && (p.ldy & 7) == 0 && (pad_rows || (N & 7) == 0);
     auto epilogue = [&](int gs) __attribute__((always_inline)) {
         // ---- epilogue from registers (the next tile's first slices are already loading) ----
+        if constexpr (EPI_LDS) {
+            if (lds_ok) {
+                unsigned char* stg = smem + STAGE_BYTES * STAGES + wave * EPI_WAVE;
+                switch (act) {
+                case SOX_ACT_NONE: store_tile_lds<SOX_ACT_NONE>(Y, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, stg); break;
+                case SOX_ACT_GELU: store_tile_lds<SOX_ACT_GELU>(Y, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, stg); break;
+                default: store_tile_lds<-1>(Y, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, act, stg); break;
+                }
+                if (gs + 1 < total) {
+                    tile_origin(vid + (gs + 1) / nk * G, bm_cur, bn_cur);
+                    init_acc(gs + 1);
+                }
+                return;
+            }
+        }
         switch (act) {
         case SOX_ACT_NONE: store_tile<SOX_ACT_NONE>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, ctp, cto, pad_rows); break;
         case SOX_ACT_RELU: store_tile<SOX_ACT_RELU>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, ctp, cto, pad_rows); break;
@@ -421,54 +477,6 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
 
 #pragma unroll
     for (int s = 0; s < STAGES; s++) issue(s);
-    if constexpr (PF) {
-        // Small tiles (a few MFMAs per k-step): a k-step's MFMAs cannot cover an LDS read, so every
-        // fragment of the next slice is read right after the barrier that publishes it, in flight
-        // under this slice's MFMAs, and the DMA sources of the slice after that are computed there
-        // too. Fragments double-buffer by slice parity (two slices per loop trip, constant indices).
-        half8 sa[2][KS][TI], sb[2][KS][TJ];
-        auto read_slice = [&](int gs, half8 (&fa)[KS][TI], half8 (&fb)[KS][TJ]) __attribute__((always_inline)) {
-            const unsigned char* st = smem + (gs % STAGES) * STAGE_BYTES;
-            static_for<0, KS>([&](auto ss) {
-                constexpr int k = decltype(ss)::value;
-                static_for<0, TJ>([&](auto jj) { fb[k][decltype(jj)::value] = *(const half8*)(st + b_off[k][decltype(jj)::value]); });
-                static_for<0, TI>([&](auto ii) { fa[k][decltype(ii)::value] = *(const half8*)(st + a_off[k][decltype(ii)::value]); });
-            });
-        };
-        Src nxt;
-        prep(STAGES, nxt);
-        wait_vmcnt<(STAGES - 1) * LOADS>();  // slice 0
-        __builtin_amdgcn_s_barrier();
-        init_acc(0);
-        read_slice(0, sa[0], sb[0]);
-        auto slice = [&](int gs, auto cc) __attribute__((always_inline)) {
-            constexpr int C = decltype(cc)::value, X = 1 - C;
-            // slice gs+1 landed and every read of slice gs is in registers, for all waves
-            wait_vmcnt<(STAGES - 2) * LOADS>();
-            wait_lgkmcnt0();
-            __builtin_amdgcn_s_barrier();
-            fire(gs + STAGES, nxt);  // into stage gs % STAGES
-            read_slice(gs + 1, sa[X], sb[X]);
-            __builtin_amdgcn_sched_barrier(0);
-            static_for<0, KS * TJ * TI>([&](auto kji) {
-                constexpr int k = decltype(kji)::value / (TJ * TI), j = (decltype(kji)::value / TI) % TJ,
-                              i = decltype(kji)::value % TI;
-                acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sb[C][k][j], sa[C][k][i], acc[j][i], 0, 0, 0);
-            });
-            prep(gs + STAGES + 1, nxt);
-            __builtin_amdgcn_sched_barrier(0);
-            if (gs % nk == nk - 1) {
-                wait_lgkmcnt0();  // init_acc reads LDS too
-                epilogue(gs);
-            }
-        };
-        for (int gs = 0; gs < total; gs += 2) {
-            slice(gs, std::integral_constant<int, 0>{});
-            if (gs + 1 < total) slice(gs + 1, std::integral_constant<int, 1>{});
-        }
-        wait_vmcnt<0>();
-        return;
-    }
     wait_vmcnt<(STAGES - 1) * LOADS>();  // slice 0
     __builtin_amdgcn_s_barrier();
     init_acc(0);
@@ -515,6 +523,11 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
 #define SOX_GEMM(NAME, BM, BN, BK, WM, WN, ST, NW, OCC, GM)                                         \
     extern "C" __global__ void __launch_bounds__(64 * NW, OCC) NAME(sox_igemm_args p) {           \
         gemm_body<BM, BN, BK, WM, WN, ST, NW, GM>(p);                                             \
+    }
+// epilogue staged through LDS (store_tile_lds)
+#define SOX_GEMM_E(NAME, BM, BN, BK, WM, WN, ST, NW, OCC, GM)                                       \
+    extern "C" __global__ void __launch_bounds__(64 * NW, OCC) NAME(sox_igemm_args p) {           \
+        gemm_body<BM, BN, BK, WM, WN, ST, NW, GM, false, true>(p);                             \
     }
 #define SOX_CONV(NAME, BM, BN, BK, WM, WN, ST, NW, OCC, GM)                                         \
     extern "C" __global__ void __launch_bounds__(64 * NW, OCC) NAME(sox_igemm_args p) {           \
