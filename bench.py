@@ -142,7 +142,7 @@ def bench_network(key: str, steps: int, replay: bool = True):
     for name, c in sorted(classes.items(), key=lambda kv: -kv[1]["ms"]):
         gbs = c["bytes"] / (c["ms"] * 1e-3) / 1e9
         tfl = c["flops"] / (c["ms"] * 1e-3) / 1e12
-        bound = "mfma" if name in ("conv", "gemm") and c["flops"] / max(c["bytes"], 1) > 313 else "hbm"
+        bound = "mfma" if name in ("conv", "gemm", "gemm_ln") and c["flops"] / max(c["bytes"], 1) > 313 else "hbm"
         frac = tfl / PEAK_FP16_TFLOPS if bound == "mfma" else gbs / PEAK_HBM_GBS
         out.append(dict(kernel=name, nodes=c["n"], ms=round(c["ms"], 4), gb_s=round(gbs, 1), tflop_s=round(tfl, 2),
                         bound=bound, frac=round(frac, 4)))

@@ -39,6 +39,9 @@ enum sox_act { SOX_ACT_NONE = 0, SOX_ACT_RELU = 1, SOX_ACT_SIGMOID = 2, SOX_ACT_
  *   M = n*oh*ow output pixels (or Gemm rows), N = oc, K = kh*kw*ic (tap-major, channel fastest).
  *   w is [N][kpad] (k fastest: ConstKind.ConvWT / GemmNK, Engine/Extensions.cs:150-153).
  *   y[m*ldy + n] = act(sum_k A[m,k] w[n,k] (+ bias[n]) (+ add[m*ldy + n]))
+ * The sox_gemm_ln_* kernels take A as the input of a LayerNorm over its rows (K) that the host folded
+ * into the Gemm: w holds gamma-scaled weights, bias = b + beta . W, and
+ *   y[m*ldy + n] = act(rstd_m (sum_k A[m,k] w[n,k] - mean_m ln_c[n]) + bias[n] (+ add)).
  * Grid: (ceil(M/BM), ceil(N/BN)); 256 threads.
  */
 typedef struct sox_igemm_args {
@@ -57,6 +60,8 @@ typedef struct sox_igemm_args {
     int32_t lda;  /* SOX_F_DENSE_A: A row stride in elements */
     int32_t tiles_n; /* ceil(N/BN): tile-order remap of the 1-D grid */
     int32_t ct_kh, ct_kw, ct_oc; /* SOX_F_CONVT: the ConvTranspose kernel (stride == kernel) and its channels */
+    float ln_eps;                /* sox_gemm_ln_*: the folded LayerNorm's epsilon */
+    const float* ln_c;           /* sox_gemm_ln_*: [N] column sums of the gamma-scaled packed weights */
 } sox_igemm_args;
 
 /*

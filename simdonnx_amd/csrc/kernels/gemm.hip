@@ -17,3 +17,8 @@ SOX_GEMM(sox_gemm_f16_64x64_k64s2, 64, 64, 64, 32, 32, 2, 4, 4, 4)
 // short K (a few slices): every slice of a tile in flight from the start
 SOX_GEMM_E(sox_gemm_f16_64x64_k64s4, 64, 64, 64, 32, 32, 4, 4, 2, 4)
 SOX_GEMM(sox_gemm_f16_128x64_k64s4, 128, 64, 64, 64, 32, 4, 4, 1, 4)
+// A rows through a LayerNorm folded into the Gemm (the default tilings)
+SOX_GEMM_LN(sox_gemm_ln_f16_256x128_w8k64s2, 256, 128, 64, 64, 64, 2, 8, 1, 4, true)
+SOX_GEMM_LN(sox_gemm_ln_f16_128x128_k64s2, 128, 128, 64, 64, 64, 2, 4, 2, 4, false)
+SOX_GEMM_LN(sox_gemm_ln_f16_128x64_k64s2, 128, 64, 64, 64, 32, 2, 4, 3, 4, false)
+SOX_GEMM_LN(sox_gemm_ln_f16_64x64_k64s4, 64, 64, 64, 32, 32, 4, 4, 2, 4, true)

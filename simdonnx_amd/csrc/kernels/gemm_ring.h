@@ -227,7 +227,8 @@ constexpr int dma_chunk(int share) {
 // is its row's offset + the tap's offset + its channel. Channels past ic (the last block of a tap
 // when BK does not divide ic) and zero-padding taps are fetched from p.zeros; ic % 8 == 0. Rows past
 // M re-read row M - 1 (never stored).
-template <int BM, int BN, int BK, int WM, int WN, int STAGES, int NW, int GM, bool CONV = false, bool EPI_LDS = false>
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int NW, int GM, bool CONV = false, bool EPI_LDS = false,
+          bool LN = false>
 __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
     constexpr int CPR = BK / 8;                 // 16-byte chunks per LDS row
     constexpr int ROWB = BK * 2;                // LDS row bytes
@@ -265,8 +266,10 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
     half_t* __restrict__ Y = (half_t*)p.y;
     const half_t* __restrict__ R = (p.flags & SOX_F_RESIDUAL) ? (const half_t*)p.add : nullptr;  // [M][ldy]
     const int act = (p.flags & SOX_F_ACT_MASK) >> SOX_F_ACT_SHIFT;
-    // a ConvTranspose's bias is per output channel, added in its scatter epilogue, not per column
-    const bool has_bias = (p.flags & SOX_F_BIAS) != 0 && !(CONV && (p.flags & SOX_F_CONVT));
+    static_assert(!LN || !CONV, "LayerNorm-folded A: dense Gemm only");
+    // a ConvTranspose's bias is per output channel, added in its scatter epilogue, not per column;
+    // with LN the bias is added after the normalisation, so the accumulators start from zero
+    const bool has_bias = (p.flags & SOX_F_BIAS) != 0 && !(CONV && (p.flags & SOX_F_CONVT)) && !LN;
     const int cblocks = CONV ? (p.ic + BK - 1) / BK : 1;  // channel blocks per tap
     const int nk = CONV ? p.kh * p.kw * cblocks : K / BK;
     const bool reflect = (p.flags & SOX_F_REFLECT) != 0;
@@ -419,6 +422,7 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
 
     float16v acc[TJ][TI];
     half8 fa0[TI], fb0[TJ], fa1[TI], fb1[TJ];
+    float ls1[TI], ls2[TI];  // LN: this lane's share of its rows' sum and sum of squares
     auto read_step = [&](int gs, int s, half8 (&fa)[TI], half8 (&fb)[TJ]) __attribute__((always_inline)) {
         const unsigned char* st = smem + (gs % STAGES) * STAGE_BYTES;
 #pragma unroll
@@ -439,6 +443,40 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
             static_for<0, 16>([&](auto qe) { v[decltype(qe)::value] = b4[decltype(qe)::value / 4][decltype(qe)::value % 4]; });
             static_for<0, TI>([&](auto ii) { acc[j][decltype(ii)::value] = v; });
         });
+        if constexpr (LN) {
+#pragma unroll
+            for (int i = 0; i < TI; i++) ls1[i] = ls2[i] = 0.0f;
+        }
+    };
+    // LN (the Gemm's A rows are the input of a LayerNorm folded into it at graph creation: W holds
+    // gamma-scaled weights, bias = b + beta W, p.ln_c[n] = sum_k W[n][k]): the accumulators hold
+    // sum_k x[m][k] W[n][k]; with the row's mean and rsqrt(var + eps) from the sums that the k-steps
+    // gathered, y = rstd (acc - mean c[n]) + bias[n], i.e. LN(x) . W^T + b up to rounding.
+    auto ln_apply = [&]() __attribute__((always_inline)) {
+        float mu[TI], rs[TI];
+        const float inv_k = 1.0f / (float)K;
+#pragma unroll
+        for (int i = 0; i < TI; i++) {  // lanes l and l + 32 hold the two k-halves of a row
+            const float s1 = ls1[i] + __shfl_xor(ls1[i], 32), s2 = ls2[i] + __shfl_xor(ls2[i], 32);
+            mu[i] = s1 * inv_k;
+            rs[i] = __builtin_amdgcn_rsqf(fmaxf(s2 * inv_k - mu[i] * mu[i], 0.0f) + p.ln_eps);
+        }
+        const bool hb = (p.flags & SOX_F_BIAS) != 0;
+        static_for<0, TJ>([&](auto jj) {
+            constexpr int j = decltype(jj)::value;
+            float4v cv[4], bv[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {  // both consts are zero-padded to a multiple of 4 floats
+                const int n = min(bn_cur + wn0 + j * 32 + 8 * q + 4 * hl, ((N + 3) & ~3) - 4);
+                cv[q] = *(const float4v*)(p.ln_c + n);
+                bv[q] = hb ? *(const float4v*)(p.bias + n) : (float4v)0.0f;
+            }
+            wait_vmcnt<0>();  // as for the residual: no loads carried into the K loop
+            static_for<0, TI * 16>([&](auto ie) {
+                constexpr int i = decltype(ie)::value / 16, e = decltype(ie)::value % 16;
+                acc[j][i][e] = rs[i] * (acc[j][i][e] - mu[i] * cv[e / 4][e % 4]) + bv[e / 4][e % 4];
+            });
+        });
     };
 
     const ConvtOut cto{p.ih, p.iw, p.ct_kh, p.ct_kw, p.ct_oc, (p.flags & SOX_F_BIAS) ? p.bias : nullptr};
@@ -448,6 +486,7 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
     const bool lds_ok = EPI_LDS && !R && !ctp && (p.ldy & 7) == 0 && (pad_rows || (N & 7) == 0);
     auto epilogue = [&](int gs) __attribute__((always_inline)) {
         // ---- epilogue from registers (the next tile's first slices are already loading) ----
+        if constexpr (LN) ln_apply();
         if constexpr (EPI_LDS) {
             if (lds_ok) {
                 unsigned char* stg = smem + STAGE_BYTES * STAGES + wave * EPI_WAVE;
@@ -503,6 +542,15 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
                 constexpr int j = decltype(ji)::value / TI, i = decltype(ji)::value % TI;
                 acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cb[j], ca[i], acc[j][i], 0, 0, 0);
             });
+            if constexpr (LN) {  // the step's 8 values of each of the lane's rows, by fp32 dot2
+                const half2v one = {(half_t)1.0f, (half_t)1.0f};
+                static_for<0, TI * 4>([&](auto ih) {
+                    constexpr int i = decltype(ih)::value / 4, h = decltype(ih)::value % 4;
+                    const half2v v = {ca[i][2 * h], ca[i][2 * h + 1]};
+                    ls1[i] = __builtin_amdgcn_fdot2(v, one, ls1[i], false);
+                    ls2[i] = __builtin_amdgcn_fdot2(v, v, ls2[i], false);
+                });
+            }
             // MFMA, read, MFMA, read, ...: this step's operands were read one step earlier, and the
             // next step's reads issue while the matrix pipe works through this step
             constexpr int RD = TI + TJ, MF = TI * TJ;
@@ -528,6 +576,11 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
 #define SOX_GEMM_E(NAME, BM, BN, BK, WM, WN, ST, NW, OCC, GM)                                       \
     extern "C" __global__ void __launch_bounds__(64 * NW, OCC) NAME(sox_igemm_args p) {           \
         gemm_body<BM, BN, BK, WM, WN, ST, NW, GM, false, true>(p);                             \
+    }
+// A rows LayerNorm'ed on the fly (the LayerNorm folded into the Gemm); E = epilogue through LDS
+#define SOX_GEMM_LN(NAME, BM, BN, BK, WM, WN, ST, NW, OCC, GM, E)                                  \
+    extern "C" __global__ void __launch_bounds__(64 * NW, OCC) NAME(sox_igemm_args p) {           \
+        gemm_body<BM, BN, BK, WM, WN, ST, NW, GM, false, E, true>(p);                             \
     }
 #define SOX_CONV(NAME, BM, BN, BK, WM, WN, ST, NW, OCC, GM)                                         \
     extern "C" __global__ void __launch_bounds__(64 * NW, OCC) NAME(sox_igemm_args p) {           \

@@ -210,6 +210,48 @@ def test_gemm_softmax_padded_rows(hip, case):
     assert max_rel(got, want) < TOL[True]
 
 
+# (rows, k, n, act, trans_b, tail, mean): a LayerNorm whose output only a Gemm reads folds into the Gemm
+# (sox_gemm_ln_*, one dispatch). tail: "softmax" (the class head: N % 4 != 0, padded rows), "residual"
+# (the block's Add of the LayerNorm's own input in the Gemm epilogue); mean: an offset added to every
+# input row (the single-pass variance against a mean 8x the spread). The last two cases stay unfolded:
+# K % 64 != 0 and fewer than 64 rows.
+LN_GEMM_CASES = [(2560, 192, 576, "none", 0, None, 0.0), (2560, 192, 768, "gelu", 0, None, 0.0),
+                 (300, 192, 6625, "none", 0, "softmax", 0.0), (1000, 128, 256, "relu", 1, None, 8.0),
+                 (2560, 192, 192, "none", 0, "residual", 0.5), (200, 40, 64, "none", 0, None, 0.0),
+                 (40, 64, 64, "none", 0, None, 0.0)]
+
+
+@pytest.mark.parametrize("case", LN_GEMM_CASES, ids=lambda c: "x".join(str(v) for v in c))
+def test_layernorm_folded_into_gemm(hip, case):
+    m, k, n, act, tb, tail, mean = case
+    x = f16(synth.uniform(16, 1, (m, k), -1, 1) + mean)
+    gam = 1.0 + synth.uniform(16, 2, (k,), -0.2, 0.2)
+    bet = synth.uniform(16, 3, (k,), -0.2, 0.2)
+    w = f16(synth.normal(16, 4, (n, k) if tb else (k, n), 0.1))
+    b = synth.uniform(16, 5, (n,), -0.2, 0.2)
+    pb = PlanBuilder()
+    xv = pb.input((m, k), None, "x")
+    h = pb.layer_norm(xv, gam, bet, 1e-5, name="ln")
+    y = pb.gemm(h, w, b, act=act if tail != "residual" else "none", trans_b=bool(tb), name="gemm")
+    if tail == "softmax":
+        y = pb.softmax(y, name="softmax")
+    elif tail == "residual":
+        y = pb.add(xv, y, name="res")
+    plan = pb.build(y)
+    g = hip.graph(plan, True)
+    folded = k % 64 == 0 and m >= 64
+    names = [d[0] for d in g.dispatches]
+    assert names == (["gemm_ln"] if folded else ["layernorm", "gemm"]) + (["softmax"] if tail == "softmax" else [])
+    got = run(hip, plan, [x], True)
+    wk = w.T if tb else w
+    want = O.gemm(O.layer_norm(x, gam, bet, 1e-5), np.ascontiguousarray(wk), b, act=act if tail != "residual" else "none")
+    if tail == "softmax":
+        want = O.softmax(f16(want))
+    elif tail == "residual":
+        want = x + f16(want)
+    assert max_rel(got, want) < TOL[True]
+
+
 # (batch, ic, oc, stride, h, w, act, residual): 3x3 zero-padded convs on the halo route (stride 1),
 # with tile, output-channel and input-channel-block tails; the stride-2 case takes the ring
 HALO_CASES = [(1, 96, 24, 1, 30, 30, "none", False), (2, 40, 40, 1, 17, 35, "relu", True),
