@@ -949,101 +949,118 @@ extern "C" __global__ void __launch_bounds__(256) sox_pool_f32(sox_pool_args p) 
 
 // ------------------------------------------------------------------------------------------
 // Attention on matrix cores (attn.comp's SDPA, D = 32 or 64, S <= 128), fp16 storage.
-// One wave per (batch, head, 16 queries). S^T = K Q^T is built with v_mfma_f32_16x16x32_f16
-// straight from global memory (lane l: K row s = 16j + l%16, Q row t = l%16, 8 consecutive d),
-// so lane l ends up holding the scores of query t = l%16 for keys s = 16j + 4(l/16) + i. The
-// softmax over s is an in-register max/sum plus two cross-lane steps (lanes l, l^16, l^32, l^48).
-// O = P V reuses that register layout directly as the MFMA A operand: within each 32-key step the
-// lane's 8 keys are {32c + 4g + i, 32c + 16 + 4g + i} (g = l/16), and the B operand (V) is read at
-// the same key permutation, which leaves the sum over keys unchanged.
+// One workgroup per (batch, head); its waves take 16 queries at a time. K ([s][d], rows padded by
+// 16 bytes) and V^T ([d][s]) are staged in LDS once per workgroup with 16-byte loads, and each wave's
+// first Q fragments load in the same round trip.
+// S^T = K Q^T is built with v_mfma_f32_16x16x32_f16 (lane l: K row s = 16j + l%16, Q row t = l%16,
+// 8 consecutive d), so lane l ends up holding the scores of query t = l%16 for keys
+// s = 16j + 4(l/16) + i. The softmax over s is an in-register max/sum plus two cross-lane steps
+// (lanes l, l^16, l^32, l^48). O = P V reuses that register layout directly as the MFMA A operand:
+// within each 32-key step the lane's 8 keys are {32c + 4g + i, 32c + 16 + 4g + i} (g = l/16), and
+// the B operand (V) is read at the same key permutation (two 8-byte runs of V^T), which leaves the
+// sum over keys unchanged. Keys past S hold P = 0 and V = 0.
 // ------------------------------------------------------------------------------------------
 template <int NJ, int KD>
 __device__ __forceinline__ void attn_mfma_body(const sox_attn_args& p) {
-    const int lane = threadIdx.x & 63;
+    constexpr int S = 16 * NJ, D = 32 * KD, NC = (NJ + 1) / 2, SP = 32 * NC, JD = 2 * KD;
+    constexpr int KP = D + 8, VP = SP + 8;  // LDS row pitches in halves
+    __shared__ __attribute__((aligned(16))) half_t ks[S * KP];
+    __shared__ __attribute__((aligned(16))) half_t vt[D * VP];
+    const int tid = threadIdx.x, nthr = blockDim.x, lane = tid & 63, wave = tid >> 6, nwaves = nthr >> 6;
     const int l16 = lane & 15, g = lane >> 4;
-    const int bh = blockIdx.x, tb = blockIdx.y;
+    const int bh = blockIdx.x;
     const int b = bh / p.heads, h = bh - b * p.heads;
     const half_t* __restrict__ q = (const half_t*)p.q + b * p.q_sb + h * p.q_sh;
     const half_t* __restrict__ k = (const half_t*)p.k + b * p.k_sb + h * p.k_sh;
     const half_t* __restrict__ v = (const half_t*)p.v + b * p.v_sb + h * p.v_sh;
-    const int t = tb * 16 + l16;
+    const int tblocks = (p.t + 15) / 16;
+    auto load_q = [&](int tb, half8 (&qf)[KD]) {
+        const int t = tb * 16 + l16;
+#pragma unroll
+        for (int kd = 0; kd < KD; kd++)
+            qf[kd] = t < p.t ? *(const half8*)(q + (long)t * p.q_st + 32 * kd + 8 * g) : (half8)(half_t)0;
+    };
     half8 qf[KD];
+    if (wave < tblocks) load_q(wave, qf);
+    for (int i = tid; i < SP * (D / 8); i += nthr) {
+        const int s = i / (D / 8), c = i - s * (D / 8);
+        const half8 zero = (half8)(half_t)0;
+        const half8 vv = s < p.s ? *(const half8*)(v + (long)s * p.v_st + 8 * c) : zero;
+        if (s < S) *(half8*)(ks + s * KP + 8 * c) = s < p.s ? *(const half8*)(k + (long)s * p.k_st + 8 * c) : zero;
 #pragma unroll
-    for (int kd = 0; kd < KD; kd++)
-        qf[kd] = t < p.t ? *(const half8*)(q + (long)t * p.q_st + 32 * kd + 8 * g) : (half8)(half_t)0;
-    float4v sc[NJ];
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        const int s = 16 * j + l16;
-        float4v acc = (float4v)0.0f;
-#pragma unroll
-        for (int kd = 0; kd < KD; kd++) {
-            half8 kf = s < p.s ? *(const half8*)(k + (long)s * p.k_st + 32 * kd + 8 * g) : (half8)(half_t)0;
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[kd], acc, 0, 0, 0);
-        }
-        sc[j] = acc;
+        for (int e = 0; e < 8; e++) vt[(8 * c + e) * VP + s] = vv[e];
     }
-    float m = -INFINITY;
+    __syncthreads();
+    for (int tb = wave; tb < tblocks; tb += nwaves) {
+        if (tb != wave) load_q(tb, qf);
+        float4v sc[NJ];
 #pragma unroll
-    for (int j = 0; j < NJ; j++)
+        for (int j = 0; j < NJ; j++) {
+            float4v acc = (float4v)0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int s = 16 * j + 4 * g + i;
-            float x = s < p.s ? sc[j][i] * p.scale : -INFINITY;
-            sc[j][i] = x;
-            m = fmaxf(m, x);
-        }
-    m = fmaxf(m, __shfl_xor(m, 16, 64));
-    m = fmaxf(m, __shfl_xor(m, 32, 64));
-    float sum = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NJ; j++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int s = 16 * j + 4 * g + i;
-            float e = s < p.s ? sox_exp(sc[j][i] - m) : 0.0f;
-            sc[j][i] = e;
-            sum += e;
-        }
-    sum += __shfl_xor(sum, 16, 64);
-    sum += __shfl_xor(sum, 32, 64);
-    constexpr int NC = (NJ + 1) / 2, JD = 2 * KD;
-    float4v o[JD];
-#pragma unroll
-    for (int jd = 0; jd < JD; jd++) o[jd] = (float4v)0.0f;
-#pragma unroll
-    for (int c = 0; c < NC; c++) {
-        half8 pa;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            pa[i] = (half_t)sc[2 * c][i];
-            pa[4 + i] = 2 * c + 1 < NJ ? (half_t)sc[2 * c + 1][i] : (half_t)0;
-        }
-#pragma unroll
-        for (int jd = 0; jd < JD; jd++) {
-            const int d = 16 * jd + l16;
-            half8 vb;
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const int s = 32 * c + 4 * g + (e < 4 ? e : 12 + e);
-                vb[e] = s < p.s ? v[(long)s * p.v_st + d] : (half_t)0;
+            for (int kd = 0; kd < KD; kd++) {
+                const half8 kf = *(const half8*)(ks + (16 * j + l16) * KP + 32 * kd + 8 * g);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[kd], acc, 0, 0, 0);
             }
-            o[jd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o[jd], 0, 0, 0);
+            sc[j] = acc;
         }
-    }
-    half_t* __restrict__ out = (half_t*)p.o + b * p.o_sb + h * p.o_sh;
+        float m = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int tt = tb * 16 + 4 * g + i;
-        const float inv = 1.0f / __shfl(sum, 4 * g + i, 64);
-        if (tt < p.t)
+        for (int j = 0; j < NJ; j++)
 #pragma unroll
-            for (int jd = 0; jd < JD; jd++) out[(long)tt * p.o_st + 16 * jd + l16] = (half_t)(o[jd][i] * inv);
+            for (int i = 0; i < 4; i++) {
+                const int s = 16 * j + 4 * g + i;
+                const float x = s < p.s ? sc[j][i] * p.scale : -INFINITY;
+                sc[j][i] = x;
+                m = fmaxf(m, x);
+            }
+        m = fmaxf(m, __shfl_xor(m, 16, 64));
+        m = fmaxf(m, __shfl_xor(m, 32, 64));
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int s = 16 * j + 4 * g + i;
+                const float e = s < p.s ? sox_exp(sc[j][i] - m) : 0.0f;
+                sc[j][i] = e;
+                sum += e;
+            }
+        sum += __shfl_xor(sum, 16, 64);
+        sum += __shfl_xor(sum, 32, 64);
+        float4v o[JD];
+#pragma unroll
+        for (int jd = 0; jd < JD; jd++) o[jd] = (float4v)0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            half8 pa;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                pa[i] = (half_t)sc[2 * c][i];
+                pa[4 + i] = 2 * c + 1 < NJ ? (half_t)sc[2 * c + 1][i] : (half_t)0;
+            }
+#pragma unroll
+            for (int jd = 0; jd < JD; jd++) {
+                const half_t* row = vt + (16 * jd + l16) * VP + 32 * c + 4 * g;
+                const half4 lo = *(const half4*)row, hi = *(const half4*)(row + 16);
+                const half8 vb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                o[jd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o[jd], 0, 0, 0);
+            }
+        }
+        half_t* __restrict__ out = (half_t*)p.o + b * p.o_sb + h * p.o_sh;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int tt = tb * 16 + 4 * g + i;
+            const float inv = 1.0f / __shfl(sum, 4 * g + i, 64);
+            if (tt < p.t)
+#pragma unroll
+                for (int jd = 0; jd < JD; jd++) out[(long)tt * p.o_st + 16 * jd + l16] = (half_t)(o[jd][i] * inv);
+        }
     }
 }
 
 #define SOX_ATTN_MFMA(S, D)                                                                                  \
-    extern "C" __global__ void __launch_bounds__(64) sox_attn_f16_mfma_s##S##_d##D(sox_attn_args p) {         \
+    extern "C" __global__ void __launch_bounds__(512) sox_attn_f16_mfma_s##S##_d##D(sox_attn_args p) {        \
         attn_mfma_body<S / 16, D / 32>(p);                                                                   \
     }
 SOX_ATTN_MFMA(32, 32)
@@ -1112,22 +1129,23 @@ __device__ __forceinline__ void conv_direct_body(const sox_igemm_args& p) {
 
 // 3x3 taps over 3 channels (the RGB stems): all 27 input values of a pixel are loaded up front
 // (out-of-image taps read pixel 0 and take the pad value) instead of one dependent load per term.
+// The weights are staged k-major ([K][oc]), so a thread's OCV weights of one term are OCV / 4
+// 16-byte LDS reads.
 template <typename T, int OCV>
 __device__ __forceinline__ void conv_direct_333_body(const sox_igemm_args& p) {
     constexpr int KH = 3, KW = 3, IC = 3, K = KH * KW * IC;
-    extern __shared__ float wl[];  // [oc][K]
+    extern __shared__ float wl[];  // [K][oc]
     for (int i = threadIdx.x; i < p.n * K; i += blockDim.x) {
         const int o = i / K, kk = i - o * K;
-        wl[i] = to_f(((const T*)p.w)[(long)o * p.kpad + kk]);
+        wl[kk * p.n + o] = to_f(((const T*)p.w)[(long)o * p.kpad + kk]);
     }
     __syncthreads();
     const int ocg = p.n / OCV;
-    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (long)p.m * ocg) return;
-    const int og = (int)(idx % ocg);
-    const long m = idx / ocg;
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;  // m * ocg < 2^31 (the launcher checks)
+    if (idx >= p.m * ocg) return;
+    const int m = idx / ocg, og = idx - m * ocg;
     const int ohw = p.oh * p.ow;
-    const int b = (int)(m / ohw), r = (int)(m - (long)b * ohw);
+    const int b = m / ohw, r = m - b * ohw;
     const int oy = r / p.ow, ox = r - oy * p.ow;
     const bool reflect = (p.flags & SOX_F_REFLECT) != 0;
     const T* __restrict__ x = (const T*)p.x + (long)b * p.ih * p.iw * IC;
@@ -1150,14 +1168,18 @@ __device__ __forceinline__ void conv_direct_333_body(const sox_igemm_args& p) {
     float acc[OCV];
 #pragma unroll
     for (int e = 0; e < OCV; e++) acc[e] = (p.flags & SOX_F_BIAS) ? p.bias[og * OCV + e] : 0.0f;
-    const float* w0 = wl + (long)og * OCV * K;
+    const float* w0 = wl + og * OCV;  // oc % 4 == 0: 16-byte aligned rows
 #pragma unroll
-    for (int kk = 0; kk < K; kk++)
+    for (int kk = 0; kk < K; kk++) {
+        float4v wv[OCV / 4];
 #pragma unroll
-        for (int e = 0; e < OCV; e++) acc[e] = __builtin_fmaf(xv[kk], w0[e * K + kk], acc[e]);
+        for (int v = 0; v < OCV / 4; v++) wv[v] = *(const float4v*)(w0 + kk * p.n + 4 * v);
+#pragma unroll
+        for (int e = 0; e < OCV; e++) acc[e] = __builtin_fmaf(xv[kk], wv[e / 4][e % 4], acc[e]);
+    }
     const int act = (p.flags & SOX_F_ACT_MASK) >> SOX_F_ACT_SHIFT;
     typedef typename VecT<T, OCV>::Vec Vec;
-    const long o = m * p.ldy + og * OCV;
+    const long o = (long)m * p.ldy + og * OCV;
     if (p.flags & SOX_F_RESIDUAL) {
         const Vec av = *(const Vec*)((const T*)p.add + o);
 #pragma unroll
@@ -1165,7 +1187,7 @@ __device__ __forceinline__ void conv_direct_333_body(const sox_igemm_args& p) {
     }
     Vec out;
 #pragma unroll
-    for (int e = 0; e < OCV; e++) out[e] = (T)sox_act(acc[e], act);
+    for (int e = 0; e < OCV; e++) out[e] = (T)(sizeof(T) == 2 ? act_fast(acc[e], act) : sox_act(acc[e], act));
     *(Vec*)((T*)p.y + o) = out;
 }
 

@@ -65,6 +65,26 @@ SOX_DEV float sox_act(float v, int act) {
     }
 }
 
+// erf-GELU with the A&S 7.1.26 erf, rearranged for few instructions:
+//   gelu(x) = x Phi(x) = max(x, 0) - 0.5 |x| (1 - erf(|x| / sqrt2)),
+//   1 - erf(z) = t P(t) exp(-z^2),  t = 1 / (1 + 0.3275911 z)   (z >= 0),
+// with the 0.5 folded into P's coefficients, the hardware reciprocal and exp2 (fp16 outputs: their
+// ~1e-7 relative error is far below the output rounding). |x| is capped at 16 inside the erf term
+// (where that term is < 1e-50) so x = +-inf gives +inf / 0.
+SOX_DEV float gelu_fast(float x) {
+    const float ax = fminf(fabsf(x), 16.0f);
+    const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f * 0.70710678118654752f, ax, 1.0f));
+    float p = 0.5f * 1.061405429f;
+    p = __builtin_fmaf(p, t, 0.5f * -1.453152027f);
+    p = __builtin_fmaf(p, t, 0.5f * 1.421413741f);
+    p = __builtin_fmaf(p, t, 0.5f * -0.284496736f);
+    p = __builtin_fmaf(p, t, 0.5f * 0.254829592f);
+    const float e = __builtin_amdgcn_exp2f((ax * -0.72134752044448170f) * ax);  // exp(-x^2 / 2)
+    return __builtin_fmaf(-(ax * (p * t)), e, fmaxf(x, 0.0f));
+}
+
+SOX_DEV float act_fast(float v, int act) { return act == SOX_ACT_GELU ? gelu_fast(v) : sox_act(v, act); }
+
 SOX_DEV float sox_ew(float a, float b, int op) {
     switch (op) {
         case 0: return a + b;

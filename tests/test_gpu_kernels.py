@@ -337,9 +337,13 @@ def test_layernorm_softmax(hip, half):
 
 
 @pytest.mark.parametrize("half", [False, True], ids=["f32", "f16"])
-def test_attention_packed_qkv(hip, half):
-    """Fused attention over a packed [N, T, 3*H*D] qkv (GpuOpTests attention packed-qkv case)."""
-    nb, t, heads, d = 4, 80, 6, 32
+@pytest.mark.parametrize("shape", [(4, 80, 6, 32), (2, 37, 3, 64), (3, 128, 2, 32), (1, 20, 4, 64), (2, 64, 2, 64),
+                                   (5, 50, 1, 32), (2, 130, 2, 32)], ids=lambda c: "x".join(str(v) for v in c))
+def test_attention_packed_qkv(hip, half, shape):
+    """Fused attention over a packed [N, T, 3*H*D] qkv (GpuOpTests attention packed-qkv case): the
+    fp16 matrix-core kernel for every key-count bucket (32 / 64 / 80 / 128, with key tails) and head
+    size 32 / 64, and the general kernel past 128 keys."""
+    nb, t, heads, d = shape
     cv = f16 if half else (lambda a: a)
     qkv = cv(synth.uniform(5, 1, (nb, t, 3 * heads * d), -1, 1))
     pb = PlanBuilder()
