@@ -210,6 +210,34 @@ def test_gemm_softmax_padded_rows(hip, case):
     assert max_rel(got, want) < TOL[True]
 
 
+# (batch, ic, oc, k, stride, h, w, act, residual, reflect): fp32 convs with ic % 16 == 0, kh*kw*ic up to 576
+# and zero padding take the short-K matrix-core kernel (whole tile in LDS, K split over the waves); pixel
+# and channel tails, stride 2, residual; the reflect-padded case takes the general kernel
+F32_SHORT_CASES = [(1, 64, 64, 3, 1, 64, 64, "relu", False, False), (2, 64, 96, 3, 2, 33, 29, "gelu", True, False),
+                   (1, 64, 36, 1, 1, 10, 10, "none", False, False), (1, 16, 8, 4, 1, 12, 12, "hardswish", True, False),
+                   (1, 64, 40, 3, 1, 15, 17, "sigmoid", False, True), (3, 128, 24, 1, 1, 7, 9, "relu", True, False)]
+
+
+@pytest.mark.parametrize("case", F32_SHORT_CASES, ids=lambda c: "x".join(str(v) for v in c))
+def test_conv_f32_short_route(hip, case):
+    n, ic, oc, k, s, h, w, act, res, refl = case
+    x = synth.uniform(17, 1, (n, h, w, ic), -1, 1)
+    wt = synth.uniform(17, 2, (oc, ic, k, k), -0.25, 0.25)
+    b = synth.uniform(17, 3, (oc,), -0.1, 0.1)
+    pad = (k - 1) // 2 if k % 2 else k // 2
+    pads = (pad, pad, k - 1 - pad, k - 1 - pad)
+    oh, ow = (h + k - 1 - k) // s + 1, (w + k - 1 - k) // s + 1
+    add = synth.uniform(17, 4, (n, oh, ow, oc), -1, 1) if res else None
+    mode = 1 if refl else 0
+    plan, ins = conv_plan(x, wt, b, add, (s, s), pads, act, mode, 0.0)
+    g = hip.graph(plan, False)
+    assert [d[0] for d in g.dispatches] == ["conv"]
+    got = run(hip, plan, ins, False)
+    want = O.conv(x, wt, b, add, stride=(s, s), pads=pads, act=act, pad_mode=mode)
+    assert got.shape == want.shape
+    assert max_rel(got, want) < TOL[False]
+
+
 # (rows, k, n, act, trans_b, tail, mean): a LayerNorm whose output only a Gemm reads folds into the Gemm
 # (sox_gemm_ln_*, one dispatch). tail: "softmax" (the class head: N % 4 != 0, padded rows), "residual"
 # (the block's Add of the LayerNorm's own input in the Gemm epilogue); mean: an offset added to every
