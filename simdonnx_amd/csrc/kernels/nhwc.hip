@@ -342,7 +342,56 @@ __device__ __forceinline__ void convt_pix_body(const sox_convt_args& p) {
     }
 }
 
+// ConvTranspose to one output channel (the DB head's probability map, 24 -> 1 with a 2x2 kernel):
+// one input pixel per thread, its channels in 16-byte loads, the kh*kw taps' dot products against
+// the [tap][ic] weights staged in LDS (every lane reads the same word: broadcasts), and each output
+// row's kw values written by one store. Route: oc == 1, kh*kw <= 4, kw <= 2, ic % (16 / sizeof(T)) == 0.
+template <typename T>
+__device__ __forceinline__ void convt_one_body(const sox_convt_args& p) {
+    extern __shared__ float wl[];  // [tap][ic] (the [tap][ic][oc] packing with oc = 1)
+    typedef typename V16<T>::Vec Vec;
+    constexpr int VE = V16<T>::N;
+    const int taps = p.kh * p.kw, nw = taps * p.ic;
+    for (int i = threadIdx.x; i < nw; i += blockDim.x) wl[i] = to_f(((const T*)p.w)[i]);
+    __syncthreads();
+    const long pixels = (long)p.n * p.ih * p.iw;
+    const long pix = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (pix >= pixels) return;
+    const float bv = (p.flags & SOX_F_BIAS) ? p.bias[0] : 0.0f;
+    float acc[4] = {bv, bv, bv, bv};
+    const T* __restrict__ xp = (const T*)p.x + pix * p.ic;
+    for (int c0 = 0; c0 < p.ic; c0 += VE) {
+        const Vec xv = *(const Vec*)(xp + c0);
+#pragma unroll
+        for (int e = 0; e < VE; e++) {
+            const float xe = to_f(xv[e]);
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+                if (t < taps) acc[t] = __builtin_fmaf(xe, wl[t * p.ic + c0 + e], acc[t]);
+        }
+    }
+    const int act = (p.flags & SOX_F_ACT_MASK) >> SOX_F_ACT_SHIFT;
+    const int x = (int)(pix % p.iw);
+    const long q = pix / p.iw;
+    const int y = (int)(q % p.ih), b = (int)(q / p.ih);
+    const int ow = p.iw * p.kw, oh = p.ih * p.kh;
+    for (int dy = 0; dy < p.kh; dy++) {
+        T* out = (T*)p.y + ((long)b * oh + (y * p.kh + dy)) * ow + (long)x * p.kw;
+        if (p.kw == 2) {
+            typedef typename VecT<T, 2>::Vec Vec2;
+            Vec2 v;
+            v[0] = (T)sox_act(acc[2 * dy], act);
+            v[1] = (T)sox_act(acc[2 * dy + 1], act);
+            *(Vec2*)out = v;
+        } else {
+            for (int dx = 0; dx < p.kw; dx++) out[dx] = (T)sox_act(acc[dy * p.kw + dx], act);
+        }
+    }
+}
+
 extern "C" __global__ void __launch_bounds__(256) sox_convt_pix_f16(sox_convt_args p) { convt_pix_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_convt_one_f16(sox_convt_args p) { convt_one_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_convt_one_f32(sox_convt_args p) { convt_one_body<float>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_convt_pix_f32(sox_convt_args p) { convt_pix_body<float>(p); }
 
 // ------------------------------------------------------------------------------------------

@@ -134,8 +134,10 @@ def test_conv_transpose_matches_oracle(hip, i, half, path, monkeypatch):
     assert max_rel(got, want) < TOL[half]
 
 
-# (batch, ic, oc, k, h, w, act): ConvTranspose (stride == kernel) shapes beyond the fixtures
-CONVT_SHAPES = [(2, 32, 16, 3, 7, 5, "relu"), (1, 16, 5, 2, 33, 17, "sigmoid"), (1, 64, 96, 2, 13, 11, "none")]
+# (batch, ic, oc, k, h, w, act): ConvTranspose (stride == kernel) shapes beyond the fixtures; oc = 1 with
+# a 2x2 or 1x1 kernel takes the one-channel pixel kernel (the DB head's probability map)
+CONVT_SHAPES = [(2, 32, 16, 3, 7, 5, "relu"), (1, 16, 5, 2, 33, 17, "sigmoid"), (1, 64, 96, 2, 13, 11, "none"),
+                (1, 24, 1, 2, 45, 31, "sigmoid"), (2, 16, 1, 1, 9, 14, "relu"), (1, 8, 1, 3, 5, 6, "none")]
 
 
 @pytest.mark.parametrize("half", [False, True], ids=["f32", "f16"])
