@@ -4,7 +4,9 @@
  *
  * Each kernel takes exactly one of these structs by value, so its kernarg segment IS the struct:
  * a host fills it and passes its bytes to sox_launch (hipModuleLaunchKernel with
- * HIP_LAUNCH_PARAM_BUFFER_POINTER). Field order is device pointers first, then the parameter
+ * HIP_LAUNCH_PARAM_BUFFER_POINTER), always sizeof the whole struct as declared here: the runtime
+ * lays the block out as given, and a shorter one (a host built against an older copy of a struct
+ * that has since grown) is not what the kernel reads. Field order is device pointers first, then the parameter
  * block, mirroring the reference's binding order + push-constant struct for the matching shader
  * (e.g. Backends/Vulkan/Shaders/conv_cm.comp:86-91 and its ND(...) call, Backends/Vulkan/VkGraph.cs:664-674).
  *
