@@ -367,6 +367,21 @@ def test_layernorm_softmax(hip, half):
 
 
 @pytest.mark.parametrize("half", [False, True], ids=["f32", "f16"])
+@pytest.mark.parametrize("rows,len_", [(37, 1), (37, 13), (19, 2048), (19, 2049), (23, 6625), (5, 8192), (5, 8193),
+                                       (3, 20000)])
+def test_softmax_lengths(hip, rows, len_, half):
+    """Row softmax on the LDS-staged kernel (rows <= 16384, including the class head's 6625) and the
+    streaming one past it, with a per-row offset spread so the max subtraction matters."""
+    cv = f16 if half else (lambda a: a)
+    x = cv(synth.uniform(18, 1, (rows, len_), -4, 4) + synth.uniform(18, 2, (rows, 1), -20, 20))
+    pb = PlanBuilder()
+    xv = pb.input((rows, len_), None, "x")
+    y = pb.softmax(xv, name="softmax")
+    got = run(hip, pb.build(y), [x], half)
+    assert max_rel(got, O.softmax(x)) < TOL[half]
+
+
+@pytest.mark.parametrize("half", [False, True], ids=["f32", "f16"])
 @pytest.mark.parametrize("shape", [(4, 80, 6, 32), (2, 37, 3, 64), (3, 128, 2, 32), (1, 20, 4, 64), (2, 64, 2, 64),
                                    (5, 50, 1, 32), (2, 130, 2, 32)], ids=lambda c: "x".join(str(v) for v in c))
 def test_attention_packed_qkv(hip, half, shape):
