@@ -14,6 +14,8 @@ Also reported on the same line:
   cpu_baseline  the CPU oracle (a C++ restatement of the reference's AVX-512/AVX2 Gemm micro-kernel
                 + GELU epilogue) on the same workload, all host cores
   conv3x3       the fp32 Conv3x3 + bias + ReLU 1x64x64x64 kernel (us, TFLOP/s)
+  ops           the kernels of the rest of the ExecOp surface (resize, pad, transpose, slice, unary,
+                depth-space, pools, MatMul) at detector / recognizer sizes, GB/s vs the HBM peak
 """
 from __future__ import annotations
 
@@ -172,6 +174,79 @@ def bench_copy(steps: int):
     return dict(bytes_per_launch=2 * n * 2, ms=ms, gb_s=2 * n * 2 / (ms * 1e-3) / 1e9)
 
 
+def _ops_cases():
+    """One-node plans of the rest of the ExecOp surface at the sizes the detector / recognizer shapes
+    give them (fp16 storage): (label, plan, inputs, algorithmic bytes, flops). Bytes count each
+    tensor read or written once at 2 bytes per element."""
+    import numpy as np
+    from simdonnx_amd import synth
+    from simdonnx_amd.plan import NHWC, PlanBuilder
+    cases = []
+
+    def img(shape):
+        return synth.normal(77, 1, shape, 1.0)
+
+    def add_case(label, build, shapes, out_elems, flops=0):
+        pb = PlanBuilder()
+        y = build(pb)
+        ins = [img(sh) for sh in shapes]
+        cases.append((label, pb.build(y), ins, 2 * (sum(int(np.prod(sh)) for sh in shapes) + out_elems), flops))
+
+    add_case("bilinear x2 + addend, 1x240x240x24 -> 480x480",
+             lambda pb: pb.resize_bilinear(pb.input((1, 24, 240, 240), NHWC, "x"), 2, pb.input((1, 24, 480, 480), NHWC, "a"),
+                                           relu=True, name="bil"),
+             [(1, 240, 240, 24), (1, 480, 480, 24)], 480 * 480 * 24)
+    add_case("pad reflect 3, 1x480x480x32",
+             lambda pb: pb.pad(pb.input((1, 32, 480, 480), NHWC, "x"), (0, 0, 3, 3, 0, 0, 3, 3), 1, name="pad"),
+             [(1, 480, 480, 32)], 486 * 486 * 32)
+    add_case("transpose NHWC->NCHW, 1x480x480x24",
+             lambda pb: pb.transpose(pb.input((1, 480, 480, 24), None, "x"), (0, 3, 1, 2), name="tr"),
+             [(1, 480, 480, 24)], 480 * 480 * 24)
+    add_case("slice k of packed qkv, 32x80x576 -> 32x80x192",
+             lambda pb: pb.slice(pb.input((32, 80, 576), None, "x"), (192,), (384,), (2,), (1,), name="sl"),
+             [(32, 80, 576)], 32 * 80 * 192)
+    add_case("tanh, 8M elements",
+             lambda pb: pb.scalar_act("Tanh", pb.input((8 << 20,), None, "x"), 1.0, 1.0, name="tanh"),
+             [(8 << 20,)], 8 << 20)
+    add_case("depth-to-space b2 DCR, 1x240x240x96 -> 480x480x24",
+             lambda pb: pb.depth_to_space(pb.input((1, 96, 240, 240), NHWC, "x"), 2, False, name="d2s"),
+             [(1, 240, 240, 96)], 480 * 480 * 24)
+    add_case("avgpool 3x3 s2, 1x240x240x64",
+             lambda pb: pb.avg_pool(pb.input((1, 64, 240, 240), NHWC, "x"), (3, 3), (2, 2), (1, 1, 1, 1), name="avg"),
+             [(1, 240, 240, 64)], 120 * 120 * 64)
+    add_case("global avgpool, 1x240x240x96",
+             lambda pb: pb.global_avg_pool(pb.input((1, 96, 240, 240), NHWC, "x"), name="gap"),
+             [(1, 240, 240, 96)], 96)
+    add_case("matmul 192 x [80,32]x[32,80]",
+             lambda pb: pb.matmul(pb.input((192, 80, 32), None, "a"), pb.input((192, 32, 80), None, "b"), name="mm"),
+             [(192, 80, 32), (192, 32, 80)], 192 * 80 * 80, 2 * 192 * 80 * 32 * 80)
+    return cases
+
+
+def bench_ops(steps: int):
+    """Per-launch time of each kernel of the rest of the ExecOp surface, against the HBM roofline."""
+    from simdonnx_amd.backend import HipBackend, HipInferenceSession
+    hip = HipBackend.default()
+    out = []
+    for label, plan, ins, nbytes, flops in _ops_cases():
+        g = hip.graph(plan, True)
+        kern = [d[0] for d in g.dispatches]
+        with HipInferenceSession(g) as s:
+            for i, x in enumerate(ins):
+                s.set_input(x, i)
+            s.run()
+            s.time(20)
+            ms = s.time(steps) / steps
+        g.release()
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        rec = dict(op=label, kernels=kern, us=round(ms * 1e3, 2), algorithmic_mb=round(nbytes / 1e6, 2),
+                   gb_s=round(gbs, 1), bound="hbm", frac=round(gbs / PEAK_HBM_GBS, 4))
+        if flops:
+            rec["tflop_s"] = round(flops / (ms * 1e-3) / 1e12, 2)
+        out.append(rec)
+    return out
+
+
 def cpu_detector_ms():
     """The oracle running the whole detector plan (reference CPU kernels restated), ms per image."""
     import oracle as O
@@ -223,7 +298,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-replay", action="store_true",
                     help="launch network dispatches one by one instead of replaying a HIP graph (profiler runs)")
-    ap.add_argument("--only", choices=["gemm", "conv", "detector", "recognizer", "mobilenetv3", "copy"],
+    ap.add_argument("--only", choices=["gemm", "conv", "detector", "recognizer", "mobilenetv3", "copy", "ops"],
                     help="run one workload only (profiling runs); prints its own JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -232,7 +307,8 @@ def main():
         sys.exit(2)
     if args.only:
         fn = {"gemm": lambda: bench_gemm(args.steps, args.warmup), "conv": lambda: bench_conv(args.steps),
-              "copy": lambda: bench_copy(args.steps)}.get(args.only) or (lambda: bench_network(args.only, args.steps, not args.no_replay))
+              "copy": lambda: bench_copy(args.steps),
+              "ops": lambda: {"ops": bench_ops(args.steps)}}.get(args.only) or (lambda: bench_network(args.only, args.steps, not args.no_replay))
         r = fn()
         print(json.dumps({"only": args.only, **{k: v for k, v in r.items() if k != "kernel_ms"}}), flush=True)
         return
@@ -269,6 +345,10 @@ def main():
         out["conv3x3_bias_relu_fp32"] = bench_conv(200)
     except Exception as e:
         out["conv3x3_bias_relu_fp32"] = {"error": repr(e)}
+    try:
+        out["ops"] = bench_ops(200)
+    except Exception as e:
+        out["ops"] = {"error": repr(e)}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
         try:

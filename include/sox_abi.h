@@ -236,6 +236,86 @@ typedef struct sox_pool_args {
     int32_t flags; /* bit0 relu */
 } sox_pool_args;
 
+/* ---- the rest of the ExecOp surface (Backends/Vulkan/VkGraph.cs:795-1068) ---- */
+
+/* Bilinear resize, half-pixel source coordinates clamped at the borders (bilinear.comp;
+ * Kernels/Nhwc.cs:773-870), out = [relu](lerp) + [relu](add). */
+typedef struct sox_bilinear_args {
+    const void* x;
+    const void* add;
+    void* y;
+    int32_t n, ih, iw, c, oh, ow;
+    float sy, sx;
+    int32_t flags; /* bit0 relu on the resized value, bit1 addend, bit2 relu on the addend */
+} sox_bilinear_args;
+
+/* Rank-4 pad in physical (storage) order (pad.comp): source index o - pb per dim, out of range
+ * -> value (constant) or the reflected index (reflect). */
+typedef struct sox_pad_args {
+    const void* x;
+    void* y;
+    int32_t id[4], od[4], pb[4];
+    int32_t reflect;
+    float value;
+} sox_pad_args;
+
+/* Strided gather, rank <= 6 (transpose.comp / slice.comp; Kernels/Ops.cs:798-883):
+ * y[o] = x[base + sum_k o_k * str[k]], o_k the digits of the output index in od[]. */
+typedef struct sox_gather_args {
+    const void* x;
+    void* y;
+    int64_t count, base;
+    int64_t str[6];
+    int32_t od[6];
+} sox_gather_args;
+
+/* LeakyRelu (0) / Tanh (1, a = in scale, b = out scale) / Clip (2, a = min, b = max) / Erf (3)
+ * (unary2.comp; Kernels/Act.cs:83-147). */
+typedef struct sox_unary2_args {
+    const void* x;
+    void* y;
+    int64_t count;
+    int32_t mode;
+    float a, b;
+} sox_unary2_args;
+
+/* DepthToSpace (s2d = 0) / SpaceToDepth (s2d = 1), NHWC, CRD or DCR (d2s.comp / s2d.comp;
+ * Kernels/Nhwc.Det.cs:210-282). */
+typedef struct sox_d2s_args {
+    const void* x;
+    void* y;
+    int64_t count;
+    int32_t n, ih, iw, ic, oh, ow, oc, block, crd, s2d;
+} sox_d2s_args;
+
+/* Average pool of an NHWC tensor (avgpool.comp; Kernels/Ops.Seq.cs:180-215). */
+typedef struct sox_avgpool_args {
+    const void* x;
+    void* y;
+    int32_t n, ih, iw, c, oh, ow;
+    int32_t kh, kw, sh, sw, pt, pl;
+    int32_t count_include_pad;
+} sox_avgpool_args;
+
+/* GlobalAvgPool finish (gap_sum.comp): y[b][c] = (sum over chunks, in chunk order, of
+ * part[b][chunk][c]) * inv_hw. */
+typedef struct sox_gap_mean_args {
+    const float* part;
+    void* y;
+    int32_t n, c, chunks;
+    float inv_hw;
+} sox_gap_mean_args;
+
+/* Batched MatMul, activation x activation (the gemm.comp matmul route; Kernels/Ops.Seq.cs:92-116):
+ * y[b] = a[b] (m x k) . b[b or 0] (k x n), element strides between batches (b_stride 0 = broadcast). */
+typedef struct sox_matmul_args {
+    const void* a;
+    const void* b;
+    void* y;
+    int32_t batch, m, n, k;
+    int64_t a_stride, b_stride, y_stride;
+} sox_matmul_args;
+
 #ifdef __cplusplus
 }
 #endif

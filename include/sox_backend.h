@@ -77,6 +77,26 @@ typedef struct sox_attention_p {                                             /* 
     int32_t out_layout[4];           /* physical order of the [n,h,t,d] output; all -1 = identity */
 } sox_attention_p;
 
+typedef struct sox_resize_p {                                                /* ResizeP :95-101 */
+    float scales[4];                 /* only [.., sh, sw] used */
+    int32_t fuse_relu, add_relu;     /* relu on the resized value / on the addend In[1] */
+} sox_resize_p;
+typedef struct sox_pad_p {                                                   /* PadP :176-181 */
+    int32_t rank;
+    int32_t pads[12];                /* [2*rank] logical begin.., end.. */
+    int32_t mode;                    /* PadMode: 0 constant, 1 reflect */
+    float value;
+} sox_pad_p;
+typedef struct sox_transpose_p { int32_t rank; int32_t perm[6]; } sox_transpose_p; /* TransposeP :183-186 (physical perm) */
+typedef struct sox_slice_p {                                                 /* SliceP :188-194 (physical axes, resolved starts) */
+    int32_t naxes;
+    int32_t starts[6], ends[6], axes[6], steps[6];
+} sox_slice_p;
+typedef struct sox_leaky_relu_p { float alpha; } sox_leaky_relu_p;           /* LeakyReluP :123-126 */
+typedef struct sox_tanh_p { float in_scale, out_scale; } sox_tanh_p;         /* TanhP :129-133 */
+typedef struct sox_clip_p { float min, max; } sox_clip_p;                    /* ClipP :134-138 */
+typedef struct sox_depth_to_space_p { int32_t block, crd; } sox_depth_to_space_p; /* DepthToSpaceP :139-145 */
+
 /* ---- plan (ExecPlan) ---- */
 int sox_plan_create(sox_plan** plan);
 void sox_plan_destroy(sox_plan* plan);

@@ -270,3 +270,105 @@ def erf_core(x):
 
 def gelu_core(x):
     return lib().ora_gelu_core(float(x))
+
+
+# ---- the rest of the GPU op surface (Engine/Session.cs:178-270, 345-410) ----
+
+def resize_bilinear(x, scale_y, scale_x, add=None, *, relu=False, add_relu=False):
+    """Nhwc.ResizeBilinear (Kernels/Nhwc.cs:773-870), NHWC batch."""
+    x, add = _f32(x), _f32(add)
+    n, ih, iw, c = x.shape
+    oh, ow = int(ih * scale_y), int(iw * scale_x)
+    out = np.empty((n, oh, ow, c), np.float32)
+    for i in range(n):
+        oi = np.empty((oh, ow, c), np.float32)
+        ai = None if add is None else np.ascontiguousarray(add[i])
+        _check(lib().ora_resize_bilinear(_p(np.ascontiguousarray(x[i])), ih, iw, c, _p(oi), oh, ow,
+                                         ctypes.c_float(scale_y), ctypes.c_float(scale_x), int(relu), _p(ai),
+                                         int(add_relu)), "resize_bilinear")
+        out[i] = oi
+    return out
+
+
+def pad_nhwc(x, pad_t, pad_l, pad_b, pad_r, mode=0, value=0.0):
+    """Nhwc.Pad (Kernels/Nhwc.cs:877-900): spatial pad of an NHWC batch, constant (0) or reflect (1)."""
+    x = _f32(x)
+    n, ih, iw, c = x.shape
+    oh, ow = ih + pad_t + pad_b, iw + pad_l + pad_r
+    out = np.empty((n, oh, ow, c), np.float32)
+    for i in range(n):
+        oi = np.empty((oh, ow, c), np.float32)
+        _check(lib().ora_pad_nhwc(_p(np.ascontiguousarray(x[i])), ih, iw, c, _p(oi), oh, ow, pad_t, pad_l, mode,
+                                  ctypes.c_float(value)), "pad")
+        out[i] = oi
+    return out
+
+
+def avg_pool(x, kernel, stride, pads, count_include_pad=False):
+    """Nhwc.AvgPool (Kernels/Ops.Seq.cs:180-215), NHWC batch, pads (t, l, b, r)."""
+    x = _f32(x)
+    n, ih, iw, c = x.shape
+    oh = conv_out_size(ih, kernel[0], stride[0], pads[0], pads[2])
+    ow = conv_out_size(iw, kernel[1], stride[1], pads[1], pads[3])
+    out = np.empty((n, oh, ow, c), np.float32)
+    for i in range(n):
+        oi = np.empty((oh, ow, c), np.float32)
+        _check(lib().ora_avg_pool_nhwc(_p(np.ascontiguousarray(x[i])), ih, iw, c, _p(oi), oh, ow, kernel[0],
+                                       kernel[1], stride[0], stride[1], pads[0], pads[1], int(count_include_pad)),
+               "avg_pool")
+        out[i] = oi
+    return out
+
+
+def depth_to_space(x, block, crd=False, inverse=False):
+    """Nhwc.DepthToSpace / SpaceToDepth (Kernels/Nhwc.Det.cs:210-282), NHWC batch."""
+    x = _f32(x)
+    n, ih, iw, ic = x.shape
+    bb = block * block
+    shape = (n, ih // block, iw // block, ic * bb) if inverse else (n, ih * block, iw * block, ic // bb)
+    out = np.empty(shape, np.float32)
+    for i in range(n):
+        oi = np.empty(shape[1:], np.float32)
+        _check(lib().ora_depth_space(_p(np.ascontiguousarray(x[i])), ih, iw, ic, _p(oi), block, int(crd),
+                                     int(inverse)), "depth_space")
+        out[i] = oi
+    return out
+
+
+UNARY2 = {"LeakyRelu": 0, "Tanh": 1, "Clip": 2, "Erf": 3}
+
+
+def unary2(x, op, a=0.0, b=0.0):
+    """Act.ApplyLeakyRelu / ApplyTanh / ApplyClip / ApplyErf (Kernels/Act.cs:83-147)."""
+    x = _f32(x)
+    out = np.empty_like(x)
+    _check(lib().ora_unary2(_p(x), ctypes.c_long(x.size), UNARY2[op], ctypes.c_float(a), ctypes.c_float(b),
+                            _p(out)), "unary2")
+    return out
+
+
+def transpose(x, perm):
+    """Ops.Transpose (Kernels/Ops.cs:798-868): an index permutation, no arithmetic."""
+    return np.ascontiguousarray(np.transpose(_f32(x), perm))
+
+
+def slice_(x, starts, ends, axes, steps):
+    """Ops.Slice (Kernels/Ops.cs:870-883): a strided gather from resolved starts; no arithmetic."""
+    x = _f32(x)
+    sl = [slice(None)] * x.ndim
+    for s0, e0, a, st in zip(starts, ends, axes, steps):
+        sl[a] = slice(s0, e0 if e0 >= 0 else None, st)
+    return np.ascontiguousarray(x[tuple(sl)])
+
+
+def matmul_bcast(a, b):
+    """Ops.MatMul with B broadcast over A's batch (one B) or matched batches (Kernels/Ops.Seq.cs:92-116)."""
+    a, b = _f32(a), _f32(b)
+    m, k = a.shape[-2:]
+    n = b.shape[-1]
+    batch = a.size // (m * k)
+    bb = b.size // (k * n)
+    a3 = a.reshape(batch, m, k)
+    b3 = np.broadcast_to(b.reshape(bb, k, n), (batch, k, n)) if bb == 1 else b.reshape(batch, k, n)
+    return matmul(a3, np.ascontiguousarray(b3)).reshape(a.shape[:-2] + (m, n))
+

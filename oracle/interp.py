@@ -134,6 +134,29 @@ def run_plan(plan, inputs, keep=False, f16_storage=False):
             v = np.ascontiguousarray(qkv[:, :, 2].transpose(0, 2, 1, 3)).reshape(nb * h, t, d)
             o = O.attention(q, k, v, p.scale).reshape(nb, h, t, d)
             y = np.ascontiguousarray(o.transpose(0, 2, 1, 3))  # stored [N, T, H, D]
+        elif node.op == "ResizeBilinear":
+            x = get(node.ins[0])
+            add = get(node.ins[1]) if len(node.ins) > 1 else None
+            y = O.resize_bilinear(x, p.scales[-2], p.scales[-1], add, relu=p.fuse_relu, add_relu=p.add_relu)
+        elif node.op == "Pad":
+            x = get(node.ins[0])  # NHWC, spatial pads only (Kernels/Nhwc.cs:877-900)
+            r = len(p.pads) // 2
+            assert r == 4 and p.pads[0] == p.pads[1] == p.pads[4] == p.pads[5] == 0
+            y = O.pad_nhwc(x, p.pads[2], p.pads[3], p.pads[6], p.pads[7], p.mode, p.value)
+        elif node.op == "Transpose":
+            y = O.transpose(get(node.ins[0]), p.perm)
+        elif node.op == "Slice":
+            y = O.slice_(get(node.ins[0]), p.starts, p.ends, p.axes, p.steps)
+        elif node.op in ("LeakyRelu", "Tanh", "Clip", "Erf"):
+            y = O.unary2(get(node.ins[0]), node.op, *((p.a, p.b) if p is not None else (0.0, 0.0)))
+        elif node.op in ("DepthToSpace", "SpaceToDepth"):
+            y = O.depth_to_space(get(node.ins[0]), p.block, p.crd, node.op == "SpaceToDepth")
+        elif node.op == "AvgPool":
+            y = O.avg_pool(get(node.ins[0]), p.kernel, p.strides, p.pads, p.count_include_pad)
+        elif node.op == "GlobalAvgPool":
+            y = O.global_avg_pool(get(node.ins[0]))
+        elif node.op == "MatMul":
+            y = O.matmul_bcast(get(node.ins[0]), get(node.ins[1]))
         else:
             raise NotImplementedError(f"oracle interpreter: {node.op}")
         env[out] = rnd(np.ascontiguousarray(y, dtype=np.float32).reshape(oshape))

@@ -114,6 +114,21 @@ float ora_act(float x, int act);
 /* IEEE binary16 round-to-nearest-even (the (Half) cast of Engine/Extensions.cs:315). */
 void ora_round_f16(const float* src, float* dst, long count);
 
+/* Nhwc.ResizeBilinear (Kernels/Nhwc.cs:773-870), one image: half-pixel coordinates clamped at the
+ * borders; out = [relu](lerp) + [relu](add) (add nullable). */
+int ora_resize_bilinear(const float* src, int ih, int iw, int c, float* dst, int oh, int ow, float sy, float sx,
+                        int relu, const float* add, int add_relu);
+/* Nhwc.Pad (Kernels/Nhwc.cs:877-900), spatial, one image; mode 0 constant, 1 reflect. */
+int ora_pad_nhwc(const float* src, int ih, int iw, int c, float* dst, int oh, int ow, int pad_t, int pad_l,
+                 int mode, float value);
+/* Nhwc.AvgPool (Kernels/Ops.Seq.cs:180-215), one image. */
+int ora_avg_pool_nhwc(const float* src, int ih, int iw, int c, float* dst, int oh, int ow, int kh, int kw, int sh,
+                      int sw, int pad_t, int pad_l, int count_include_pad);
+/* Nhwc.DepthToSpace (dir 0) / SpaceToDepth (dir 1), NHWC, one image (Kernels/Nhwc.Det.cs:210-282). */
+int ora_depth_space(const float* src, int ih, int iw, int ic, float* dst, int b, int crd, int dir);
+/* LeakyRelu (0) / Tanh (1) / Clip (2) / Erf (3) (Kernels/Act.cs:83-147). */
+int ora_unary2(const float* src, long count, int mode, float a, float b, float* dst);
+
 #ifdef __cplusplus
 }
 #endif

@@ -885,4 +885,140 @@ void ora_round_f16(const float* src, float* dst, long count) {
     for (long i = 0; i < count; i++) dst[i] = round_f16(src[i]);
 }
 
+
+// ---------------------------------------------------------------------------------------------
+// The rest of the GPU op surface (the ExecOp cases of Backends/Vulkan/VkGraph.cs:795-1068) as the
+// CPU engine computes them (Engine/Session.cs:178-270, 345-410).
+// ---------------------------------------------------------------------------------------------
+
+// Nhwc.ResizeAxis (Kernels/Nhwc.cs:773-783): half-pixel source coordinate, both taps clamped.
+static void resize_axis(int out_len, int in_len, float scale, int* i0, int* i1, float* wt) {
+    for (int o = 0; o < out_len; o++) {
+        float f = (o + 0.5f) / scale - 0.5f;
+        float fl = floorf(f);
+        i0[o] = std::min(std::max((int)fl, 0), in_len - 1);
+        i1[o] = std::min(std::max((int)fl + 1, 0), in_len - 1);
+        wt[o] = f - fl;
+    }
+}
+
+int ora_resize_bilinear(const float* src, int ih, int iw, int c, float* dst, int oh, int ow, float sy, float sx,
+                        int relu, const float* add, int add_relu) {
+    std::vector<int> y0(oh), y1(oh), x0(ow), x1(ow);
+    std::vector<float> wy(oh), wx(ow);
+    resize_axis(oh, ih, sy, y0.data(), y1.data(), wy.data());
+    resize_axis(ow, iw, sx, x0.data(), x1.data(), wx.data());
+#pragma omp parallel for schedule(static) num_threads(threads())
+    for (int y = 0; y < oh; y++) {
+        const float* r0 = src + (long)y0[y] * iw * c;
+        const float* r1 = src + (long)y1[y] * iw * c;
+        for (int x = 0; x < ow; x++) {
+            const float *a = r0 + (long)x0[x] * c, *b = r0 + (long)x1[x] * c;
+            const float *e = r1 + (long)x0[x] * c, *f = r1 + (long)x1[x] * c;
+            long ob = ((long)y * ow + x) * c;
+            for (int ch = 0; ch < c; ch++) {  // Nhwc.ResizePixel (Kernels/Nhwc.cs:788-814)
+                float top = a[ch] + (b[ch] - a[ch]) * wx[x];
+                float bot = e[ch] + (f[ch] - e[ch]) * wx[x];
+                float v = top + (bot - top) * wy[y];
+                if (relu) v = fmaxf(v, 0.0f);
+                if (add) v += add_relu ? fmaxf(add[ob + ch], 0.0f) : add[ob + ch];
+                dst[ob + ch] = v;
+            }
+        }
+    }
+    return 0;
+}
+
+// Nhwc.Pad (Kernels/Nhwc.cs:877-900): spatial pad of one NHWC image; mode 0 constant, 1 reflect.
+int ora_pad_nhwc(const float* src, int ih, int iw, int c, float* dst, int oh, int ow, int pad_t, int pad_l,
+                 int mode, float value) {
+    std::vector<int> rm = make_map(oh, 1, 1, pad_t, ih, mode), cm = make_map(ow, 1, 1, pad_l, iw, mode);
+    for (int y = 0; y < oh; y++)
+        for (int x = 0; x < ow; x++) {
+            float* o = dst + ((long)y * ow + x) * c;
+            if (rm[y] < 0 || cm[x] < 0)
+                for (int ch = 0; ch < c; ch++) o[ch] = value;
+            else
+                memcpy(o, src + ((long)rm[y] * iw + cm[x]) * c, sizeof(float) * c);
+        }
+    return 0;
+}
+
+// Nhwc.AvgPool (Kernels/Ops.Seq.cs:180-215): taps summed in (ky, kx) order, then one multiply by
+// 1 / count (kh*kw with count_include_pad, else the in-bounds taps).
+int ora_avg_pool_nhwc(const float* src, int ih, int iw, int c, float* dst, int oh, int ow, int kh, int kw, int sh,
+                      int sw, int pad_t, int pad_l, int count_include_pad) {
+    std::vector<int> rm = make_map(oh, kh, sh, pad_t, ih, 0), cm = make_map(ow, kw, sw, pad_l, iw, 0);
+#pragma omp parallel for schedule(static) num_threads(threads())
+    for (int y = 0; y < oh; y++)
+        for (int x = 0; x < ow; x++) {
+            float* o = dst + ((long)y * ow + x) * c;
+            for (int ch = 0; ch < c; ch++) o[ch] = 0.0f;
+            int cnt = 0;
+            for (int ky = 0; ky < kh; ky++) {
+                int r = rm[(long)y * kh + ky];
+                if (r < 0) continue;
+                for (int kx = 0; kx < kw; kx++) {
+                    int cc = cm[(long)x * kw + kx];
+                    if (cc < 0) continue;
+                    const float* s = src + ((long)r * iw + cc) * c;
+                    for (int ch = 0; ch < c; ch++) o[ch] += s[ch];
+                    cnt++;
+                }
+            }
+            float inv = 1.0f / (count_include_pad ? kh * kw : std::max(cnt, 1));
+            for (int ch = 0; ch < c; ch++) o[ch] *= inv;
+        }
+    return 0;
+}
+
+// Nhwc.DepthToSpace / SpaceToDepth, NHWC (Kernels/Nhwc.Det.cs:210-282). dir 0: depth-to-space
+// (src [ih][iw][ic] -> [ih*b][iw*b][ic/b^2]), 1: space-to-depth ([ih][iw][ic] -> [ih/b][iw/b][ic*b^2]).
+int ora_depth_space(const float* src, int ih, int iw, int ic, float* dst, int b, int crd, int dir) {
+    const int bb = b * b;
+    if (dir == 0) {
+        const int oc = ic / bb, oh = ih * b, ow = iw * b;
+        for (int y = 0; y < oh; y++)
+            for (int x = 0; x < ow; x++) {
+                const float* s = src + ((long)(y / b) * iw + x / b) * ic;
+                float* o = dst + ((long)y * ow + x) * oc;
+                const int sub = (y % b) * b + x % b;
+                for (int ch = 0; ch < oc; ch++) o[ch] = crd ? s[ch * bb + sub] : s[(long)sub * oc + ch];
+            }
+    } else {
+        const int oc = ic * bb, oh = ih / b, ow = iw / b;
+        for (int y = 0; y < oh; y++)
+            for (int x = 0; x < ow; x++) {
+                float* o = dst + ((long)y * ow + x) * oc;
+                for (int sub = 0; sub < bb; sub++) {
+                    const float* s = src + ((long)(y * b + sub / b) * iw + x * b + sub % b) * ic;
+                    for (int ch = 0; ch < ic; ch++) {
+                        if (crd) o[ch * bb + sub] = s[ch];
+                        else o[(long)sub * ic + ch] = s[ch];
+                    }
+                }
+            }
+    }
+    return 0;
+}
+
+// Act.ApplyLeakyRelu / ApplyTanh / ApplyClip / ApplyErf (Kernels/Act.cs:83-147), the vector forms:
+// mode 0 leaky (max(x, a x) for a <= 1, else min), 1 tanh = 2o sigmoid(2i x) - o with the Cephes
+// sigmoid core (a = i, b = o), 2 clip min(max(x, a), b), 3 erf (A&S 7.1.26 core).
+int ora_unary2(const float* src, long count, int mode, float a, float b, float* dst) {
+#pragma omp parallel for schedule(static) num_threads(threads())
+    for (long i = 0; i < count; i++) {
+        const float x = src[i];
+        float y;
+        switch (mode) {
+            case 0: y = a <= 1.0f ? fmaxf(x, x * a) : fminf(x, x * a); break;
+            case 1: y = sigmoid_core(x * (2.0f * a)) * (2.0f * b) - b; break;
+            case 2: y = fminf(fmaxf(x, a), b); break;
+            default: y = erf_core(x); break;
+        }
+        dst[i] = y;
+    }
+    return 0;
+}
+
 }  // extern "C"

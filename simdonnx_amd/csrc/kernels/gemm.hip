@@ -5,6 +5,7 @@
 SOX_GEMM(sox_gemm_f16_256x192_k32s5, 256, 192, 32, 128, 96, 5, 4, 1, 4)
 SOX_GEMM(sox_gemm_f16_256x192_k32s4, 256, 192, 32, 128, 96, 4, 4, 1, 4)
 SOX_GEMM_E(sox_gemm_f16_256x192_w8k64s2, 256, 192, 64, 64, 96, 2, 8, 1, 4)
+SOX_GEMM_E(sox_gemm_f16_128x192_k32s3, 128, 192, 32, 64, 96, 3, 4, 2, 4)
 SOX_GEMM(sox_gemm_f16_256x256_w8k32s4, 256, 256, 32, 128, 64, 4, 8, 1, 4)
 SOX_GEMM(sox_gemm_f16_256x256_w8k64s2, 256, 256, 64, 128, 64, 2, 8, 1, 4)
 SOX_GEMM(sox_gemm_f16_256x128_k32s3, 256, 128, 32, 128, 64, 3, 4, 2, 4)

@@ -1,0 +1,315 @@
+// The rest of the ExecOp surface on gfx950 (the cases of Backends/Vulkan/VkGraph.cs:795-1068):
+// bilinear resize, pad, transpose / slice (one strided gather), LeakyRelu / Tanh / Clip / Erf,
+// DepthToSpace / SpaceToDepth, average pool, global average pool and batched MatMul.
+//
+// All of them move bytes rather than multiply: one work item per output element or per 16-byte
+// channel vector of an NHWC pixel (when the channel count allows), fp32 math, fp16 or fp32 storage.
+// Index arithmetic is 32-bit; the launchers reject tensors past 2^31 elements.
+#include "sox_device.h"
+
+template <typename T, int CV> struct Vt {
+    typedef T V __attribute__((ext_vector_type(CV)));
+};
+
+SOX_DEV long gid() { return (long)blockIdx.x * blockDim.x + threadIdx.x; }
+
+// ------------------------------------------------------------------------------------------
+// Bilinear resize (Kernels/Nhwc.cs:773-870): per axis f = (o + 0.5) / scale - 0.5, taps floor(f)
+// and floor(f) + 1 clamped to the image, weight f - floor(f); v = top + (bot - top) wy with
+// top/bot = a + (b - a) wx; [relu]; + [relu](addend). No contraction, so the per-element operations
+// are the CPU's.
+// ------------------------------------------------------------------------------------------
+template <typename T, int CV>
+__device__ __forceinline__ void bilinear_body(const sox_bilinear_args& p) {
+#pragma clang fp contract(off)
+    typedef typename Vt<T, CV>::V Vec;
+    const int cvn = p.c / CV;
+    const long idx = gid();
+    if (idx >= (long)p.n * p.oh * p.ow * cvn) return;
+    const int c0 = (int)(idx % cvn) * CV;
+    const long pix = idx / cvn;
+    const int ox = (int)(pix % p.ow);
+    const int q = (int)(pix / p.ow), oy = q % p.oh, b = q / p.oh;
+    const float fy = ((float)oy + 0.5f) / p.sy - 0.5f, fx = ((float)ox + 0.5f) / p.sx - 0.5f;
+    const float fly = floorf(fy), flx = floorf(fx);
+    const int y0 = min(max((int)fly, 0), p.ih - 1), y1 = min(max((int)fly + 1, 0), p.ih - 1);
+    const int x0 = min(max((int)flx, 0), p.iw - 1), x1 = min(max((int)flx + 1, 0), p.iw - 1);
+    const float wy = fy - fly, wx = fx - flx;
+    const T* img = (const T*)p.x + (long)b * p.ih * p.iw * p.c + c0;
+    const Vec va = *(const Vec*)(img + ((long)y0 * p.iw + x0) * p.c);
+    const Vec vb = *(const Vec*)(img + ((long)y0 * p.iw + x1) * p.c);
+    const Vec ve = *(const Vec*)(img + ((long)y1 * p.iw + x0) * p.c);
+    const Vec vf = *(const Vec*)(img + ((long)y1 * p.iw + x1) * p.c);
+    Vec vadd;
+    if (p.flags & 2) vadd = *(const Vec*)((const T*)p.add + pix * p.c + c0);
+    Vec out;
+#pragma unroll
+    for (int e = 0; e < CV; e++) {
+        const float a = to_f(va[e]), bb = to_f(vb[e]), ee = to_f(ve[e]), ff = to_f(vf[e]);
+        const float top = a + (bb - a) * wx;
+        const float bot = ee + (ff - ee) * wx;
+        float v = top + (bot - top) * wy;
+        if (p.flags & 1) v = fmaxf(v, 0.0f);
+        if (p.flags & 2) {
+            const float s = to_f(vadd[e]);
+            v += (p.flags & 4) ? fmaxf(s, 0.0f) : s;
+        }
+        out[e] = (T)v;
+    }
+    *(Vec*)((T*)p.y + pix * p.c + c0) = out;
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_bilinear_f16_v(sox_bilinear_args p) { bilinear_body<half_t, 8>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_bilinear_f16_s(sox_bilinear_args p) { bilinear_body<half_t, 1>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_bilinear_f32_v(sox_bilinear_args p) { bilinear_body<float, 4>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_bilinear_f32_s(sox_bilinear_args p) { bilinear_body<float, 1>(p); }
+
+// ------------------------------------------------------------------------------------------
+// Rank-4 pad in storage order (Kernels/Nhwc.cs:877-900 for the NHWC spatial case): source index
+// o - pb per dim; outside -> the constant, or the reflected index (Nhwc.Reflect, no edge repeat).
+// CV > 1 only when the innermost dim is unpadded and a multiple of CV (the launcher checks).
+// ------------------------------------------------------------------------------------------
+template <typename T, int CV>
+__device__ __forceinline__ void pad_body(const sox_pad_args& p) {
+    typedef typename Vt<T, CV>::V Vec;
+    const int d3v = p.od[3] / CV;
+    const long idx = gid();
+    if (idx >= (long)p.od[0] * p.od[1] * p.od[2] * d3v) return;
+    int s3 = (int)(idx % d3v) * CV;
+    int r = (int)(idx / d3v);
+    int s2 = r % p.od[2];
+    r /= p.od[2];
+    int s1 = r % p.od[1], s0 = r / p.od[1];
+    int s[4] = {s0 - p.pb[0], s1 - p.pb[1], s2 - p.pb[2], s3 - p.pb[3]};
+    bool inside = true;
+#pragma unroll
+    for (int d = 0; d < 4; d++)
+        if ((unsigned)s[d] >= (unsigned)p.id[d]) {
+            if (p.reflect) s[d] = sox_reflect(s[d], p.id[d]);
+            else inside = false;
+        }
+    Vec v;
+    if (inside) {
+        v = *(const Vec*)((const T*)p.x + (((long)s[0] * p.id[1] + s[1]) * p.id[2] + s[2]) * p.id[3] + s[3]);
+    } else {
+#pragma unroll
+        for (int e = 0; e < CV; e++) v[e] = (T)p.value;
+    }
+    *(Vec*)((T*)p.y + idx * CV) = v;
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_pad_f16_v(sox_pad_args p) { pad_body<half_t, 8>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_pad_f16_s(sox_pad_args p) { pad_body<half_t, 1>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_pad_f32_v(sox_pad_args p) { pad_body<float, 4>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_pad_f32_s(sox_pad_args p) { pad_body<float, 1>(p); }
+
+// ------------------------------------------------------------------------------------------
+// Strided gather (Transpose, Slice; Kernels/Ops.cs:798-883): the output index's digits over od[]
+// (innermost last) times the per-dim source strides, from base. The launcher checks that every
+// source offset stays inside the input.
+// ------------------------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void gather_body(const sox_gather_args& p) {
+    const long idx = gid();
+    if (idx >= p.count) return;
+    unsigned r = (unsigned)idx;
+    long off = p.base;
+#pragma unroll
+    for (int k = 5; k >= 0; k--) {
+        const unsigned d = (unsigned)p.od[k];
+        const unsigned o = r % d;
+        r /= d;
+        off += (long)o * p.str[k];
+    }
+    ((T*)p.y)[idx] = ((const T*)p.x)[off];
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_gather_f16(sox_gather_args p) { gather_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_gather_f32(sox_gather_args p) { gather_body<float>(p); }
+
+// ------------------------------------------------------------------------------------------
+// LeakyRelu / Tanh / Clip / Erf (Kernels/Act.cs:83-147, the vector forms): leaky = max(x, a x)
+// for a <= 1 else min(x, a x); o tanh(i x) = 2o sigmoid(2i x) - o with the Cephes sigmoid;
+// clip = min(max(x, lo), hi); erf = A&S 7.1.26.
+// ------------------------------------------------------------------------------------------
+SOX_DEV float unary2_op(float x, int mode, float a, float b) {
+#pragma clang fp contract(off)
+    switch (mode) {
+        case 0: return a <= 1.0f ? fmaxf(x, x * a) : fminf(x, x * a);
+        case 1: return sox_sigmoid(x * (2.0f * a)) * (2.0f * b) - b;
+        case 2: return fminf(fmaxf(x, a), b);
+        default: return sox_erf(x);
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ void unary2_body(const sox_unary2_args& p) {
+    constexpr int CV = 16 / sizeof(T);
+    typedef typename Vt<T, CV>::V Vec;
+    const long base = gid() * CV;
+    const T* x = (const T*)p.x;
+    T* y = (T*)p.y;
+    if (base + CV <= p.count) {
+        const Vec xv = *(const Vec*)(x + base);
+        Vec out;
+#pragma unroll
+        for (int e = 0; e < CV; e++) out[e] = (T)unary2_op(to_f(xv[e]), p.mode, p.a, p.b);
+        *(Vec*)(y + base) = out;
+    } else {
+        for (long i = base; i < p.count; i++) y[i] = (T)unary2_op(to_f(x[i]), p.mode, p.a, p.b);
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_unary2_f16(sox_unary2_args p) { unary2_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_unary2_f32(sox_unary2_args p) { unary2_body<float>(p); }
+
+// ------------------------------------------------------------------------------------------
+// DepthToSpace / SpaceToDepth, NHWC (Kernels/Nhwc.Det.cs:210-282). Depth-to-space: output (y, x, c)
+// reads input (y / b, x / b) channel c b^2 + sub (CRD) or sub oc + c (DCR), sub = (y % b) b + x % b.
+// Space-to-depth is the inverse: output channel c' = c b^2 + sub (CRD) or sub ic + c (DCR) reads
+// input (y b + sub / b, x b + sub % b) channel c. One work item per output element; consecutive
+// items are consecutive output channels (coalesced stores).
+// ------------------------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void d2s_body(const sox_d2s_args& p) {
+    const long idx = gid();
+    if (idx >= p.count) return;
+    const int bk = p.block, bb = bk * bk;
+    const int ch = (int)(idx % p.oc);
+    const int pix = (int)(idx / p.oc);
+    const int ox = pix % p.ow, q = pix / p.ow, oy = q % p.oh, b = q / p.oh;
+    int sy, sx, sc;
+    if (!p.s2d) {
+        const int sub = (oy % bk) * bk + ox % bk;
+        sy = oy / bk;
+        sx = ox / bk;
+        sc = p.crd ? ch * bb + sub : sub * p.oc + ch;
+    } else {
+        const int sub = p.crd ? ch % bb : ch / p.ic;
+        sc = p.crd ? ch / bb : ch % p.ic;
+        sy = oy * bk + sub / bk;
+        sx = ox * bk + sub % bk;
+    }
+    ((T*)p.y)[idx] = ((const T*)p.x)[(((long)b * p.ih + sy) * p.iw + sx) * p.ic + sc];
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_d2s_f16(sox_d2s_args p) { d2s_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_d2s_f32(sox_d2s_args p) { d2s_body<float>(p); }
+
+// ------------------------------------------------------------------------------------------
+// Average pool, NHWC (Kernels/Ops.Seq.cs:180-215): taps summed in (ky, kx) order from zero, then
+// one multiply by 1 / count, count = kh kw (count_include_pad) or the in-bounds taps.
+// ------------------------------------------------------------------------------------------
+template <typename T, int CV>
+__device__ __forceinline__ void avgpool_body(const sox_avgpool_args& p) {
+    typedef typename Vt<T, CV>::V Vec;
+    const int cvn = p.c / CV;
+    const long idx = gid();
+    if (idx >= (long)p.n * p.oh * p.ow * cvn) return;
+    const int c0 = (int)(idx % cvn) * CV;
+    const int pix = (int)(idx / cvn);
+    const int ox = pix % p.ow, q = pix / p.ow, oy = q % p.oh, b = q / p.oh;
+    const T* img = (const T*)p.x + (long)b * p.ih * p.iw * p.c + c0;
+    float acc[CV];
+#pragma unroll
+    for (int e = 0; e < CV; e++) acc[e] = 0.0f;
+    int cnt = 0;
+    for (int ky = 0; ky < p.kh; ky++) {
+        const int iy = oy * p.sh + ky - p.pt;
+        if ((unsigned)iy >= (unsigned)p.ih) continue;
+        for (int kx = 0; kx < p.kw; kx++) {
+            const int ix = ox * p.sw + kx - p.pl;
+            if ((unsigned)ix >= (unsigned)p.iw) continue;
+            const Vec v = *(const Vec*)(img + ((long)iy * p.iw + ix) * p.c);
+#pragma unroll
+            for (int e = 0; e < CV; e++) acc[e] += to_f(v[e]);
+            cnt++;
+        }
+    }
+    const float inv = 1.0f / (float)(p.count_include_pad ? p.kh * p.kw : max(cnt, 1));
+    Vec out;
+#pragma unroll
+    for (int e = 0; e < CV; e++) out[e] = (T)(acc[e] * inv);
+    *(Vec*)((T*)p.y + (long)pix * p.c + c0) = out;
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_avgpool_f16_v(sox_avgpool_args p) { avgpool_body<half_t, 8>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_avgpool_f16_s(sox_avgpool_args p) { avgpool_body<half_t, 1>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_avgpool_f32_v(sox_avgpool_args p) { avgpool_body<float, 4>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_avgpool_f32_s(sox_avgpool_args p) { avgpool_body<float, 1>(p); }
+
+// ------------------------------------------------------------------------------------------
+// GlobalAvgPool finish (gap_sum.comp): the GAP partial kernel's per-chunk channel sums, added in
+// chunk order, times 1 / hw.
+// ------------------------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void gap_mean_body(const sox_gap_mean_args& p) {
+    const long idx = gid();
+    if (idx >= (long)p.n * p.c) return;
+    const int b = (int)(idx / p.c), ch = (int)(idx % p.c);
+    const float* part = p.part + (long)b * p.chunks * p.c + ch;
+    float s = 0.0f;
+    for (int k = 0; k < p.chunks; k++) s += part[(long)k * p.c];
+    ((T*)p.y)[idx] = (T)(s * p.inv_hw);
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_gap_mean_f16(sox_gap_mean_args p) { gap_mean_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_gap_mean_f32(sox_gap_mean_args p) { gap_mean_body<float>(p); }
+
+// ------------------------------------------------------------------------------------------
+// Batched MatMul of two activations (Kernels/Ops.Seq.cs:92-116): y[b] = a[b] . b[b or 0], fp32
+// accumulation in ascending k, one fma each. 64 x 64 output tile per 256-thread workgroup (4 x 4
+// per thread), 16-deep k slices staged in LDS as fp32 ([k][m] and [k][n], so each thread reads
+// its 4 rows / 4 columns as one 16-byte LDS read). Grid (ceil(n / 64), ceil(m / 64), batch).
+// ------------------------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void matmul_body(const sox_matmul_args& p) {
+    __shared__ __attribute__((aligned(16))) float As[16][64];
+    __shared__ __attribute__((aligned(16))) float Bs[16][64];
+    const int t = threadIdx.x, tm = t / 16, tn = t % 16;
+    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64, bz = blockIdx.z;
+    const T* __restrict__ A = (const T*)p.a + bz * p.a_stride;
+    const T* __restrict__ B = (const T*)p.b + bz * p.b_stride;
+    T* __restrict__ Y = (T*)p.y + bz * p.y_stride;
+    float acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = 0.0f;
+    for (int k0 = 0; k0 < p.k; k0 += 16) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int e = t + 256 * i;
+            const int ar = e / 16, ak = e % 16;  // A: 64 rows x 16 k, k fastest (row-contiguous reads)
+            const int gm = m0 + ar, gk = k0 + ak;
+            As[ak][ar] = (gm < p.m && gk < p.k) ? to_f(A[(long)gm * p.k + gk]) : 0.0f;
+            const int bk = e / 64, bn = e % 64;  // B: 16 k x 64 columns, columns fastest
+            const int gk2 = k0 + bk, gn = n0 + bn;
+            Bs[bk][bn] = (gk2 < p.k && gn < p.n) ? to_f(B[(long)gk2 * p.n + gn]) : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < 16; kk++) {
+            const float4v a4 = *(const float4v*)&As[kk][tm * 4];
+            const float4v b4 = *(const float4v*)&Bs[kk][tn * 4];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] = __builtin_fmaf(a4[i], b4[j], acc[i][j]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int gm = m0 + tm * 4 + i;
+        if (gm >= p.m) continue;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int gn = n0 + tn * 4 + j;
+            if (gn < p.n) Y[(long)gm * p.n + gn] = (T)acc[i][j];
+        }
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_matmul_f16(sox_matmul_args p) { matmul_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_matmul_f32(sox_matmul_args p) { matmul_body<float>(p); }

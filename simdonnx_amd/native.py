@@ -87,6 +87,39 @@ class AttentionP(ctypes.Structure):
                 ("out_layout", c_int32 * 4)]
 
 
+class ResizeP(ctypes.Structure):
+    _fields_ = [("scales", c_float * 4), ("fuse_relu", c_int32), ("add_relu", c_int32)]
+
+
+class PadP(ctypes.Structure):
+    _fields_ = [("rank", c_int32), ("pads", c_int32 * 12), ("mode", c_int32), ("value", c_float)]
+
+
+class TransposeP(ctypes.Structure):
+    _fields_ = [("rank", c_int32), ("perm", c_int32 * 6)]
+
+
+class SliceP(ctypes.Structure):
+    _fields_ = [("naxes", c_int32), ("starts", c_int32 * 6), ("ends", c_int32 * 6), ("axes", c_int32 * 6),
+                ("steps", c_int32 * 6)]
+
+
+class LeakyReluP(ctypes.Structure):
+    _fields_ = [("alpha", c_float)]
+
+
+class TanhP(ctypes.Structure):
+    _fields_ = [("in_scale", c_float), ("out_scale", c_float)]
+
+
+class ClipP(ctypes.Structure):
+    _fields_ = [("min", c_float), ("max", c_float)]
+
+
+class DepthToSpaceP(ctypes.Structure):
+    _fields_ = [("block", c_int32), ("crd", c_int32)]
+
+
 class Bind(ctypes.Structure):
     _fields_ = [("slot", c_int32), ("pad_", c_int32), ("offset", c_uint64), ("size", c_uint64)]
 

@@ -192,6 +192,7 @@ class PoolP:
     strides: tuple
     pads: tuple
     relu: bool = False
+    count_include_pad: bool = False
 
     def native(self):
         p = N.PoolP()
@@ -199,7 +200,91 @@ class PoolP:
         p.strides[:] = list(self.strides)
         p.pads[:] = list(self.pads)
         p.fuse_relu = int(self.relu)
+        p.count_include_pad = int(self.count_include_pad)
         return p
+
+
+@dataclass
+class ResizeP:
+    """ResizeP (ExecPlan.cs:95-101): bilinear; out = [relu](resize(x)) + [relu](In[1])."""
+    scales: tuple
+    fuse_relu: bool = False
+    add_relu: bool = False
+
+    def native(self):
+        p = N.ResizeP()
+        p.scales[:] = list(self.scales)
+        p.fuse_relu, p.add_relu = int(self.fuse_relu), int(self.add_relu)
+        return p
+
+
+@dataclass
+class PadP:
+    """PadP (ExecPlan.cs:176-181): logical [2*rank] begin.., end.. pads, constant or reflect."""
+    pads: tuple
+    mode: int = 0
+    value: float = 0.0
+
+    def native(self):
+        p = N.PadP()
+        p.rank = len(self.pads) // 2
+        p.pads[:len(self.pads)] = list(self.pads)
+        p.mode, p.value = self.mode, self.value
+        return p
+
+
+@dataclass
+class TransposeP:
+    """TransposeP (ExecPlan.cs:183-186), a physical permutation."""
+    perm: tuple
+
+    def native(self):
+        p = N.TransposeP()
+        p.rank = len(self.perm)
+        p.perm[:len(self.perm)] = list(self.perm)
+        return p
+
+
+@dataclass
+class SliceP:
+    """SliceP (ExecPlan.cs:188-194), physical axes, starts already clamped."""
+    starts: tuple
+    ends: tuple
+    axes: tuple
+    steps: tuple
+
+    def native(self):
+        p = N.SliceP()
+        k = len(self.axes)
+        p.naxes = k
+        p.starts[:k], p.ends[:k], p.axes[:k], p.steps[:k] = (list(self.starts), list(self.ends), list(self.axes),
+                                                               list(self.steps))
+        return p
+
+
+@dataclass
+class ScalarP:
+    """LeakyReluP (alpha), TanhP (in_scale, out_scale), ClipP (min, max) (ExecPlan.cs:123-138)."""
+    kind: str
+    a: float = 0.0
+    b: float = 0.0
+
+    def native(self):
+        if self.kind == "LeakyRelu":
+            return N.LeakyReluP(self.a)
+        if self.kind == "Tanh":
+            return N.TanhP(self.a, self.b)
+        return N.ClipP(self.a, self.b)
+
+
+@dataclass
+class DepthToSpaceP:
+    """DepthToSpaceP (ExecPlan.cs:139-145)."""
+    block: int
+    crd: bool = False
+
+    def native(self):
+        return N.DepthToSpaceP(self.block, int(self.crd))
 
 
 @dataclass
@@ -462,6 +547,75 @@ class PlanBuilder:
         self._node("Attention", [view, view, view], [y], p, name)
         # [N, T, H*D] token view of the output (its transpose dissolved into the layout)
         return self.alias(y, (nb, t, heads * head_dim), None, name + ".tokens")
+
+    def resize_bilinear(self, x, scale, add=None, *, relu=False, add_relu=False, name=""):
+        """Bilinear x`scale` resize (+ [relu]) (+ [relu] same-shape addend) (ResizeP)."""
+        n, h, w, c = self.values[x].phys
+        oh, ow = int(h * scale), int(w * scale)
+        y = self.image(n, c, oh, ow, name)
+        ins = [x] if add is None else [x, add]
+        return self._node("ResizeBilinear", ins, [y], ResizeP((1.0, 1.0, float(scale), float(scale)), relu, add_relu),
+                          name)
+
+    def pad(self, x, pads, mode=0, value=0.0, name=""):
+        """Pad with logical [2*rank] pads (begin.., end..) (PadP)."""
+        v = self.values[x]
+        r = len(v.shape)
+        shape = tuple(v.shape[d] + pads[d] + pads[r + d] for d in range(r))
+        y = self.activation(shape, v.layout, name)
+        return self._node("Pad", [x], [y], PadP(tuple(pads), mode, value), name)
+
+    def transpose(self, x, perm, name=""):
+        """Transpose of an identity-layout value (TransposeP; the perm is then also physical)."""
+        v = self.values[x]
+        assert v.layout is None
+        y = self.activation(tuple(v.shape[p] for p in perm), None, name)
+        return self._node("Transpose", [x], [y], TransposeP(tuple(perm)), name)
+
+    def slice(self, x, starts, ends, axes, steps, name=""):
+        """Slice of an identity-layout value with resolved (clamped) starts / ends (SliceP)."""
+        v = self.values[x]
+        assert v.layout is None
+        shape = list(v.shape)
+        for s0, e0, a, st in zip(starts, ends, axes, steps):
+            shape[a] = max(0, (e0 - s0 + (st - (1 if st > 0 else -1))) // st)
+        y = self.activation(tuple(shape), None, name)
+        return self._node("Slice", [x], [y], SliceP(tuple(starts), tuple(ends), tuple(axes), tuple(steps)), name)
+
+    def scalar_act(self, op, x, a=0.0, b=0.0, name=""):
+        """LeakyRelu (a = alpha) / Tanh (a = in scale, b = out scale) / Clip (a = min, b = max) / Erf."""
+        val = self.values[x]
+        y = self.activation(val.shape, val.layout, name)
+        return self._node(op, [x], [y], None if op == "Erf" else ScalarP(op, a, b), name)
+
+    def depth_to_space(self, x, block, crd=False, inverse=False, name=""):
+        """DepthToSpace (or SpaceToDepth with inverse=True) of an NHWC image (DepthToSpaceP)."""
+        n, h, w, c = self.values[x].phys
+        if inverse:
+            y = self.image(n, c * block * block, h // block, w // block, name)
+        else:
+            y = self.image(n, c // (block * block), h * block, w * block, name)
+        return self._node("SpaceToDepth" if inverse else "DepthToSpace", [x], [y], DepthToSpaceP(block, crd), name)
+
+    def avg_pool(self, x, kernel, stride, pads, count_include_pad=False, name=""):
+        """AveragePool of an NHWC image, pads (t, l, b, r) (PoolP)."""
+        n, h, w, c = self.values[x].phys
+        oh = _out_size(h, kernel[0], stride[0], pads[0], pads[2])
+        ow = _out_size(w, kernel[1], stride[1], pads[1], pads[3])
+        y = self.image(n, c, oh, ow, name)
+        return self._node("AvgPool", [x], [y], PoolP(tuple(kernel), tuple(stride), tuple(pads), False,
+                                                    count_include_pad), name)
+
+    def global_avg_pool(self, x, name=""):
+        n, h, w, c = self.values[x].phys
+        y = self.image(n, c, 1, 1, name)
+        return self._node("GlobalAvgPool", [x], [y], None, name)
+
+    def matmul(self, a, b, name=""):
+        """Batched MatMul [.., M, K] x [.., K, N] (B may have one batch), identity layouts."""
+        va, vb = self.values[a], self.values[b]
+        y = self.activation(tuple(va.shape[:-1]) + (vb.shape[-1],), None, name)
+        return self._node("MatMul", [a, b], [y], None, name)
 
     def ext(self, name, ins, out_shape, params: bytes = b"", layout=None, node_name=""):
         """ExecOp.Ext node of a consumer-registered operator."""

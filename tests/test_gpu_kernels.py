@@ -418,7 +418,7 @@ GEMM_KERNELS = ["sox_gemm_f16_256x192_k32s5", "sox_gemm_f16_256x128_w8k64s2", "s
                 "sox_gemm_f16_128x64_k64s2", "sox_gemm_f16_64x64_k64s2", "sox_gemm_f16_256x192_k32s4",
                 "sox_gemm_f16_256x192_w8k64s2", "sox_gemm_f16_256x256_w8k32s4", "sox_gemm_f16_256x256_w8k64s2",
                 "sox_gemm_f16_256x128_k32s3", "sox_gemm_f16_256x128_k32s5", "sox_gemm_f16_128x128_k32s4",
-                "sox_gemm_f16_64x64_k64s4", "sox_gemm_f16_128x64_k64s4"]
+                "sox_gemm_f16_64x64_k64s4", "sox_gemm_f16_128x64_k64s4", "sox_gemm_f16_128x192_k32s3"]
 
 
 @pytest.mark.parametrize("kernel", GEMM_KERNELS)

@@ -48,6 +48,9 @@ def test_kernarg_abi_layout():
     assert ctypes.sizeof(N.GemmP) == 12
     assert ctypes.sizeof(N.AttentionP) == 4 * (1 + 12 + 3 + 3 + 4)
     assert ctypes.sizeof(N.Bind) == 24
+    assert ctypes.sizeof(N.ResizeP) == 4 * 6 and ctypes.sizeof(N.PadP) == 4 * 15
+    assert ctypes.sizeof(N.TransposeP) == 4 * 7 and ctypes.sizeof(N.SliceP) == 4 * 25
+    assert ctypes.sizeof(N.DepthToSpaceP) == 8 and ctypes.sizeof(N.TanhP) == 8 and ctypes.sizeof(N.ClipP) == 8
 
 
 def test_code_objects_embedded_for_gfx950():

@@ -1,0 +1,87 @@
+"""Pins the oracle's restatement of the rest of the GPU op surface (bilinear resize, pad, average
+pool, DepthToSpace / SpaceToDepth, LeakyRelu / Tanh / Clip / Erf, global average pool, batched
+MatMul with a broadcast operand, transpose, slice) before it checks the HIP kernels.
+
+Expected values are the committed torch-float64 golden vectors of tests/golden/make_golden_ops.py
+(library routines and the ONNX definitions), plus invariants: SpaceToDepth inverts DepthToSpace in
+both channel orders, a transpose twice with inverse perms is the identity, a slice equals numpy's.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+from tests.conftest import max_rel
+
+G = np.load(os.path.join(os.path.dirname(__file__), "golden", "golden_ops.npz"))
+
+
+def _n(prefix):
+    return len({k.split("_")[0] for k in G.files if k.startswith(prefix) and k[len(prefix)].isdigit()})
+
+
+@pytest.mark.parametrize("i", range(_n("bil")))
+def test_resize_bilinear_golden(i):
+    s, relu, has_add, add_relu = G[f"bil{i}_meta"]
+    add = G[f"bil{i}_add"] if has_add else None
+    got = O.resize_bilinear(G[f"bil{i}_x"], float(s), float(s), add, relu=bool(relu), add_relu=bool(add_relu))
+    assert got.shape == G[f"bil{i}_y"].shape
+    assert max_rel(got, G[f"bil{i}_y"]) < 2e-6
+
+
+@pytest.mark.parametrize("i", range(_n("pad")))
+def test_pad_golden(i):
+    t, l, b, r, mode, value = G[f"pad{i}_meta"]
+    got = O.pad_nhwc(G[f"pad{i}_x"], int(t), int(l), int(b), int(r), int(mode), float(value))
+    assert np.array_equal(got, G[f"pad{i}_y"])  # copies and fills only
+
+
+@pytest.mark.parametrize("i", range(_n("avg")))
+def test_avg_pool_golden(i):
+    k, s, t, l, b, r, cip = (int(v) for v in G[f"avg{i}_meta"])
+    got = O.avg_pool(G[f"avg{i}_x"], (k, k), (s, s), (t, l, b, r), bool(cip))
+    assert got.shape == G[f"avg{i}_y"].shape
+    assert max_rel(got, G[f"avg{i}_y"]) < 2e-6
+
+
+@pytest.mark.parametrize("i", range(_n("d2s")))
+def test_depth_to_space_golden_and_inverse(i):
+    x, b = G[f"d2s{i}_x"], int(G[f"d2s{i}_meta"][0])
+    for crd, key in ((True, "crd"), (False, "dcr")):
+        y = O.depth_to_space(x, b, crd)
+        assert np.array_equal(y, G[f"d2s{i}_{key}"])
+        assert np.array_equal(O.depth_to_space(y, b, crd, inverse=True), x)
+
+
+@pytest.mark.parametrize("i", range(_n("s2d")))
+def test_space_to_depth_golden(i):
+    x, b = G[f"s2d{i}_x"], int(G[f"s2d{i}_meta"][0])
+    for crd, key in ((True, "crd"), (False, "dcr")):
+        assert np.array_equal(O.depth_to_space(x, b, crd, inverse=True), G[f"s2d{i}_{key}"])
+
+
+def test_unary2_golden():
+    x = G["un_x"]
+    assert max_rel(O.unary2(x, "LeakyRelu", 0.1), G["un_leaky01"]) < 1e-6
+    assert max_rel(O.unary2(x, "LeakyRelu", 2.0), G["un_leaky2"]) < 1e-6  # the a > 1 (min) branch
+    assert max_rel(O.unary2(x, "Tanh", 1.0, 1.0), G["un_tanh"]) < 1e-6
+    assert max_rel(O.unary2(x, "Tanh", 2.0 / 3.0, 1.7159), G["un_tanh_scaled"]) < 1e-6
+    assert np.array_equal(O.unary2(x, "Clip", -1.0, 0.75), G["un_clip"])
+    assert max_rel(O.unary2(x, "Erf"), G["un_erf"]) < 5e-7  # A&S 7.1.26: |err| <= 1.5e-7
+
+
+def test_gap_and_matmul_broadcast_golden():
+    assert max_rel(O.global_avg_pool(G["gap_x"]), G["gap_y"]) < 1e-6
+    for i in range(_n("mm")):
+        assert max_rel(O.matmul_bcast(G[f"mm{i}_a"], G[f"mm{i}_b"]), G[f"mm{i}_y"]) < 1e-5
+
+
+def test_transpose_slice_index_ops():
+    x = G["gap_x"]  # [2, 13, 11, 40]
+    perm = (0, 3, 1, 2)
+    y = O.transpose(x, perm)
+    assert y.shape == (2, 40, 13, 11) and y[1, 7, 4, 9] == x[1, 4, 9, 7]
+    assert np.array_equal(O.transpose(y, np.argsort(perm)), x)
+    s = O.slice_(x, (1, 10, 3), (12, 2, 40), (1, 2, 3), (2, -3, 5))
+    assert np.array_equal(s, x[:, 1:12:2, 10:2:-3, 3:40:5])
