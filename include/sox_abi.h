@@ -269,6 +269,14 @@ typedef struct sox_gather_args {
     int32_t od[6];
 } sox_gather_args;
 
+/* Batched 2D transpose (a permutation that swaps two contiguous groups of dims):
+ * y[b][c][r] = x[b][r][c], grid (ceil(cols / 64), ceil(rows / 64), batch). */
+typedef struct sox_transpose2d_args {
+    const void* x;
+    void* y;
+    int32_t rows, cols;
+} sox_transpose2d_args;
+
 /* LeakyRelu (0) / Tanh (1, a = in scale, b = out scale) / Clip (2, a = min, b = max) / Erf (3)
  * (unary2.comp; Kernels/Act.cs:83-147). */
 typedef struct sox_unary2_args {
@@ -297,8 +305,8 @@ typedef struct sox_avgpool_args {
     int32_t count_include_pad;
 } sox_avgpool_args;
 
-/* GlobalAvgPool finish (gap_sum.comp): y[b][c] = (sum over chunks, in chunk order, of
- * part[b][chunk][c]) * inv_hw. */
+/* GlobalAvgPool finish (gap_sum.comp): y[b][c] = (sum over chunks of part[b][chunk][c]) * inv_hw,
+ * chunks added in 4 interleaved phases, the phase sums in phase order. Grid (ceil(c / 64), n). */
 typedef struct sox_gap_mean_args {
     const float* part;
     void* y;

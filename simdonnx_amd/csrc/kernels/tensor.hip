@@ -128,6 +128,38 @@ extern "C" __global__ void __launch_bounds__(256) sox_gather_f16(sox_gather_args
 extern "C" __global__ void __launch_bounds__(256) sox_gather_f32(sox_gather_args p) { gather_body<float>(p); }
 
 // ------------------------------------------------------------------------------------------
+// Batched 2D transpose through LDS, the permutations that swap two contiguous groups of dims
+// (NHWC <-> NCHW, the last-two-dims swap; the reference's fast paths, Kernels/Ops.cs:802-868):
+// x [batch][R][C] -> y [batch][C][R]. A 256-thread workgroup moves one 64 x 64 tile: reads 64
+// consecutive columns of 16 rows per pass, writes 64 consecutive rows of 16 columns per pass. The
+// tile rows are padded by one 4-byte word, so the column reads hit 64 distinct banks.
+// Grid (ceil(C / 64), ceil(R / 64), batch).
+// ------------------------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void transpose2d_body(const sox_transpose2d_args& p) {
+    constexpr int PADE = 4 / sizeof(T);  // one 4-byte word of padding per tile row
+    __shared__ T tile[64][64 + PADE];
+    const int tx = threadIdx.x % 64, ty = threadIdx.x / 64;
+    const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
+    const T* __restrict__ x = (const T*)p.x + (long)blockIdx.z * p.rows * p.cols;
+    T* __restrict__ y = (T*)p.y + (long)blockIdx.z * p.rows * p.cols;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        const int r = r0 + ty + 4 * k, c = c0 + tx;
+        if (r < p.rows && c < p.cols) tile[ty + 4 * k][tx] = x[(long)r * p.cols + c];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        const int c = c0 + ty + 4 * k, r = r0 + tx;
+        if (r < p.rows && c < p.cols) y[(long)c * p.rows + r] = tile[tx][ty + 4 * k];
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_transpose2d_f16(sox_transpose2d_args p) { transpose2d_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_transpose2d_f32(sox_transpose2d_args p) { transpose2d_body<float>(p); }
+
+// ------------------------------------------------------------------------------------------
 // LeakyRelu / Tanh / Clip / Erf (Kernels/Act.cs:83-147, the vector forms): leaky = max(x, a x)
 // for a <= 1 else min(x, a x); o tanh(i x) = 2o sigmoid(2i x) - o with the Cephes sigmoid;
 // clip = min(max(x, lo), hi); erf = A&S 7.1.26.
@@ -196,6 +228,37 @@ __device__ __forceinline__ void d2s_body(const sox_d2s_args& p) {
 extern "C" __global__ void __launch_bounds__(256) sox_d2s_f16(sox_d2s_args p) { d2s_body<half_t>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_d2s_f32(sox_d2s_args p) { d2s_body<float>(p); }
 
+// DCR order with whole 16-byte channel vectors: the CV consecutive output channels of a work item
+// are CV consecutive input channels (depth-to-space: sub oc + c; space-to-depth: output channel
+// sub ic + c), so each item is one 16-byte load and store. The launcher routes here when oc
+// (depth-to-space) or ic (space-to-depth) is a multiple of CV.
+template <typename T, int CV>
+__device__ __forceinline__ void d2s_dcr_body(const sox_d2s_args& p) {
+    typedef typename Vt<T, CV>::V Vec;
+    const long idx = gid();
+    if (idx * CV >= p.count) return;
+    const int bk = p.block;
+    const int ch = (int)((idx * CV) % p.oc);
+    const int pix = (int)((idx * CV) / p.oc);
+    const int ox = pix % p.ow, q = pix / p.ow, oy = q % p.oh, b = q / p.oh;
+    int sy, sx, sc;
+    if (!p.s2d) {
+        const int sub = (oy % bk) * bk + ox % bk;
+        sy = oy / bk;
+        sx = ox / bk;
+        sc = sub * p.oc + ch;
+    } else {
+        const int sub = ch / p.ic;
+        sc = ch % p.ic;
+        sy = oy * bk + sub / bk;
+        sx = ox * bk + sub % bk;
+    }
+    *(Vec*)((T*)p.y + idx * CV) = *(const Vec*)((const T*)p.x + (((long)b * p.ih + sy) * p.iw + sx) * p.ic + sc);
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_d2s_dcr_f16(sox_d2s_args p) { d2s_dcr_body<half_t, 8>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_d2s_dcr_f32(sox_d2s_args p) { d2s_dcr_body<float, 4>(p); }
+
 // ------------------------------------------------------------------------------------------
 // Average pool, NHWC (Kernels/Ops.Seq.cs:180-215): taps summed in (ky, kx) order from zero, then
 // one multiply by 1 / count, count = kh kw (count_include_pad) or the in-bounds taps.
@@ -239,18 +302,33 @@ extern "C" __global__ void __launch_bounds__(256) sox_avgpool_f32_v(sox_avgpool_
 extern "C" __global__ void __launch_bounds__(256) sox_avgpool_f32_s(sox_avgpool_args p) { avgpool_body<float, 1>(p); }
 
 // ------------------------------------------------------------------------------------------
-// GlobalAvgPool finish (gap_sum.comp): the GAP partial kernel's per-chunk channel sums, added in
-// chunk order, times 1 / hw.
+// GlobalAvgPool finish (gap_sum.comp): the GAP partial kernel's per-chunk channel sums times
+// 1 / hw. Grid (ceil(c / 64), n): thread (phase f = t / 64, channel t % 64) adds chunks f, f + 4,
+// f + 8, ... with 8 loads in flight, then the 4 phase sums are added in phase order.
 // ------------------------------------------------------------------------------------------
 template <typename T>
 __device__ __forceinline__ void gap_mean_body(const sox_gap_mean_args& p) {
-    const long idx = gid();
-    if (idx >= (long)p.n * p.c) return;
-    const int b = (int)(idx / p.c), ch = (int)(idx % p.c);
-    const float* part = p.part + (long)b * p.chunks * p.c + ch;
+    __shared__ float red[4][64];
+    const int t = threadIdx.x, f = t / 64, cl = t % 64;
+    const int ch = blockIdx.x * 64 + cl, b = blockIdx.y;
     float s = 0.0f;
-    for (int k = 0; k < p.chunks; k++) s += part[(long)k * p.c];
-    ((T*)p.y)[idx] = (T)(s * p.inv_hw);
+    if (ch < p.c) {
+        const float* part = p.part + (long)b * p.chunks * p.c + ch;
+        for (int k0 = f; k0 < p.chunks; k0 += 32) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int k = k0 + 4 * u;
+                v[u] = k < p.chunks ? part[(long)k * p.c] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) s += v[u];
+        }
+    }
+    red[f][cl] = s;
+    __syncthreads();
+    if (f == 0 && ch < p.c)
+        ((T*)p.y)[(long)b * p.c + ch] = (T)((((red[0][cl] + red[1][cl]) + red[2][cl]) + red[3][cl]) * p.inv_hw);
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_gap_mean_f16(sox_gap_mean_args p) { gap_mean_body<half_t>(p); }

@@ -79,8 +79,10 @@ def test_pad(hip, shape, pads, mode, value, half):
 
 @HALF
 @pytest.mark.parametrize("shape,perm", [((2, 13, 11, 40), (0, 3, 1, 2)), ((4, 80, 6, 32), (0, 2, 1, 3)),
-                                        ((3, 5, 7), (2, 0, 1)), ((2, 3, 4, 5, 6, 7), (5, 3, 1, 0, 2, 4))])
+                                        ((3, 5, 7), (2, 0, 1)), ((2, 3, 4, 5, 6, 7), (5, 3, 1, 0, 2, 4)),
+                                        ((4, 80, 33), (0, 2, 1)), ((2, 24, 70, 65), (0, 2, 3, 1))])
 def test_transpose(hip, shape, perm, half):
+    """Swaps of two contiguous dim groups run the LDS-tiled 2D transpose, other perms the gather."""
     x = img(4, shape, half)
     pb = PlanBuilder()
     xv = pb.input(shape, None, "x")
@@ -120,7 +122,8 @@ def test_unary2(hip, op, a, b, half):
 @HALF
 @pytest.mark.parametrize("shape,block,crd,inverse", [
     ((1, 3, 4, 8), 2, True, False), ((2, 2, 3, 27), 3, False, False), ((1, 60, 60, 64), 2, False, False),
-    ((1, 6, 8, 3), 2, True, True), ((2, 6, 9, 4), 3, False, True), ((1, 120, 120, 16), 2, True, True)])
+    ((1, 6, 8, 3), 2, True, True), ((2, 6, 9, 4), 3, False, True), ((1, 120, 120, 16), 2, True, True),
+    ((1, 12, 12, 16), 2, False, True)])
 def test_depth_space(hip, shape, block, crd, inverse, half):
     n, h, w, c = shape
     x = img(7, shape, half)
