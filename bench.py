@@ -174,6 +174,36 @@ def bench_copy(steps: int):
     return dict(bytes_per_launch=2 * n * 2, ms=ms, gb_s=2 * n * 2 / (ms * 1e-3) / 1e9)
 
 
+def bench_recognizer_ctc(steps: int, replay: bool = True):
+    """The recognizer with the fused CTC head (HipCtcProjection) in place of head Gemm + softmax:
+    the features plan replayed (HIP events), then the head on the device features, host-timed per
+    call including its launch, the copy home of the indices and probabilities and the wait."""
+    from simdonnx_amd import graphs
+    from simdonnx_amd.backend import HipBackend, HipCtcProjection, HipInferenceSession
+    hip = HipBackend.default()
+    plan, ins, (hw, hb) = graphs.svtr(head="features")
+    ctc = HipCtcProjection(hip, hw, hb, hw.shape[0], hw.shape[1])
+    g = hip.graph(plan, True)
+    rows = plan.values[plan.output].count // hw.shape[0]
+    with HipInferenceSession(g) as s:
+        s.set_input(ins[0])
+        s.set_replay(replay)
+        s.run()
+        s.time(200)
+        ms_feat = s.time(steps) / steps
+        for _ in range(20):
+            ctc.argmax(s, plan.output, 32, rows // 32)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            ctc.argmax(s, plan.output, 32, rows // 32)
+        ms_head = (time.perf_counter() - t0) * 1e3 / steps
+    g.release()
+    ctc.close()
+    return dict(workload="SVTR-style recognizer, 32x3x48x320, fused CTC head (argmax + probability per row)",
+                ms_features=round(ms_feat, 4), ms_ctc_head_host=round(ms_head, 4),
+                ms_per_batch=round(ms_feat + ms_head, 4), rows=rows, classes=int(hw.shape[1]))
+
+
 def _ops_cases():
     """One-node plans of the rest of the ExecOp surface at the sizes the detector / recognizer shapes
     give them (fp16 storage): (label, plan, inputs, algorithmic bytes, flops). Bytes count each
@@ -298,7 +328,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-replay", action="store_true",
                     help="launch network dispatches one by one instead of replaying a HIP graph (profiler runs)")
-    ap.add_argument("--only", choices=["gemm", "conv", "detector", "recognizer", "mobilenetv3", "copy", "ops"],
+    ap.add_argument("--only", choices=["gemm", "conv", "detector", "recognizer", "mobilenetv3", "copy", "ops",
+                                       "recognizer_ctc"],
                     help="run one workload only (profiling runs); prints its own JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -308,7 +339,8 @@ def main():
     if args.only:
         fn = {"gemm": lambda: bench_gemm(args.steps, args.warmup), "conv": lambda: bench_conv(args.steps),
               "copy": lambda: bench_copy(args.steps),
-              "ops": lambda: {"ops": bench_ops(args.steps)}}.get(args.only) or (lambda: bench_network(args.only, args.steps, not args.no_replay))
+              "ops": lambda: {"ops": bench_ops(args.steps)},
+              "recognizer_ctc": lambda: bench_recognizer_ctc(args.steps, not args.no_replay)}.get(args.only) or (lambda: bench_network(args.only, args.steps, not args.no_replay))
         r = fn()
         print(json.dumps({"only": args.only, **{k: v for k, v in r.items() if k != "kernel_ms"}}), flush=True)
         return
@@ -345,6 +377,10 @@ def main():
         out["conv3x3_bias_relu_fp32"] = bench_conv(200)
     except Exception as e:
         out["conv3x3_bias_relu_fp32"] = {"error": repr(e)}
+    try:
+        out["recognizer_ctc"] = bench_recognizer_ctc(200, not args.no_replay)
+    except Exception as e:
+        out["recognizer_ctc"] = {"error": repr(e)}
     try:
         out["ops"] = bench_ops(200)
     except Exception as e:

@@ -324,6 +324,27 @@ typedef struct sox_matmul_args {
     int64_t a_stride, b_stride, y_stride;
 } sox_matmul_args;
 
+/* CTC head, pass 1 (Decoding/Kernels/MatMul.ArgMax.cs:29-299): per (row block of 128, column range
+ * of cols_per_split) the rows' (max, sum of exp(logit - max), argmax) over the range, logits =
+ * x . W^T + bias. Grid (ceil(rows / 256), splits), 512 threads; cols_per_split * (inner * 2 + 4) <= 128 KiB. */
+typedef struct sox_ctc_args {
+    const void* x;      /* features fp16 [rows][inner] */
+    const void* w;      /* weights fp16 [columns][ldw], the inner values of a column contiguous */
+    const float* bias;  /* [columns] when has_bias */
+    float* part;        /* [splits][rows][3]: max, sum (NaN: a non-finite logit), argmax (int bits) */
+    int32_t rows, inner, columns, ldw, cols_per_split, has_bias;
+} sox_ctc_args;
+
+/* CTC head, pass 2: the splits (<= 64) of a row merged by one wave; probability = min(1, 1 / sum);
+ * *status = 1 when a logit or the sum was not finite. 256 threads, ceil(rows / 4) workgroups. */
+typedef struct sox_ctc_merge_args {
+    const float* part;
+    int32_t* indices;
+    float* probs;
+    int32_t* status;
+    int32_t rows, splits;
+} sox_ctc_merge_args;
+
 #ifdef __cplusplus
 }
 #endif

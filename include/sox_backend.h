@@ -179,6 +179,29 @@ int sox_session_read_value(sox_session* session, int32_t value, float* host, int
 int sox_session_value_ptr(sox_session* session, int32_t value, void** dev);
 void* sox_session_stream(sox_session* session);
 
+/* ---- CTC head (CtcProjection, Decoding/CtcProjection.cs:12-75) ----
+ * The class projection of a CTC head fused with the per-row argmax and the winner's softmax
+ * probability, run on the device over a session's features so the [rows, classes] logits are never
+ * stored or copied home. Create packs the weights once (fp16, column-major per class, as the GPU
+ * const contract rounds them) and keeps them on the device; one object serves any number of sessions
+ * (calls on one object serialize on its lock). */
+typedef struct sox_ctc sox_ctc;
+/* weights: row-major [inner][columns] (an ONNX MatMul's B); bias: [columns] or NULL. */
+int sox_ctc_create(sox_backend* backend, const float* weights, const float* bias, int32_t inner, int32_t columns,
+                   sox_ctc** ctc);
+void sox_ctc_destroy(sox_ctc* ctc);
+/* IsFused (CtcProjection.cs:41-42): 1 when the fused kernel serves this head (inner >= 64,
+ * columns >= 1024, as MatMul.CanFuseArgMax; on the GPU also inner % 16 == 0 and inner <= 256). */
+int sox_ctc_is_fused(sox_ctc* ctc);
+/* ArgMax (CtcProjection.cs:44-58) over the activation `feature_value` of a session of an fp16 graph
+ * ([batch * rows, inner], after sox_session_run / _wait): indices[r] = the largest logit's column
+ * (ties keep the first), probabilities[r] = its softmax probability in (0, 1]. Runs on the
+ * session's stream and returns when the host arrays are written. SOX_E_UNSUPPORTED when the head
+ * is not fused (nothing written, the reference's false), SOX_E_INVALID for a non-finite logit
+ * ("Recognizer output is invalid."). */
+int sox_ctc_argmax(sox_ctc* ctc, sox_session* session, int32_t feature_value, int32_t batch, int32_t rows,
+                   int32_t* indices, float* probabilities);
+
 #ifdef __cplusplus
 }
 #endif

@@ -372,3 +372,18 @@ def matmul_bcast(a, b):
     b3 = np.broadcast_to(b.reshape(bb, k, n), (batch, k, n)) if bb == 1 else b.reshape(batch, k, n)
     return matmul(a3, np.ascontiguousarray(b3)).reshape(a.shape[:-2] + (m, n))
 
+
+def ctc_argmax(x, w, bias=None):
+    """CtcProjection.ArgMax (Decoding/Kernels/MatMul.ArgMax.cs:130-299): (indices, probabilities) per
+    row of x [rows, inner] against w [inner, columns]; raises ValueError on a non-finite logit."""
+    x, w, bias = _f32(x), _f32(w), _f32(bias)
+    rows, inner = x.shape[0], x.shape[1]
+    columns = w.shape[1]
+    idx = np.empty(rows, np.int32)
+    prob = np.empty(rows, np.float32)
+    rc = lib().ora_ctc_argmax(_p(x), _p(w), _p(bias), ctypes.c_long(rows), inner, columns,
+                              idx.ctypes.data_as(ctypes.c_void_p), _p(prob))
+    if rc != 0:
+        raise ValueError("Recognizer output is invalid.")
+    return idx, prob
+

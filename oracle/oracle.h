@@ -129,6 +129,11 @@ int ora_depth_space(const float* src, int ih, int iw, int ic, float* dst, int b,
 /* LeakyRelu (0) / Tanh (1) / Clip (2) / Erf (3) (Kernels/Act.cs:83-147). */
 int ora_unary2(const float* src, long count, int mode, float a, float b, float* dst);
 
+/* CtcProjection.ArgMax, scalar kernel (Decoding/Kernels/MatMul.ArgMax.cs:130-299): x [rows][inner],
+ * w row-major [inner][columns], bias nullable. -1 on a non-finite logit. */
+int ora_ctc_argmax(const float* x, const float* w, const float* bias, long rows, int inner, int columns, int* indices,
+                   float* probs);
+
 #ifdef __cplusplus
 }
 #endif

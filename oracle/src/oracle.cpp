@@ -1021,4 +1021,39 @@ int ora_unary2(const float* src, long count, int mode, float a, float b, float* 
     return 0;
 }
 
+// CtcProjection.ArgMax, the scalar kernel (Decoding/Kernels/MatMul.ArgMax.cs:130-299, Row1): per row,
+// logit = bias + sum_k x w (k ascending, one multiply and add each), UpdateArgMax (:267-278): a
+// larger logit rescales the running sum by exp(max - logit) and adds 1, else adds exp(logit - max);
+// ties keep the first column; probability = min(1, 1 / sum) (:287-292). Returns -1 on a non-finite
+// logit or sum (the reference throws "Recognizer output is invalid.").
+int ora_ctc_argmax(const float* x, const float* w, const float* bias, long rows, int inner, int columns, int* indices,
+                   float* probs) {
+    int bad = 0;
+#pragma omp parallel for schedule(static) num_threads(threads()) reduction(| : bad)
+    for (long r = 0; r < rows; r++) {
+        const float* xr = x + r * inner;
+        float mx = -INFINITY, sum = 0.0f;
+        int best = 0;
+        for (int col = 0; col < columns; col++) {
+            float v = bias ? bias[col] : 0.0f;
+            for (int k = 0; k < inner; k++) v += xr[k] * w[(long)k * columns + col];
+            if (!std::isfinite(v)) {
+                bad = 1;
+                break;
+            }
+            if (v > mx) {
+                sum = sum * expf(mx - v) + 1.0f;
+                mx = v;
+                best = col;
+            } else {
+                sum += expf(v - mx);
+            }
+        }
+        if (!(sum > 0.0f) || std::isinf(sum)) bad = 1;
+        indices[r] = best;
+        probs[r] = std::min(1.0f, 1.0f / sum);
+    }
+    return bad ? -1 : 0;
+}
+
 }  // extern "C"

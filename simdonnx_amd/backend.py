@@ -266,3 +266,48 @@ class HipInferenceSession:
         N.check(N.backend().sox_session_read_value(self.h, vid, out.ctypes.data_as(ctypes.POINTER(N.c_float)),
                                                    v.count), "read_value")
         return out.reshape(v.phys)
+
+
+class HipCtcProjection:
+    """CtcProjection (Decoding/CtcProjection.cs:12-75) on the device: the CTC head's class projection
+    fused with the per-row argmax and the winner's softmax probability, over a session's features
+    (sox_ctc_* of include/sox_backend.h). One object serves any number of sessions."""
+
+    def __init__(self, backend: HipBackend, weights: np.ndarray, bias: Optional[np.ndarray], inner: int, columns: int):
+        w = np.ascontiguousarray(weights, dtype=np.float32)
+        if w.size != inner * columns:
+            raise ValueError("weights must hold inner x columns floats")
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        if b is not None and b.size != columns:
+            raise ValueError("bias must hold columns floats")
+        h = N.c_void_p()
+        N.check(N.backend().sox_ctc_create(backend.h, w.ctypes.data, None if b is None else b.ctypes.data, inner,
+                                           columns, ctypes.byref(h)), "CtcProjection")
+        self.h, self.inner, self.columns = h, inner, columns
+
+    @property
+    def is_fused(self) -> bool:
+        return bool(N.backend().sox_ctc_is_fused(self.h))
+
+    def argmax(self, session: "HipInferenceSession", feature_value: int, batch: int, rows: int):
+        """(indices int32 [batch*rows], probabilities float32 [batch*rows]) of the session's features,
+        or None when the head is not fused (the reference's false). A non-finite logit raises."""
+        idx = np.empty(batch * rows, np.int32)
+        prob = np.empty(batch * rows, np.float32)
+        rc = N.backend().sox_ctc_argmax(self.h, session.h, feature_value, batch, rows, idx.ctypes.data, prob.ctypes.data)
+        if rc == N.SOX_E_UNSUPPORTED:
+            return None
+        N.check(rc, "CtcProjection.ArgMax")
+        return idx, prob
+
+    def close(self):
+        if self.h:
+            N.backend().sox_ctc_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+

@@ -178,11 +178,13 @@ def dbnet(seed: int = 4, n=1, size=960):
     return plan, [xin]
 
 
-def svtr(seed: int = 5, n=32, h=48, w=320, dim=192, heads=6, depth=8, mlp=4, classes=6625):
+def svtr(seed: int = 5, n=32, h=48, w=320, dim=192, heads=6, depth=8, mlp=4, classes=6625, head="softmax"):
     """Config 5: SVTR/CRNN-style recognizer. Stem: two conv3x3 s2 + BN(folded) + GELU (3->32->64);
     the 64 x 12 x 80 map collapses its height with a 12x1 conv to dim (80 tokens x 192); 8 mixer
     blocks x = x + proj(attn(LN(x))), x = x + fc2(GELU(fc1(LN(x)))); final LN; linear head to
-    `classes` + softmax. Weights ~ N(0, 0.02) for the mixer / head Gemms (He-normal for convs)."""
+    `classes` + softmax. Weights ~ N(0, 0.02) for the mixer / head Gemms (He-normal for convs).
+    head="features": the plan ends at the final LayerNorm (the [n*80, dim] features a CTC head reads)
+    and the head's (weights [dim, classes], bias) come back as a third item."""
     pb = PlanBuilder()
     ids = _Ids()
     x = pb.input((n, 3, h, w), NHWC, "image")
@@ -215,10 +217,14 @@ def svtr(seed: int = 5, n=32, h=48, w=320, dim=192, heads=6, depth=8, mlp=4, cla
         f2 = lin(f1, dim * mlp, dim, name=f"blk{b}.fc2")
         tok = pb.add(tok, f2, name=f"blk{b}.res2")
     tok = ln(tok, "norm")
+    xin = synth.normal(seed, 10_000, (n, h, w, 3), 1.0)
+    if head == "features":
+        hw = synth.normal(seed, ids(), (dim, classes), 0.02)
+        hb = _bias(seed, ids, classes)
+        return pb.build(tok), [xin], (hw, hb)
     logits = lin(tok, dim, classes, name="head")
     y = pb.softmax(logits, name="softmax")
     plan = pb.build(y)
-    xin = synth.normal(seed, 10_000, (n, h, w, 3), 1.0)
     return plan, [xin]
 
 

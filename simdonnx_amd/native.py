@@ -207,6 +207,10 @@ BACKEND_API = {
     "sox_session_read_value": (c_int32, [c_void_p, c_int32, ctypes.POINTER(c_float), c_int64]),
     "sox_session_value_ptr": (c_int32, [c_void_p, c_int32, ctypes.POINTER(c_void_p)]),
     "sox_session_stream": (c_void_p, [c_void_p]),
+    "sox_ctc_create": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, ctypes.POINTER(c_void_p)]),
+    "sox_ctc_destroy": (None, [c_void_p]),
+    "sox_ctc_is_fused": (c_int32, [c_void_p]),
+    "sox_ctc_argmax": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p]),
 }
 
 _thin = None

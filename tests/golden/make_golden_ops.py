@@ -1,12 +1,14 @@
 """Writes the golden vectors that pin the oracle's restatement of the rest of the GPU op surface:
 bilinear resize (+ relu, + addend), constant / reflect pad, average pool (with and without the
 padded taps counted), DepthToSpace / SpaceToDepth (CRD and DCR), LeakyRelu / Tanh / Clip / Erf,
-global average pool and batched MatMul with a broadcast right operand.
+global average pool, batched MatMul with a broadcast right operand and the CTC head's fused
+projection + argmax + softmax probability.
 
 Each expected output is a library routine or the ONNX definition evaluated by torch in float64:
 F.interpolate(bilinear, align_corners=False), F.pad(constant / reflect), F.avg_pool2d,
 F.pixel_shuffle / pixel_unshuffle (CRD) and the ONNX DCR reshape-transpose, F.leaky_relu,
-torch.tanh / clamp / erf, mean over H W, torch.matmul. Inputs come from simdonnx_amd.synth (seeded);
+torch.tanh / clamp / erf, mean over H W, torch.matmul, and for the CTC head torch.argmax / softmax of
+the float64 logits. Inputs come from simdonnx_amd.synth (seeded);
 the file stores the inputs and the float64 results rounded to float32.
 
 Run:  python tests/golden/make_golden_ops.py      (writes tests/golden/golden_ops.npz)
@@ -116,6 +118,14 @@ def main():
         b = synth.normal(970 + i, 2, (1 if bc else bt, k, nn), 0.2)
         out[f"mm{i}_a"], out[f"mm{i}_b"] = a, b
         out[f"mm{i}_y"] = torch.matmul(t64(a), t64(b)).numpy().astype(np.float32)
+    # CTC head: logits = x W + b, the first index of the row maximum and softmax(logits)[argmax]
+    x = synth.normal(980, 1, (70, 64), 1.0)
+    w = synth.normal(980, 2, (64, 1100), 0.1)
+    b = synth.uniform(980, 3, (1100,), -0.1, 0.1)
+    lg = t64(x) @ t64(w) + t64(b)
+    out["ctc_x"], out["ctc_w"], out["ctc_b"] = x, w, b
+    out["ctc_idx"] = torch.argmax(lg, dim=1).numpy().astype(np.int32)
+    out["ctc_prob"] = torch.softmax(lg, dim=1).max(dim=1).values.numpy().astype(np.float32)
     path = os.path.join(HERE, "golden_ops.npz")
     np.savez_compressed(path, **out)
     print("wrote", path, os.path.getsize(path), "bytes")

@@ -85,3 +85,22 @@ def test_transpose_slice_index_ops():
     assert np.array_equal(O.transpose(y, np.argsort(perm)), x)
     s = O.slice_(x, (1, 10, 3), (12, 2, 40), (1, 2, 3), (2, -3, 5))
     assert np.array_equal(s, x[:, 1:12:2, 10:2:-3, 3:40:5])
+
+
+def test_ctc_argmax_golden():
+    """Fused projection + argmax + softmax probability (CtcProjection.ArgMax) vs torch float64."""
+    idx, prob = O.ctc_argmax(G["ctc_x"], G["ctc_w"], G["ctc_b"])
+    assert np.array_equal(idx, G["ctc_idx"])
+    assert max_rel(prob, G["ctc_prob"]) < 1e-5
+
+
+def test_ctc_argmax_ties_and_invalid():
+    """Equal logits keep the first column; a non-finite logit raises (MatMul.ArgMax.cs:267-278)."""
+    x, w, b = G["ctc_x"][:8].copy(), G["ctc_w"].copy(), G["ctc_b"].copy()
+    w[:, 900] = w[:, 5]
+    b[5] = b[900] = 100.0  # both dominate every row, exactly equal
+    idx, prob = O.ctc_argmax(x, w, b)
+    assert (idx == 5).all() and np.allclose(prob, 0.5, rtol=1e-5)
+    x[3, 7] = np.inf
+    with pytest.raises(ValueError):
+        O.ctc_argmax(x, w, b)
