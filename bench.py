@@ -247,6 +247,20 @@ def _ops_cases():
     add_case("global avgpool, 1x240x240x96",
              lambda pb: pb.global_avg_pool(pb.input((1, 96, 240, 240), NHWC, "x"), name="gap"),
              [(1, 240, 240, 96)], 96)
+    add_case("safediv, 1x480x480x24",
+             lambda pb: pb.safe_div(pb.input((1, 480, 480, 24), None, "a"), pb.input((1, 480, 480, 24), None, "b"),
+                                    1e-3, -4.0, 4.0, name="sd"),
+             [(1, 480, 480, 24), (1, 480, 480, 24)], 480 * 480 * 24)
+    add_case("channel shift 5 groups along W, 1x120x120x96",
+             lambda pb: pb.channel_shift(pb.input((1, 96, 120, 120), NHWC, "x"), 3, (16, 32, 48, 64, 80),
+                                         (-2, -1, 0, 1, 2), name="sh"),
+             [(1, 120, 120, 96)], 120 * 120 * 96)
+    wh = synth.normal(78, 3, (1, 24), 0.2)
+    add_case("uphead x2 + skip -> 1 ch sigmoid, 1x240x240x24 -> 480x480",
+             lambda pb: pb.up_head(pb.input((1, 24, 240, 240), NHWC, "x"), pb.input((1, 24, 480, 480), NHWC, "s"), wh,
+                                   np.zeros(1, np.float32), 2, resize_relu=True, skip_relu=True, act="sigmoid",
+                                   name="uh"),
+             [(1, 240, 240, 24), (1, 480, 480, 24)], 480 * 480)
     add_case("matmul 192 x [80,32]x[32,80]",
              lambda pb: pb.matmul(pb.input((192, 80, 32), None, "a"), pb.input((192, 32, 80), None, "b"), name="mm"),
              [(192, 80, 32), (192, 32, 80)], 192 * 80 * 80, 2 * 192 * 80 * 32 * 80)

@@ -345,6 +345,45 @@ typedef struct sox_ctc_merge_args {
     int32_t rows, splits;
 } sox_ctc_merge_args;
 
+/* Built-in extension op SafeDiv (Engine/Fusions/SafeDivOp.cs; safediv.comp): y = clamp(a / max(b, eps),
+ * lo, hi) in fp32 over same-shape operands. */
+typedef struct sox_safediv_args {
+    const void* a;
+    const void* b;
+    void* y;
+    int64_t count;
+    float eps, lo, hi;
+} sox_safediv_args;
+
+/* Built-in extension op ChannelShift (Engine/Fusions/ChannelShiftOp.cs; shift.comp), NHWC: channel group g
+ * (channels [ends[g-1], ends[g])) reads the pixel offs[g] away along H (axis 2) or W (axis 3), zero
+ * outside; channels past the last group end copy unshifted. */
+typedef struct sox_shift_args {
+    const void* x;
+    void* y;
+    int32_t n, h, w, c, axis, ngroups;
+    int32_t ends[5], offs[5];
+} sox_shift_args;
+
+/* Built-in extension op UpHead (Engine/Fusions/UpHeadOp.cs; uphead.comp / uphead_sc.comp), NHWC, one
+ * thread per output pixel: s[c] = [relu](bilinear(x)) + [relu](skip), out[o] = act(bias[o] +
+ * sum_c w[o][c] s[c]) for o < oc <= 8. With a skip conv (flags bit 3) the skip is recomputed per pixel
+ * from its input sk ([oh][ow][skc], stride 1) by the conv w_sc [c][skc][kh][kw] + b_sc (+ relu). */
+typedef struct sox_uphead_args {
+    const void* x;
+    const void* skip;     /* the skip tensor [oh][ow][c], or the skip conv's input [oh][ow][skc] */
+    const void* w;        /* [oc][c], storage type */
+    const float* bias;    /* [oc] (flags bit 2) */
+    void* y;
+    const void* w_sc;     /* [c][skc][kh][kw], storage type */
+    const float* b_sc;    /* [c] (sc_flags bit 0) */
+    int32_t n, ih, iw, c, oh, ow, oc;
+    float sy, sx;
+    int32_t flags;        /* bit0 relu on the resize, bit1 relu on the skip, bit2 bias, bit3 skip conv, act << 4 */
+    int32_t skc, kh, kw, pt, pl, sc_flags;  /* sc_flags: bit0 bias, bit1 reflect pad, bit2 relu */
+    float sc_pad_value;
+} sox_uphead_args;
+
 #ifdef __cplusplus
 }
 #endif

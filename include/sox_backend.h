@@ -97,6 +97,21 @@ typedef struct sox_tanh_p { float in_scale, out_scale; } sox_tanh_p;         /* 
 typedef struct sox_clip_p { float min, max; } sox_clip_p;                    /* ClipP :134-138 */
 typedef struct sox_depth_to_space_p { int32_t block, crd; } sox_depth_to_space_p; /* DepthToSpaceP :139-145 */
 
+/* Records of the built-in extension ops (ExecOp.Ext with these names; Engine/Fusions/*.cs). */
+typedef struct sox_safediv_p { float eps, lo, hi; } sox_safediv_p;      /* SafeDivP, SafeDivOp.cs:9-13 */
+typedef struct sox_shift_p {                                               /* ShiftP, ChannelShiftOp.cs:9-14 */
+    int32_t axis;                    /* logical spatial axis: 2 = H, 3 = W */
+    int32_t ngroups;                 /* <= 5 */
+    int32_t group_ends[5], offsets[5];
+} sox_shift_p;
+typedef struct sox_uphead_p {                                              /* UpHeadP, UpHeadOp.cs:15-32 */
+    float scales[4];
+    int32_t resize_relu, skip_relu, act;
+    int32_t has_skip_conv;           /* In[1] is the skip conv's input (UpHeadP.SkipConv) */
+    sox_conv_p skip_conv;
+    int32_t skip_w, skip_b;          /* the skip conv's weight / bias value ids (-1 none) */
+} sox_uphead_p;
+
 /* ---- plan (ExecPlan) ---- */
 int sox_plan_create(sox_plan** plan);
 void sox_plan_destroy(sox_plan* plan);

@@ -387,3 +387,43 @@ def ctc_argmax(x, w, bias=None):
         raise ValueError("Recognizer output is invalid.")
     return idx, prob
 
+
+def safe_div(a, b, eps, lo, hi):
+    """SafeDiv (Kernels/FusedKernels.cs:35-57)."""
+    a, b = _f32(a), _f32(b)
+    out = np.empty_like(a)
+    lib().ora_safediv(_p(a), _p(b), _p(out), ctypes.c_long(a.size), ctypes.c_float(eps), ctypes.c_float(lo),
+                      ctypes.c_float(hi))
+    return out
+
+
+def channel_shift(x, axis, ends, offs):
+    """ChannelShift (Kernels/FusedKernels.cs:195-222), NHWC batch."""
+    x = _f32(x)
+    n, h, w, c = x.shape
+    e = (ctypes.c_int * 5)(*ends)
+    o = (ctypes.c_int * 5)(*offs)
+    out = np.empty_like(x)
+    for i in range(n):
+        oi = np.empty((h, w, c), np.float32)
+        lib().ora_channel_shift(_p(np.ascontiguousarray(x[i])), h, w, c, _p(oi), axis, e, o, len(ends))
+        out[i] = oi
+    return out
+
+
+def up_head(x, skip, w, bias, scale, *, resize_relu=False, skip_relu=False, act="none"):
+    """UpHead with a stored skip (Kernels/FusedKernels.cs:62-192), NHWC batch; w [oc, c]."""
+    x, skip, w, bias = _f32(x), _f32(skip), _f32(w), _f32(bias)
+    n, ih, iw, c = x.shape
+    oc = w.shape[0]
+    oh, ow = int(ih * scale), int(iw * scale)
+    out = np.empty((n, oh, ow, oc), np.float32)
+    for i in range(n):
+        oi = np.empty((oh, ow, oc), np.float32)
+        _check(lib().ora_uphead(_p(np.ascontiguousarray(x[i])), ih, iw, c, _p(np.ascontiguousarray(skip[i])), _p(oi),
+                                oh, ow, ctypes.c_float(scale), ctypes.c_float(scale), _p(w.reshape(oc, c)), _p(bias),
+                                oc, int(resize_relu), int(skip_relu), ACT[act] if isinstance(act, str) else act),
+               "up_head")
+        out[i] = oi
+    return out
+

@@ -29,6 +29,12 @@ def f32_params(plan):
         if n.op == "ChannelGate":
             ids.update(n.ins[1:])
             ids.update(r for r in (n.p.b1, n.p.b2) if r >= 0)
+        if n.op == "Ext" and n.ext == "UpHead":
+            from simdonnx_amd import native as N
+            q = N.UpHeadP.from_buffer_copy(n.p)
+            ids.update(n.ins[3:])
+            if q.skip_b >= 0:
+                ids.add(q.skip_b)
     return ids
 
 
@@ -157,6 +163,27 @@ def run_plan(plan, inputs, keep=False, f16_storage=False):
             y = O.global_avg_pool(get(node.ins[0]))
         elif node.op == "MatMul":
             y = O.matmul_bcast(get(node.ins[0]), get(node.ins[1]))
+        elif node.op == "Ext" and node.ext in ("SafeDiv", "ChannelShift", "UpHead"):
+            from simdonnx_amd import native as N  # the records' layout only
+            if node.ext == "SafeDiv":
+                q = N.SafeDivP.from_buffer_copy(node.p)
+                y = O.safe_div(get(node.ins[0]), get(node.ins[1]), q.eps, q.lo, q.hi)
+            elif node.ext == "ChannelShift":
+                q = N.ShiftP.from_buffer_copy(node.p)
+                y = O.channel_shift(get(node.ins[0]), q.axis, list(q.group_ends)[:q.ngroups], list(q.offsets)[:q.ngroups])
+            else:
+                q = N.UpHeadP.from_buffer_copy(node.p)
+                skip = get(node.ins[1])
+                if q.has_skip_conv:  # recomputed by the stem conv's direct kernel (FusedKernels.cs:81-83)
+                    sc = q.skip_conv
+                    acts = {v: k for k, v in O.ACT.items()}
+                    skip = O.conv(skip, get(q.skip_w), get(q.skip_b) if q.skip_b >= 0 else None, None, stride=(1, 1),
+                                  pads=tuple(sc.pads), act=acts[sc.act], pad_mode=sc.pad_mode, pad_value=sc.pad_value,
+                                  algo=1)
+                w = get(node.ins[2])
+                y = O.up_head(get(node.ins[0]), skip, w.reshape(w.shape[0], -1),
+                              get(node.ins[3]) if len(node.ins) > 3 else None, q.scales[3],
+                              resize_relu=bool(q.resize_relu), skip_relu=bool(q.skip_relu), act=q.act)
         else:
             raise NotImplementedError(f"oracle interpreter: {node.op}")
         env[out] = rnd(np.ascontiguousarray(y, dtype=np.float32).reshape(oshape))

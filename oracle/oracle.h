@@ -134,6 +134,14 @@ int ora_unary2(const float* src, long count, int mode, float a, float b, float* 
 int ora_ctc_argmax(const float* x, const float* w, const float* bias, long rows, int inner, int columns, int* indices,
                    float* probs);
 
+/* Built-in extension ops (Kernels/FusedKernels.cs): SafeDiv (:35-57), ChannelShift NHWC one image
+ * (:195-222), UpHead one image with a stored skip (:62-192; w [oc][c], oc <= 8, bias nullable). */
+int ora_safediv(const float* a, const float* b, float* dst, long count, float eps, float lo, float hi);
+int ora_channel_shift(const float* src, int h, int w, int c, float* dst, int axis, const int* ends, const int* offs,
+                      int ngroups);
+int ora_uphead(const float* src, int ih, int iw, int c, const float* skip, float* dst, int oh, int ow, float sy,
+               float sx, const float* w, const float* bias, int oc, int resize_relu, int skip_relu, int act);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1056,4 +1056,66 @@ int ora_ctc_argmax(const float* x, const float* w, const float* bias, long rows,
     return bad ? -1 : 0;
 }
 
+// SafeDiv (Kernels/FusedKernels.cs:35-57): clamp(a / max(b, eps), lo, hi).
+int ora_safediv(const float* a, const float* b, float* dst, long count, float eps, float lo, float hi) {
+    for (long i = 0; i < count; i++) dst[i] = std::min(std::max(a[i] / std::max(b[i], eps), lo), hi);
+    return 0;
+}
+
+// ChannelShift, NHWC, one image (Kernels/FusedKernels.cs:195-222).
+int ora_channel_shift(const float* src, int h, int w, int c, float* dst, int axis, const int* ends, const int* offs,
+                      int ngroups) {
+    for (int y = 0; y < h; y++)
+        for (int x = 0; x < w; x++) {
+            float* o = dst + ((long)y * w + x) * c;
+            int g0 = 0;
+            for (int g = 0; g < ngroups; g++) {
+                const int g1 = ends[g];
+                const int sy = axis == 2 ? y + offs[g] : y, sx = axis == 2 ? x : x + offs[g];
+                for (int ch = g0; ch < g1; ch++)
+                    o[ch] = ((unsigned)sy < (unsigned)h && (unsigned)sx < (unsigned)w) ? src[((long)sy * w + sx) * c + ch] : 0.0f;
+                g0 = g1;
+            }
+            for (int ch = g0; ch < c; ch++) o[ch] = src[((long)y * w + x) * c + ch];
+        }
+    return 0;
+}
+
+// UpHead, one image, the scalar path (Kernels/FusedKernels.cs:62-192): s = ResizePixel(x) with the
+// skip as its addend, acc = bias then acc += s[c] w[o][c] in ascending c, then the activation.
+int ora_uphead(const float* src, int ih, int iw, int c, const float* skip, float* dst, int oh, int ow, float sy,
+               float sx, const float* w, const float* bias, int oc, int resize_relu, int skip_relu, int act) {
+    if (oc > 8) return -1;
+    std::vector<int> y0(oh), y1(oh), x0(ow), x1(ow);
+    std::vector<float> wy(oh), wx(ow);
+    resize_axis(oh, ih, sy, y0.data(), y1.data(), wy.data());
+    resize_axis(ow, iw, sx, x0.data(), x1.data(), wx.data());
+#pragma omp parallel for schedule(static) num_threads(threads())
+    for (int y = 0; y < oh; y++) {
+        std::vector<float> s(c);
+        for (int x = 0; x < ow; x++) {
+            const float* a = src + ((long)y0[y] * iw + x0[x]) * c;
+            const float* b = src + ((long)y0[y] * iw + x1[x]) * c;
+            const float* e = src + ((long)y1[y] * iw + x0[x]) * c;
+            const float* f = src + ((long)y1[y] * iw + x1[x]) * c;
+            const float* k = skip + ((long)y * ow + x) * c;
+            for (int ch = 0; ch < c; ch++) {
+                float top = a[ch] + (b[ch] - a[ch]) * wx[x];
+                float bot = e[ch] + (f[ch] - e[ch]) * wx[x];
+                float v = top + (bot - top) * wy[y];
+                if (resize_relu) v = fmaxf(v, 0.0f);
+                v += skip_relu ? fmaxf(k[ch], 0.0f) : k[ch];
+                s[ch] = v;
+            }
+            float acc[8];
+            for (int o = 0; o < oc; o++) acc[o] = bias ? bias[o] : 0.0f;
+            for (int ch = 0; ch < c; ch++)
+                for (int o = 0; o < oc; o++) acc[o] += s[ch] * w[(long)o * c + ch];
+            float* out = dst + ((long)y * ow + x) * oc;
+            for (int o = 0; o < oc; o++) out[o] = act8(acc[o], act);
+        }
+    }
+    return 0;
+}
+
 }  // extern "C"

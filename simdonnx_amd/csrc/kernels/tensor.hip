@@ -391,3 +391,163 @@ __device__ __forceinline__ void matmul_body(const sox_matmul_args& p) {
 
 extern "C" __global__ void __launch_bounds__(256) sox_matmul_f16(sox_matmul_args p) { matmul_body<half_t>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_matmul_f32(sox_matmul_args p) { matmul_body<float>(p); }
+
+// ------------------------------------------------------------------------------------------
+// SafeDiv (Engine/Fusions/SafeDivOp.cs, Kernels/FusedKernels.cs:35-57): y = clamp(a / max(b, eps),
+// lo, hi), fp32 math whatever the storage (the eps floor survives fp16 storage).
+// ------------------------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void safediv_body(const sox_safediv_args& p) {
+    constexpr int CV = 16 / sizeof(T);
+    typedef typename Vt<T, CV>::V Vec;
+    const long base = gid() * CV;
+    const T* a = (const T*)p.a;
+    const T* b = (const T*)p.b;
+    T* y = (T*)p.y;
+    auto f = [&](float av, float bv) { return fminf(fmaxf(av / fmaxf(bv, p.eps), p.lo), p.hi); };
+    if (base + CV <= p.count) {
+        const Vec av = *(const Vec*)(a + base), bv = *(const Vec*)(b + base);
+        Vec out;
+#pragma unroll
+        for (int e = 0; e < CV; e++) out[e] = (T)f(to_f(av[e]), to_f(bv[e]));
+        *(Vec*)(y + base) = out;
+    } else {
+        for (long i = base; i < p.count; i++) y[i] = (T)f(to_f(a[i]), to_f(b[i]));
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_safediv_f16(sox_safediv_args p) { safediv_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_safediv_f32(sox_safediv_args p) { safediv_body<float>(p); }
+
+// ------------------------------------------------------------------------------------------
+// ChannelShift (Engine/Fusions/ChannelShiftOp.cs, Kernels/FusedKernels.cs:195-222), NHWC: one work
+// item per CV channels of an output pixel (CV > 1 only when every group end is a multiple of CV).
+// ------------------------------------------------------------------------------------------
+template <typename T, int CV>
+__device__ __forceinline__ void shift_body(const sox_shift_args& p) {
+    typedef typename Vt<T, CV>::V Vec;
+    const int cvn = p.c / CV;
+    const long idx = gid();
+    if (idx >= (long)p.n * p.h * p.w * cvn) return;
+    const int c0 = (int)(idx % cvn) * CV;
+    const int pix = (int)(idx / cvn);
+    const int x = pix % p.w, q = pix / p.w, yy = q % p.h, b = q / p.h;
+    int off = 0;
+    bool shifted = false;
+#pragma unroll
+    for (int g = 4; g >= 0; g--)  // the group holding c0: the first g with c0 < ends[g]
+        if (g < p.ngroups && c0 < p.ends[g]) {
+            off = p.offs[g];
+            shifted = true;
+        }
+    int sy = yy, sx = x;
+    if (shifted) {
+        if (p.axis == 2) sy += off;
+        else sx += off;
+    }
+    Vec v;
+    if ((unsigned)sy < (unsigned)p.h && (unsigned)sx < (unsigned)p.w) {
+        v = *(const Vec*)((const T*)p.x + (((long)b * p.h + sy) * p.w + sx) * p.c + c0);
+    } else {
+#pragma unroll
+        for (int e = 0; e < CV; e++) v[e] = (T)0.0f;
+    }
+    *(Vec*)((T*)p.y + (long)pix * p.c + c0) = v;
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_shift_f16_v(sox_shift_args p) { shift_body<half_t, 8>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_shift_f16_s(sox_shift_args p) { shift_body<half_t, 1>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_shift_f32_v(sox_shift_args p) { shift_body<float, 4>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_shift_f32_s(sox_shift_args p) { shift_body<float, 1>(p); }
+
+// ------------------------------------------------------------------------------------------
+// UpHead (Engine/Fusions/UpHeadOp.cs, Kernels/FusedKernels.cs:62-192): one thread per output pixel,
+// CV channels per load (c is a multiple of 4: 16-byte loads for fp32 and c % 8 == 0 fp16, else 8).
+// s[c] = [relu](bilinear(x)) + [relu](skip) (Nhwc.ResizePixel's operations, no contraction), then
+// out[o] = act(bias[o] + sum_c s[c] w[o][c]) in ascending c. The head weights (oc x c <= 1024) and
+// the skip conv's weights (<= 4096) sit in LDS as fp32. With the skip conv the skip channel is
+// recomputed here: bias + sum over taps (ky, kx) and input channels of x w, [relu] (the stem conv's
+// direct order, Nhwc.cs:343-373), constant or reflect padding.
+// ------------------------------------------------------------------------------------------
+template <typename T, int CV>
+__device__ __forceinline__ void uphead_body(const sox_uphead_args& p) {
+#pragma clang fp contract(off)
+    typedef typename Vt<T, CV>::V Vec;
+    __shared__ float ws[1024];
+    __shared__ float wsc[4096];
+    const bool has_sc = (p.flags & 8) != 0;
+    const int nsc = has_sc ? p.c * p.skc * p.kh * p.kw : 0;
+    for (int i = threadIdx.x; i < p.oc * p.c; i += blockDim.x) ws[i] = to_f(((const T*)p.w)[i]);
+    for (int i = threadIdx.x; i < nsc; i += blockDim.x) wsc[i] = to_f(((const T*)p.w_sc)[i]);
+    __syncthreads();
+    const long idx = gid();
+    if (idx >= (long)p.n * p.oh * p.ow) return;
+    const int ox = (int)(idx % p.ow);
+    const int q = (int)(idx / p.ow), oy = q % p.oh, b = q / p.oh;
+    const float fy = ((float)oy + 0.5f) / p.sy - 0.5f, fx = ((float)ox + 0.5f) / p.sx - 0.5f;
+    const float fly = floorf(fy), flx = floorf(fx);
+    const int y0 = min(max((int)fly, 0), p.ih - 1), y1 = min(max((int)fly + 1, 0), p.ih - 1);
+    const int x0 = min(max((int)flx, 0), p.iw - 1), x1 = min(max((int)flx + 1, 0), p.iw - 1);
+    const float wy = fy - fly, wx = fx - flx;
+    const T* img = (const T*)p.x + (long)b * p.ih * p.iw * p.c;
+    const T* pa = img + ((long)y0 * p.iw + x0) * p.c;
+    const T* pb = img + ((long)y0 * p.iw + x1) * p.c;
+    const T* pe = img + ((long)y1 * p.iw + x0) * p.c;
+    const T* pf = img + ((long)y1 * p.iw + x1) * p.c;
+    float acc[8];
+#pragma unroll
+    for (int o = 0; o < 8; o++) acc[o] = (o < p.oc && (p.flags & 4)) ? p.bias[o] : 0.0f;
+    // CV channels at a time: one 16-byte load per tap (and per skip pixel) when c allows
+    for (int c0 = 0; c0 < p.c; c0 += CV) {
+        const Vec va = *(const Vec*)(pa + c0), vb = *(const Vec*)(pb + c0);
+        const Vec ve = *(const Vec*)(pe + c0), vf = *(const Vec*)(pf + c0);
+        Vec vs;
+        if (!has_sc) vs = *(const Vec*)((const T*)p.skip + idx * p.c + c0);
+#pragma unroll
+        for (int u = 0; u < CV; u++) {
+            const int ch = c0 + u;
+            const float a = to_f(va[u]), bb = to_f(vb[u]), e = to_f(ve[u]), f = to_f(vf[u]);
+            const float top = a + (bb - a) * wx;
+            const float bot = e + (f - e) * wx;
+            float v = top + (bot - top) * wy;
+            if (p.flags & 1) v = fmaxf(v, 0.0f);
+            float sk;
+            if (has_sc) {
+                sk = (p.sc_flags & 1) ? p.b_sc[ch] : 0.0f;
+                const T* sx0 = (const T*)p.skip + (long)b * p.oh * p.ow * p.skc;
+                for (int ky = 0; ky < p.kh; ky++) {
+                    int iy = oy + ky - p.pt;
+                    bool rin = (unsigned)iy < (unsigned)p.oh;
+                    if (!rin && (p.sc_flags & 2)) { iy = sox_reflect(iy, p.oh); rin = true; }
+                    for (int kx = 0; kx < p.kw; kx++) {
+                        int ix = ox + kx - p.pl;
+                        bool cin = (unsigned)ix < (unsigned)p.ow;
+                        if (!cin && (p.sc_flags & 2)) { ix = sox_reflect(ix, p.ow); cin = true; }
+                        const float* wk = wsc + ((long)ch * p.skc * p.kh + ky) * p.kw + kx;
+                        for (int ci = 0; ci < p.skc; ci++) {
+                            const float xv = (rin && cin) ? to_f(sx0[((long)iy * p.ow + ix) * p.skc + ci]) : p.sc_pad_value;
+                            sk = __builtin_fmaf(xv, wk[(long)ci * p.kh * p.kw], sk);
+                        }
+                    }
+                }
+                if (p.sc_flags & 4) sk = fmaxf(sk, 0.0f);
+            } else {
+                sk = to_f(vs[u]);
+            }
+            v += (p.flags & 2) ? fmaxf(sk, 0.0f) : sk;
+#pragma unroll
+            for (int o = 0; o < 8; o++)
+                if (o < p.oc) acc[o] = acc[o] + v * ws[o * p.c + ch];
+        }
+    }
+    const int act = (p.flags >> 4) & 15;
+    T* yo = (T*)p.y + idx * p.oc;
+#pragma unroll
+    for (int o = 0; o < 8; o++)
+        if (o < p.oc) yo[o] = (T)sox_act(acc[o], act);
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_uphead_f16_v(sox_uphead_args p) { uphead_body<half_t, 8>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_uphead_f16_s(sox_uphead_args p) { uphead_body<half_t, 4>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_uphead_f32_v(sox_uphead_args p) { uphead_body<float, 4>(p); }
+

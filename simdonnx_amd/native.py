@@ -120,6 +120,19 @@ class DepthToSpaceP(ctypes.Structure):
     _fields_ = [("block", c_int32), ("crd", c_int32)]
 
 
+class SafeDivP(ctypes.Structure):
+    _fields_ = [("eps", c_float), ("lo", c_float), ("hi", c_float)]
+
+
+class ShiftP(ctypes.Structure):
+    _fields_ = [("axis", c_int32), ("ngroups", c_int32), ("group_ends", c_int32 * 5), ("offsets", c_int32 * 5)]
+
+
+class UpHeadP(ctypes.Structure):
+    _fields_ = [("scales", c_float * 4), ("resize_relu", c_int32), ("skip_relu", c_int32), ("act", c_int32),
+                ("has_skip_conv", c_int32), ("skip_conv", ConvP), ("skip_w", c_int32), ("skip_b", c_int32)]
+
+
 class Bind(ctypes.Structure):
     _fields_ = [("slot", c_int32), ("pad_", c_int32), ("offset", c_uint64), ("size", c_uint64)]
 

@@ -617,6 +617,45 @@ class PlanBuilder:
         y = self.activation(tuple(va.shape[:-1]) + (vb.shape[-1],), None, name)
         return self._node("MatMul", [a, b], [y], None, name)
 
+    # ---- the built-in extension ops (ExecOp.Ext, Engine/Fusions/*.cs) ----
+    def safe_div(self, a, b, eps, lo, hi, name=""):
+        """SafeDiv: clamp(a / max(b, eps), lo, hi) over same-shape operands (SafeDivP)."""
+        v = self.values[a]
+        return self.ext("SafeDiv", [a, b], v.shape, bytes(N.SafeDivP(eps, lo, hi)), v.layout, name or "safediv")
+
+    def channel_shift(self, x, axis, group_ends, offsets, name=""):
+        """ChannelShift of an NHWC image: channel group g shifted by offsets[g] along H (axis 2) or W (3)."""
+        v = self.values[x]
+        p = N.ShiftP()
+        p.axis, p.ngroups = axis, len(group_ends)
+        p.group_ends[:len(group_ends)] = list(group_ends)
+        p.offsets[:len(offsets)] = list(offsets)
+        return self.ext("ChannelShift", [x], v.shape, bytes(p), v.layout, name or "shift")
+
+    def up_head(self, x, skip, w, b, scale, *, resize_relu=False, skip_relu=False, act="none", skip_conv=None,
+                name=""):
+        """UpHead: act(bias + W . ([relu](bilinear x`scale`(x)) + [relu](skip))), W [oc, c] (UpHeadP). With
+        skip_conv = (w_sc [c, skc, kh, kw], b_sc, pads (t, l, b, r), pad_mode, pad_value, act) the `skip`
+        argument is that stride-1 conv's input and the skip is recomputed from it."""
+        n, h, ww, c = self.values[x].phys
+        oc = np.asarray(w).shape[0]
+        wv = self.const(np.asarray(w, np.float32).reshape(oc, c, 1, 1), name + ".w")
+        ins = [x, skip, wv] + ([] if b is None else [self.const(b, name + ".b")])
+        p = N.UpHeadP()
+        p.scales[:] = [1.0, 1.0, float(scale), float(scale)]
+        p.resize_relu, p.skip_relu, p.act = int(resize_relu), int(skip_relu), ACT[act]
+        p.skip_w = p.skip_b = -1
+        if skip_conv is not None:
+            w_sc, b_sc, pads, pad_mode, pad_value, sc_act = skip_conv
+            kh, kw = np.asarray(w_sc).shape[2:]
+            p.has_skip_conv = 1
+            p.skip_conv = ConvP(tuple(pads), (1, 1), (kh, kw), act=sc_act, pad_mode=pad_mode, pad_value=pad_value).native()
+            p.skip_w = self.const(w_sc, name + ".w_sc")
+            p.skip_b = -1 if b_sc is None else self.const(b_sc, name + ".b_sc")
+        y = self.activation((n, oc, int(h * scale), int(ww * scale)), NHWC, name or "uphead")
+        self._node("Ext", ins, [y], bytes(p), name or "uphead", ext="UpHead")
+        return y
+
     def ext(self, name, ins, out_shape, params: bytes = b"", layout=None, node_name=""):
         """ExecOp.Ext node of a consumer-registered operator."""
         y = self.activation(out_shape, layout, node_name or name)

@@ -1,8 +1,9 @@
 """Writes the golden vectors that pin the oracle's restatement of the rest of the GPU op surface:
 bilinear resize (+ relu, + addend), constant / reflect pad, average pool (with and without the
 padded taps counted), DepthToSpace / SpaceToDepth (CRD and DCR), LeakyRelu / Tanh / Clip / Erf,
-global average pool, batched MatMul with a broadcast right operand and the CTC head's fused
-projection + argmax + softmax probability.
+global average pool, batched MatMul with a broadcast right operand, the CTC head's fused
+projection + argmax + softmax probability, and the built-in extension ops SafeDiv, ChannelShift and
+UpHead (with a stored skip and with the skip recomputed by its 3x3 conv).
 
 Each expected output is a library routine or the ONNX definition evaluated by torch in float64:
 F.interpolate(bilinear, align_corners=False), F.pad(constant / reflect), F.avg_pool2d,
@@ -126,6 +127,50 @@ def main():
     out["ctc_x"], out["ctc_w"], out["ctc_b"] = x, w, b
     out["ctc_idx"] = torch.argmax(lg, dim=1).numpy().astype(np.int32)
     out["ctc_prob"] = torch.softmax(lg, dim=1).max(dim=1).values.numpy().astype(np.float32)
+    # built-in extension ops: SafeDiv, ChannelShift (zero-filled shifts per channel group), UpHead
+    a = synth.normal(990, 1, (2, 5, 7, 16), 1.0)
+    b = synth.uniform(990, 2, (2, 5, 7, 16), -0.5, 2.0)
+    out["sd_a"], out["sd_b"] = a, b
+    out["sd_y"] = torch.clamp(t64(a) / torch.clamp(t64(b), min=1e-3), -4.0, 4.0).numpy().astype(np.float32)
+    x = synth.normal(991, 1, (1, 6, 9, 20), 1.0)
+    out["sh_x"] = x
+    ends, offs = [4, 8, 12, 16, 20], [-2, -1, 0, 1, 2]
+    for axis in (2, 3):
+        y = np.zeros_like(x, dtype=np.float64)
+        g0 = 0
+        for g1, o in zip(ends, offs):
+            src = np.roll(x[..., g0:g1].astype(np.float64), -o, axis=axis - 1)
+            if o > 0:
+                sl = [slice(None)] * 4
+                sl[axis - 1] = slice(x.shape[axis - 1] - o, None)
+                src[tuple(sl)] = 0
+            elif o < 0:
+                sl = [slice(None)] * 4
+                sl[axis - 1] = slice(0, -o)
+                src[tuple(sl)] = 0
+            y[..., g0:g1] = src
+            g0 = g1
+        out[f"sh_y{axis}"] = y.astype(np.float32)
+    for i, (c, oc, sc) in enumerate([(16, 1, False), (32, 2, True)]):
+        x = synth.normal(992 + i, 1, (1, 12, 10, c), 1.0)
+        w = synth.normal(992 + i, 3, (oc, c), 0.2)
+        bb = synth.uniform(992 + i, 4, (oc,), -0.1, 0.1)
+        r = F.interpolate(nchw(x), scale_factor=(2.0, 2.0), mode="bilinear", align_corners=False,
+                          recompute_scale_factor=False)
+        r = torch.relu(r)
+        if sc:
+            sk_in = synth.normal(992 + i, 2, (1, 24, 20, 3), 1.0)
+            w_sc = synth.normal(992 + i, 5, (c, 3, 3, 3), 0.3)
+            b_sc = synth.uniform(992 + i, 6, (c,), -0.1, 0.1)
+            skip = torch.relu(F.conv2d(nchw(sk_in), t64(w_sc), t64(b_sc), padding=1))
+            out[f"uh{i}_skin"], out[f"uh{i}_wsc"], out[f"uh{i}_bsc"] = sk_in, w_sc, b_sc
+        else:
+            sk = synth.normal(992 + i, 2, (1, 24, 20, c), 1.0)
+            skip = nchw(sk)
+            out[f"uh{i}_skip"] = sk
+        s_ = r + torch.relu(skip)
+        y = torch.sigmoid(F.conv2d(s_, t64(w).reshape(oc, c, 1, 1), t64(bb)))
+        out[f"uh{i}_x"], out[f"uh{i}_w"], out[f"uh{i}_b"], out[f"uh{i}_y"] = x, w, bb, nhwc(y)
     path = os.path.join(HERE, "golden_ops.npz")
     np.savez_compressed(path, **out)
     print("wrote", path, os.path.getsize(path), "bytes")

@@ -173,3 +173,62 @@ def test_matmul(hip, batch, m, k, n, bcast, half):
     y = pb.matmul(av, bv, name="mm")
     got = run(hip, pb.build(y), [a, b], half, "matmul")
     assert max_rel(got, O.matmul_bcast(a, b)) < TOL[half]
+
+
+@HALF
+@pytest.mark.parametrize("shape,eps,lo,hi", [((2, 5, 7, 16), 1e-3, -4.0, 4.0), ((3, 1001), 1e-6, 0.0, 1.0)])
+def test_safe_div(hip, shape, eps, lo, hi, half):
+    a = img(11, shape, half)
+    b = synth.uniform(11, 2, shape, -0.5, 2.0)
+    b = f16(b) if half else b
+    pb = PlanBuilder()
+    av, bv = pb.input(shape, None, "a"), pb.input(shape, None, "b")
+    y = pb.safe_div(av, bv, eps, lo, hi, name="sd")
+    got = run(hip, pb.build(y), [a, b], half, "safediv")
+    assert max_rel(got, O.safe_div(a, b, eps, lo, hi)) < TOL[half]
+
+
+@HALF
+@pytest.mark.parametrize("shape,axis,ends,offs", [((1, 6, 9, 20), 2, (4, 8, 12, 16, 20), (-2, -1, 0, 1, 2)),
+                                                  ((2, 40, 40, 64), 3, (16, 32, 48, 56), (1, -1, 3, -3)),
+                                                  ((1, 7, 5, 13), 3, (3, 9), (2, -1))])
+def test_channel_shift(hip, shape, axis, ends, offs, half):
+    n, h, w, c = shape
+    x = img(12, shape, half)
+    pb = PlanBuilder()
+    xv = pb.input((n, c, h, w), NHWC, "x")
+    y = pb.channel_shift(xv, axis, ends, offs, name="sh")
+    got = run(hip, pb.build(y), [x], half, "shift")
+    assert np.array_equal(got, O.channel_shift(x, axis, list(ends), list(offs)))
+
+
+@HALF
+@pytest.mark.parametrize("c,oc,act,skip_conv,hw", [(16, 1, "sigmoid", False, (12, 10)), (32, 2, "sigmoid", True, (12, 10)),
+                                                   (96, 8, "relu", False, (30, 30)), (24, 1, "none", True, (60, 60))])
+def test_up_head(hip, c, oc, act, skip_conv, hw, half):
+    """UpHead with a stored skip and with the skip recomputed from its 3x3 conv's input (reflect pad in
+    the last case)."""
+    h, w = hw
+    x = img(13, (1, h, w, c), half)
+    wh = synth.normal(13, 3, (oc, c), 0.2)
+    bh = synth.uniform(13, 4, (oc,), -0.1, 0.1)
+    pb = PlanBuilder()
+    xv = pb.input((1, c, h, w), NHWC, "x")
+    if skip_conv:
+        sk = img(14, (1, 2 * h, 2 * w, 3), half)
+        w_sc = synth.normal(13, 5, (c, 3, 3, 3), 0.3)
+        b_sc = synth.uniform(13, 6, (c,), -0.1, 0.1)
+        mode = 1 if c == 24 else 0
+        sv = pb.input((1, 3, 2 * h, 2 * w), NHWC, "skin")
+        y = pb.up_head(xv, sv, wh, bh, 2, resize_relu=True, skip_relu=True, act=act,
+                       skip_conv=(w_sc, b_sc, (1, 1, 1, 1), mode, 0.0, "relu"), name="uh")
+        w_sc_r = f16(w_sc) if half else w_sc
+        skip = O.conv(sk, w_sc_r, b_sc, None, stride=(1, 1), pads=(1, 1, 1, 1), act="relu", pad_mode=mode, algo=1)
+    else:
+        sk = img(14, (1, 2 * h, 2 * w, c), half)
+        sv = pb.input((1, c, 2 * h, 2 * w), NHWC, "skip")
+        y = pb.up_head(xv, sv, wh, bh, 2, resize_relu=True, skip_relu=True, act=act, name="uh")
+        skip = sk
+    got = run(hip, pb.build(y), [x, sk], half, "uphead")
+    want = O.up_head(x, skip, f16(wh) if half else wh, bh, 2, resize_relu=True, skip_relu=True, act=act)
+    assert max_rel(got, want) < TOL[half]

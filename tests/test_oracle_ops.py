@@ -104,3 +104,19 @@ def test_ctc_argmax_ties_and_invalid():
     x[3, 7] = np.inf
     with pytest.raises(ValueError):
         O.ctc_argmax(x, w, b)
+
+
+def test_builtin_ext_ops_golden():
+    """SafeDiv, ChannelShift and UpHead (Engine/Fusions/*.cs, Kernels/FusedKernels.cs) vs torch / numpy."""
+    assert max_rel(O.safe_div(G["sd_a"], G["sd_b"], 1e-3, -4.0, 4.0), G["sd_y"]) < 1e-6
+    ends, offs = [4, 8, 12, 16, 20], [-2, -1, 0, 1, 2]
+    for axis in (2, 3):
+        assert np.array_equal(O.channel_shift(G["sh_x"], axis, ends, offs), G[f"sh_y{axis}"])
+    # a stored skip; and the skip recomputed by its conv (the oracle's direct conv, then the stored form)
+    got0 = O.up_head(G["uh0_x"], G["uh0_skip"], G["uh0_w"], G["uh0_b"], 2.0, resize_relu=True, skip_relu=True,
+                     act="sigmoid")
+    assert max_rel(got0, G["uh0_y"]) < 2e-6
+    skip = O.conv(G["uh1_skin"], G["uh1_wsc"], G["uh1_bsc"], None, stride=(1, 1), pads=(1, 1, 1, 1), act="relu",
+                  algo=1)
+    got1 = O.up_head(G["uh1_x"], skip, G["uh1_w"], G["uh1_b"], 2.0, resize_relu=True, skip_relu=True, act="sigmoid")
+    assert max_rel(got1, G["uh1_y"]) < 2e-6
