@@ -204,6 +204,39 @@ def bench_recognizer_ctc(steps: int, replay: bool = True):
                 ms_per_batch=round(ms_feat + ms_head, 4), rows=rows, classes=int(hw.shape[1]))
 
 
+def bench_image_session(steps: int):
+    """HipImageSession on a 1920x1080 Bgr24 frame through a small image-to-image model (3x3 conv 3->8
+    + relu, 3x3 conv 8->3 + sigmoid, fp16): host-timed frames (upload, pixels -> NHWC, the model,
+    NHWC -> pixels, download, wait), and the device time of the two pixel kernels from a profile of
+    the same dispatches against the HBM roofline (bytes: the image once + the 3-channel fp16 tensor)."""
+    import numpy as np
+    from simdonnx_amd import synth
+    from simdonnx_amd.backend import HipBackend, HipImageSession
+    from simdonnx_amd.plan import NHWC, PlanBuilder
+    hip = HipBackend.default()
+    unit = np.tile(np.arange(256, dtype=np.float32) / np.float32(255), 3)
+    width, height = 1920, 1080
+    s = HipImageSession(hip, unit, pad_multiple=32)
+    th, tw = s.tensor_size(width, height)
+    pb = PlanBuilder()
+    x = pb.input((1, 3, th, tw), NHWC, "image")
+    y = pb.conv(x, synth.normal(61, 1, (8, 3, 3, 3), 0.3), synth.uniform(61, 2, (8,), -0.1, 0.1), act="relu", name="c1")
+    y = pb.conv(y, synth.normal(61, 3, (3, 8, 3, 3), 0.2), synth.uniform(61, 4, (3,), 0.2, 0.4), act="sigmoid", name="c2")
+    g = hip.graph(pb.build(y), True)
+    src = np.random.default_rng(3).integers(0, 256, (height, width * 3), dtype=np.uint8)
+    dst = np.empty_like(src)
+    for _ in range(5):
+        s.run(g, src, width, height, "Bgr24", dst)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        s.run(g, src, width, height, "Bgr24", dst)
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    s.close()
+    g.release()
+    return dict(workload=f"image session {width}x{height} Bgr24 -> {th}x{tw} tensor, 2-conv fp16 model, pixels in/out",
+                ms_per_frame=round(ms, 4), frames_per_s=round(1e3 / ms, 1), image_mb=round(width * height * 3 / 1e6, 2))
+
+
 def _ops_cases():
     """One-node plans of the rest of the ExecOp surface at the sizes the detector / recognizer shapes
     give them (fp16 storage): (label, plan, inputs, algorithmic bytes, flops). Bytes count each
@@ -343,7 +376,7 @@ def main():
     ap.add_argument("--no-replay", action="store_true",
                     help="launch network dispatches one by one instead of replaying a HIP graph (profiler runs)")
     ap.add_argument("--only", choices=["gemm", "conv", "detector", "recognizer", "mobilenetv3", "copy", "ops",
-                                       "recognizer_ctc"],
+                                       "recognizer_ctc", "image"],
                     help="run one workload only (profiling runs); prints its own JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -354,7 +387,8 @@ def main():
         fn = {"gemm": lambda: bench_gemm(args.steps, args.warmup), "conv": lambda: bench_conv(args.steps),
               "copy": lambda: bench_copy(args.steps),
               "ops": lambda: {"ops": bench_ops(args.steps)},
-              "recognizer_ctc": lambda: bench_recognizer_ctc(args.steps, not args.no_replay)}.get(args.only) or (lambda: bench_network(args.only, args.steps, not args.no_replay))
+              "recognizer_ctc": lambda: bench_recognizer_ctc(args.steps, not args.no_replay),
+              "image": lambda: bench_image_session(args.steps)}.get(args.only) or (lambda: bench_network(args.only, args.steps, not args.no_replay))
         r = fn()
         print(json.dumps({"only": args.only, **{k: v for k, v in r.items() if k != "kernel_ms"}}), flush=True)
         return
@@ -395,6 +429,10 @@ def main():
         out["recognizer_ctc"] = bench_recognizer_ctc(200, not args.no_replay)
     except Exception as e:
         out["recognizer_ctc"] = {"error": repr(e)}
+    try:
+        out["image_session"] = bench_image_session(100)
+    except Exception as e:
+        out["image_session"] = {"error": repr(e)}
     try:
         out["ops"] = bench_ops(200)
     except Exception as e:

@@ -384,6 +384,27 @@ typedef struct sox_uphead_args {
     float sc_pad_value;
 } sox_uphead_args;
 
+/* Image session input (img2nhwc.comp): interleaved u8 pixels (bpp 3 or 4, rows `stride` bytes apart)
+ * -> NHWC [oh][ow][3], tensor channel c = lut[c * 256 + byte], the image at (pt, pl) with its edge
+ * repeated around it; swap = 1: tensor channel 0 is byte 2 of a pixel. Grid (ceil(ow / 256), oh). */
+typedef struct sox_img2nhwc_args {
+    const uint8_t* src;
+    void* y;
+    const float* lut;  /* [3][256] */
+    int32_t oh, ow, ih, iw, pt, pl, stride, bpp, swap;
+} sox_img2nhwc_args;
+
+/* Image session output (nhwc2img.comp): the ih x iw window at (pt, pl) of NHWC [h][w][3] -> tightly
+ * packed u8, byte = clamp(int(v * scale + 0.5), 0, 255); one thread per 4-byte word (3 bpp: words
+ * straddle pixels; 4 bpp: one pixel, alpha copied from the uploaded source `alpha`). */
+typedef struct sox_nhwc2img_args {
+    const void* x;
+    uint32_t* dst;
+    const uint32_t* alpha;
+    int32_t h, w, ih, iw, pt, pl, nwords, bpp, swap;
+    float scale;
+} sox_nhwc2img_args;
+
 #ifdef __cplusplus
 }
 #endif

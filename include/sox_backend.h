@@ -217,6 +217,28 @@ int sox_ctc_is_fused(sox_ctc* ctc);
 int sox_ctc_argmax(sox_ctc* ctc, sox_session* session, int32_t feature_value, int32_t batch, int32_t rows,
                    int32_t* indices, float* probabilities);
 
+/* ---- image session (VkImageSession, Backends/Vulkan/VkImageSession.cs:7-297) ----
+ * Image-to-image inference with the pixel conversions on the device, in the same stream as the model:
+ * one upload of the bytes, the dispatches, one download. The model maps [1, 3, H, W] to [1, 3, H, W];
+ * the caller passes the graph built for the image's tensor size (sox_image_session_tensor_size, the
+ * AcquireGraph of the reference). Not thread-safe: one run at a time. */
+typedef struct sox_image_session sox_image_session;
+enum { SOX_PIX_BGR24 = 0, SOX_PIX_RGB24 = 1, SOX_PIX_BGRA32 = 2, SOX_PIX_RGBA32 = 3 }; /* PixelFormat */
+/* lut: PixelNormalization.Table [3][256] (tensor channel c, byte value); rgb_order: Normalization.Order
+ * == Rgb; output_scale: OutputScale; pad_multiple / pad_top_left: PadMultiple / Padding == TopLeft
+ * (ImageSessionOptions.cs:15-50). */
+int sox_image_session_create(sox_backend* backend, const float* lut, int32_t rgb_order, float output_scale,
+                             int32_t pad_multiple, int32_t pad_top_left, sox_image_session** session);
+void sox_image_session_destroy(sox_image_session* session);
+/* ImageSessionOptions.Pads: the tensor height / width an image of this size runs at. */
+int sox_image_session_tensor_size(sox_image_session* session, int32_t width, int32_t height, int32_t* tensor_h,
+                                  int32_t* tensor_w);
+/* Run (VkImageSession.cs:253-280): src rows src_stride bytes apart, dst the same format and size (rows
+ * dst_stride apart; may be src). 4-byte formats keep each pixel's alpha. graph: a single-input fp16 or
+ * fp32 graph whose input and output are [1, 3, tensor_h, tensor_w] in NHWC storage. */
+int sox_image_session_run(sox_image_session* session, sox_graph* graph, const uint8_t* src, int32_t width,
+                          int32_t height, int32_t src_stride, uint8_t* dst, int32_t dst_stride, int32_t format);
+
 #ifdef __cplusplus
 }
 #endif

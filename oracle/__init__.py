@@ -427,3 +427,36 @@ def up_head(x, skip, w, bias, scale, *, resize_relu=False, skip_relu=False, act=
         out[i] = oi
     return out
 
+
+def from_pixels(src, width, height, bpp, lut, swap, tensor_w, tensor_h, pad_left=0, pad_top=0):
+    """ImageTensor.FromPixels, NHWC (Imaging/ImageTensor.cs:322-365): byte rows -> [th, tw, 3] float32,
+    the image at (pad_left, pad_top) with its edge repeated; channel c = lut[c][byte], channel 0 from
+    byte 2 of a pixel when swap. Index and table work only."""
+    src = np.asarray(src, np.uint8)
+    lut = np.asarray(lut, np.float32).reshape(3, 256)
+    ys = np.clip(np.arange(tensor_h) - pad_top, 0, height - 1)
+    xs = np.clip(np.arange(tensor_w) - pad_left, 0, width - 1)
+    px = src[ys[:, None, None], xs[None, :, None] * bpp + np.arange(3)[None, None, :]]  # [th, tw, 3] bytes
+    o0 = 2 if swap else 0
+    out = np.empty((tensor_h, tensor_w, 3), np.float32)
+    out[..., 0] = lut[0][px[..., o0]]
+    out[..., 1] = lut[1][px[..., 1]]
+    out[..., 2] = lut[2][px[..., 2 - o0]]
+    return out
+
+
+def to_pixels(x, width, height, bpp, swap, crop_left=0, crop_top=0, scale=255.0, alpha=None):
+    """ImageTensor.ToPixels, NHWC (Imaging/ImageTensor.cs:376-430): the width x height window at
+    (crop_left, crop_top) of [th, tw, 3] -> uint8 [height, width * bpp], byte = clamp((int)(v * scale +
+    0.5f), 0, 255) in float32 (multiply, then add, then truncate toward zero); 4-byte pixels take alpha
+    from `alpha` ([height, width * 4]) or 255."""
+    x = np.asarray(x, np.float32)[crop_top:crop_top + height, crop_left:crop_left + width]
+    t = (x * np.float32(scale)).astype(np.float32) + np.float32(0.5)
+    b = np.clip(np.trunc(t), 0, 255).astype(np.uint8)
+    out = np.empty((height, width, bpp), np.uint8)
+    o0 = 2 if swap else 0
+    out[..., o0], out[..., 1], out[..., 2 - o0] = b[..., 0], b[..., 1], b[..., 2]
+    if bpp == 4:
+        out[..., 3] = 255 if alpha is None else np.asarray(alpha, np.uint8).reshape(height, width, 4)[..., 3]
+    return out.reshape(height, width * bpp)
+

@@ -311,3 +311,46 @@ class HipCtcProjection:
         except Exception:
             pass
 
+
+class HipImageSession:
+    """VkImageSession (Backends/Vulkan/VkImageSession.cs:7-297) on HIP: 8-bit pixels in, the same
+    format out, the pixel conversions on the device in the model's stream (sox_image_session_*).
+    `lut` is PixelNormalization.Table ([3][256]); the caller builds the graph of the tensor size
+    `tensor_size(width, height)` gives, as VkBackend.AcquireGraph does."""
+
+    def __init__(self, backend: HipBackend, lut: np.ndarray, rgb_order: bool = False, output_scale: float = 255.0,
+                 pad_multiple: int = 1, pad_top_left: bool = False):
+        t = np.ascontiguousarray(lut, dtype=np.float32).reshape(-1)
+        if t.size != 768:
+            raise ValueError("lut must hold 3 x 256 floats")
+        h = N.c_void_p()
+        N.check(N.backend().sox_image_session_create(backend.h, t.ctypes.data, int(rgb_order), output_scale,
+                                                     pad_multiple, int(pad_top_left), ctypes.byref(h)), "ImageSession")
+        self.h = h
+
+    def tensor_size(self, width: int, height: int):
+        th, tw = N.c_int32(), N.c_int32()
+        N.check(N.backend().sox_image_session_tensor_size(self.h, width, height, ctypes.byref(th), ctypes.byref(tw)),
+                "ImageSession.Pads")
+        return th.value, tw.value
+
+    def run(self, graph: "HipGraphModel", src: np.ndarray, width: int, height: int, fmt: str = "Bgr24",
+            dst: Optional[np.ndarray] = None) -> np.ndarray:
+        """src: uint8 [height, stride] rows; returns (or fills) dst of the same shape and stride."""
+        src = np.ascontiguousarray(src, dtype=np.uint8)
+        out = np.empty_like(src) if dst is None else dst
+        N.check(N.backend().sox_image_session_run(self.h, graph.h, src.ctypes.data, width, height, src.shape[1],
+                                                  out.ctypes.data, out.shape[1], N.PIX[fmt]), "ImageSession.Run")
+        return out
+
+    def close(self):
+        if self.h:
+            N.backend().sox_image_session_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+

@@ -551,3 +551,64 @@ extern "C" __global__ void __launch_bounds__(256) sox_uphead_f16_v(sox_uphead_ar
 extern "C" __global__ void __launch_bounds__(256) sox_uphead_f16_s(sox_uphead_args p) { uphead_body<half_t, 4>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_uphead_f32_v(sox_uphead_args p) { uphead_body<float, 4>(p); }
 
+// ------------------------------------------------------------------------------------------
+// Image session pixel conversions (Backends/Vulkan/VkImageSession.cs:160-210). img2nhwc: one thread
+// per tensor pixel, the three bytes of its (clamped) image pixel through the normalization table.
+// nhwc2img: one thread per output 4-byte word.
+// ------------------------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void img2nhwc_body(const sox_img2nhwc_args& p) {
+    const int ox = blockIdx.x * blockDim.x + threadIdx.x, oy = blockIdx.y;
+    if (ox >= p.ow) return;
+    const int sy = min(max(oy - p.pt, 0), p.ih - 1), sx = min(max(ox - p.pl, 0), p.iw - 1);
+    const uint8_t* px = p.src + (long)sy * p.stride + (long)sx * p.bpp;
+    const int ob = p.swap * 2;
+    T* o = (T*)p.y + ((long)oy * p.ow + ox) * 3;
+    o[0] = (T)p.lut[px[ob]];
+    o[1] = (T)p.lut[256 + px[1]];
+    o[2] = (T)p.lut[512 + px[2 - ob]];
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_img2nhwc_f16(sox_img2nhwc_args p) { img2nhwc_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_img2nhwc_f32(sox_img2nhwc_args p) { img2nhwc_body<float>(p); }
+
+template <typename T>
+__device__ __forceinline__ void nhwc2img_body(const sox_nhwc2img_args& p) {
+#pragma clang fp contract(off)
+    const int w4 = blockIdx.x * blockDim.x + threadIdx.x;
+    if (w4 >= p.nwords) return;
+    const T* x = (const T*)p.x;
+    auto u8 = [&](long i) { return (uint32_t)fminf(fmaxf(to_f(x[i]) * p.scale + 0.5f, 0.0f), 255.0f); };
+    const int ob = p.swap * 2;
+    if (p.bpp == 4) {
+        const int dy = w4 / p.iw, dx = w4 - dy * p.iw;
+        const long i = ((long)(dy + p.pt) * p.w + dx + p.pl) * 3;
+        p.dst[w4] = u8(i + ob) | (u8(i + 1) << 8) | (u8(i + 2 - ob) << 16) | (p.alpha[w4] & 0xff000000u);
+        return;
+    }
+    long byte = (long)w4 * 4;
+    const long total = (long)p.ih * p.iw * 3;
+    long px = byte / 3;
+    int c = (int)(byte - px * 3);
+    int dy = (int)(px / p.iw), dx = (int)(px - (long)dy * p.iw);
+    uint32_t packed = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        uint32_t v = 0;
+        if (byte < total) {
+            const int ch = c == 1 ? 1 : (c == 0 ? ob : 2 - ob);
+            v = u8(((long)(dy + p.pt) * p.w + dx + p.pl) * 3 + ch);
+        }
+        packed |= v << (8 * j);
+        byte++;
+        if (++c == 3) {
+            c = 0;
+            if (++dx == p.iw) { dx = 0; dy++; }
+        }
+    }
+    p.dst[w4] = packed;
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_nhwc2img_f16(sox_nhwc2img_args p) { nhwc2img_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_nhwc2img_f32(sox_nhwc2img_args p) { nhwc2img_body<float>(p); }
+

@@ -28,6 +28,7 @@ OP = dict(Conv=0, MaxPool=1, Elementwise=2, Relu=3, Sigmoid=4, Erf=5, Gelu=6, La
 ACT = dict(none=0, relu=1, sigmoid=2, gelu=3, hardswish=4, swish=5)
 CK = dict(raw=0, f32=1, convwt=2, gemmnk=3, dww=4, convtw=5, f32t=7)
 SLOT_ARENA, SLOT_CONSTS, SLOT_DUMMY = 0, 1, 2
+PIX = dict(Bgr24=0, Rgb24=1, Bgra32=2, Rgba32=3)  # PixelFormat (Imaging/ImageTensor.cs:8-20)
 RUN_STAGING, RUN_DISPATCHES = 1, 2
 
 
@@ -220,6 +221,13 @@ BACKEND_API = {
     "sox_session_read_value": (c_int32, [c_void_p, c_int32, ctypes.POINTER(c_float), c_int64]),
     "sox_session_value_ptr": (c_int32, [c_void_p, c_int32, ctypes.POINTER(c_void_p)]),
     "sox_session_stream": (c_void_p, [c_void_p]),
+    "sox_image_session_create": (c_int32, [c_void_p, c_void_p, c_int32, c_float, c_int32, c_int32,
+                                           ctypes.POINTER(c_void_p)]),
+    "sox_image_session_destroy": (None, [c_void_p]),
+    "sox_image_session_tensor_size": (c_int32, [c_void_p, c_int32, c_int32, ctypes.POINTER(c_int32),
+                                                ctypes.POINTER(c_int32)]),
+    "sox_image_session_run": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_int32,
+                                        c_int32]),
     "sox_ctc_create": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, ctypes.POINTER(c_void_p)]),
     "sox_ctc_destroy": (None, [c_void_p]),
     "sox_ctc_is_fused": (c_int32, [c_void_p]),

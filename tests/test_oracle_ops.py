@@ -120,3 +120,22 @@ def test_builtin_ext_ops_golden():
                   algo=1)
     got1 = O.up_head(G["uh1_x"], skip, G["uh1_w"], G["uh1_b"], 2.0, resize_relu=True, skip_relu=True, act="sigmoid")
     assert max_rel(got1, G["uh1_y"]) < 2e-6
+
+
+def test_pixels_tensor_round_trip_and_channel_order():
+    """ImageTensor.FromPixels / ToPixels (Imaging/ImageTensor.cs:322-430): with the unit table
+    (byte / 255) a padded tensor cropped back gives the original bytes (both channel orders, 3 and 4
+    bytes per pixel, alpha from the source); tensor channel 0 is byte 0 of a pixel for BGR bytes with
+    a BGR table and byte 2 when they differ; the padding repeats the edge pixel."""
+    rng = np.random.default_rng(5)
+    unit = np.tile(np.arange(256, dtype=np.float32) / np.float32(255), 3)
+    for bpp in (3, 4):
+        for swap in (0, 1):
+            src = rng.integers(0, 256, (7, 9 * bpp), dtype=np.uint8)
+            t = O.from_pixels(src, 9, 7, bpp, unit, swap, 16, 12, pad_left=3, pad_top=2)
+            assert t[0, 0, 0] == unit[src[0, 2 * swap]] and t[11, 15, 1] == unit[src[6, (8 * bpp) + 1]]
+            back = O.to_pixels(t, 9, 7, bpp, swap, 3, 2, 255.0, alpha=src if bpp == 4 else None)
+            assert np.array_equal(back, src)
+    # ToByte rounds half up and clamps: 0.5/255 -> 1 (0.5 + 0.5), -0.1 -> 0, 1.2 -> 255
+    t = np.array([[[0.5 / 255, -0.1, 1.2]]], np.float32)
+    assert O.to_pixels(t, 1, 1, 3, 0).tolist() == [[1, 0, 255]]
