@@ -237,6 +237,60 @@ def bench_image_session(steps: int):
                 ms_per_frame=round(ms, 4), frames_per_s=round(1e3 / ms, 1), image_mb=round(width * height * 3 / 1e6, 2))
 
 
+def bench_unit_runner(steps: int):
+    """16 OCR-line units of 8 widths (a text line [1, 3, 32, w] -> conv 3x3 s2 + GELU -> 1x1 conv), fp16:
+    one HipUnitRunner run (one wave over 4 streams: upload, dispatches, download per unit, then one
+    wait) against the same units as 16 sessions run one after another. Host-timed per batch."""
+    import numpy as np
+    from simdonnx_amd import synth
+    from simdonnx_amd.backend import HipBackend, HipInferenceSession, HipUnitRunner
+    from simdonnx_amd.plan import NHWC, PlanBuilder
+    hip = HipBackend.default()
+    widths = [64, 96, 128, 160, 192, 256, 320, 480] * 2
+    graphs, xs = [], []
+    for i, w in enumerate(widths):
+        pb = PlanBuilder()
+        x = pb.input((1, 3, 32, w), NHWC, "line")
+        y = pb.conv(x, synth.he_normal(81, 1, (32, 3, 3, 3)), synth.uniform(81, 2, (32,), -0.1, 0.1), stride=2, pad=1,
+                    act="gelu", name="c1")
+        y = pb.conv(y, synth.he_normal(81, 3, (16, 32, 1, 1)), None, name="c2")
+        graphs.append(hip.graph(pb.build(y), True))
+        xs.append(synth.normal(82, i, (1, 32, w, 3), 1.0))
+    r = HipUnitRunner(hip, streams=4)
+    for g in graphs:
+        r.add(g)
+    for k, x in enumerate(xs):
+        r.input(k)[:] = x.reshape(-1)
+
+    def run_runner():
+        r.submit()
+        r.wait()
+
+    sessions = [HipInferenceSession(g) for g in graphs]
+    for s, x in zip(sessions, xs):
+        s.set_input(x)
+
+    def run_sessions():
+        for s in sessions:
+            s.run()
+
+    out = {}
+    for name, fn in (("runner_4_streams", run_runner), ("sequential_sessions", run_sessions)):
+        for _ in range(5):
+            fn()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        out[f"ms_{name}"] = round((time.perf_counter() - t0) * 1e3 / steps, 4)
+    for s in sessions:
+        s.close()
+    r.close()
+    for g in graphs:
+        g.release()
+    return dict(workload="16 OCR-line units (8 widths 64..480), conv3x3 s2 + GELU -> 1x1, fp16, host-timed per batch",
+                **out)
+
+
 def _ops_cases():
     """One-node plans of the rest of the ExecOp surface at the sizes the detector / recognizer shapes
     give them (fp16 storage): (label, plan, inputs, algorithmic bytes, flops). Bytes count each
@@ -376,7 +430,7 @@ def main():
     ap.add_argument("--no-replay", action="store_true",
                     help="launch network dispatches one by one instead of replaying a HIP graph (profiler runs)")
     ap.add_argument("--only", choices=["gemm", "conv", "detector", "recognizer", "mobilenetv3", "copy", "ops",
-                                       "recognizer_ctc", "image"],
+                                       "recognizer_ctc", "image", "runner"],
                     help="run one workload only (profiling runs); prints its own JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -388,7 +442,8 @@ def main():
               "copy": lambda: bench_copy(args.steps),
               "ops": lambda: {"ops": bench_ops(args.steps)},
               "recognizer_ctc": lambda: bench_recognizer_ctc(args.steps, not args.no_replay),
-              "image": lambda: bench_image_session(args.steps)}.get(args.only) or (lambda: bench_network(args.only, args.steps, not args.no_replay))
+              "image": lambda: bench_image_session(args.steps),
+              "runner": lambda: bench_unit_runner(args.steps)}.get(args.only) or (lambda: bench_network(args.only, args.steps, not args.no_replay))
         r = fn()
         print(json.dumps({"only": args.only, **{k: v for k, v in r.items() if k != "kernel_ms"}}), flush=True)
         return
@@ -433,6 +488,10 @@ def main():
         out["image_session"] = bench_image_session(100)
     except Exception as e:
         out["image_session"] = {"error": repr(e)}
+    try:
+        out["unit_runner"] = bench_unit_runner(100)
+    except Exception as e:
+        out["unit_runner"] = {"error": repr(e)}
     try:
         out["ops"] = bench_ops(200)
     except Exception as e:

@@ -239,6 +239,34 @@ int sox_image_session_tensor_size(sox_image_session* session, int32_t width, int
 int sox_image_session_run(sox_image_session* session, sox_graph* graph, const uint8_t* src, int32_t width,
                           int32_t height, int32_t src_stride, uint8_t* dst, int32_t dst_stride, int32_t format);
 
+/* ---- unit runner (VkUnitRunner, Backends/Vulkan/VkUnitRunner.cs:5-337) ----
+ * Several graph units per call (e.g. OCR line batches of different widths), re-recorded every run
+ * instead of one session per shape. Each unit owns a region of one grow-only arena and of the fp32
+ * host staging; the units of a wave are spread round-robin over `streams` HIP streams, so small units
+ * run side by side instead of one after another, and each wave ends on one event per stream. Waves
+ * are submitted back to back; a finished wave can be consumed while later ones still run. Not
+ * thread-safe. */
+typedef struct sox_unit_runner sox_unit_runner;
+int sox_unit_runner_create(sox_backend* backend, int32_t streams, sox_unit_runner** runner);
+void sox_unit_runner_destroy(sox_unit_runner* runner);
+/* Clear (:42-49): drops the previous run's units (it must have been waited for). */
+int sox_unit_runner_clear(sox_unit_runner* runner);
+/* Add (:51-60): a unit over `graph` (the runner takes its own reference); its index. */
+int sox_unit_runner_add(sox_unit_runner* runner, sox_graph* graph, int32_t* unit);
+/* Cut (:70-75): ends the current wave (the units added so far that are not in a wave yet). */
+int sox_unit_runner_cut(sox_unit_runner* runner);
+int sox_unit_runner_waves(sox_unit_runner* runner);
+int sox_unit_runner_wave_end(sox_unit_runner* runner, int32_t wave);
+/* Input (:87-93): the unit's input window, pinned fp32 host memory in the plan's physical layout (the
+ * first call after the last Add lays out the buffers). Output (:95-100): valid once its wave was
+ * waited for, until the next Submit. */
+int sox_unit_runner_input(sox_unit_runner* runner, int32_t unit, float** host, int64_t* count);
+int sox_unit_runner_output(sox_unit_runner* runner, int32_t unit, float** host, int64_t* count);
+/* Submit (:146-167): every wave (inputs must be written); Wait (:169-178): wave `wave` and every
+ * earlier one. */
+int sox_unit_runner_submit(sox_unit_runner* runner);
+int sox_unit_runner_wait(sox_unit_runner* runner, int32_t wave);
+
 #ifdef __cplusplus
 }
 #endif

@@ -354,3 +354,62 @@ class HipImageSession:
         except Exception:
             pass
 
+
+class HipUnitRunner:
+    """VkUnitRunner (Backends/Vulkan/VkUnitRunner.cs:5-337) on HIP: several graph units per call in
+    waves, over one grow-only arena and pinned staging, the units of a wave spread over `streams` HIP
+    streams so small units run side by side (sox_unit_runner_*). Not thread-safe."""
+
+    def __init__(self, backend: HipBackend, streams: int = 4):
+        h = N.c_void_p()
+        N.check(N.backend().sox_unit_runner_create(backend.h, streams, ctypes.byref(h)), "UnitRunner")
+        self.h = h
+        self._graphs = []
+
+    def clear(self):
+        N.check(N.backend().sox_unit_runner_clear(self.h), "UnitRunner.Clear")
+        self._graphs = []
+
+    def add(self, graph: "HipGraphModel") -> int:
+        u = N.c_int32()
+        N.check(N.backend().sox_unit_runner_add(self.h, graph.h, ctypes.byref(u)), "UnitRunner.Add")
+        self._graphs.append(graph)
+        return u.value
+
+    def cut(self):
+        N.check(N.backend().sox_unit_runner_cut(self.h), "UnitRunner.Cut")
+
+    @property
+    def waves(self) -> int:
+        return N.backend().sox_unit_runner_waves(self.h)
+
+    def _window(self, fn, unit: int) -> np.ndarray:
+        p = ctypes.POINTER(N.c_float)()
+        n = N.c_int64()
+        N.check(fn(self.h, unit, ctypes.byref(p), ctypes.byref(n)), "UnitRunner window")
+        return np.ctypeslib.as_array(p, shape=(n.value,))
+
+    def input(self, unit: int) -> np.ndarray:
+        return self._window(N.backend().sox_unit_runner_input, unit)
+
+    def output(self, unit: int) -> np.ndarray:
+        g = self._graphs[unit]
+        return self._window(N.backend().sox_unit_runner_output, unit).reshape(g.plan.values[g.plan.output].phys)
+
+    def submit(self):
+        N.check(N.backend().sox_unit_runner_submit(self.h), "UnitRunner.Submit")
+
+    def wait(self, wave: Optional[int] = None):
+        N.check(N.backend().sox_unit_runner_wait(self.h, self.waves - 1 if wave is None else wave), "UnitRunner.Wait")
+
+    def close(self):
+        if self.h:
+            N.backend().sox_unit_runner_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+

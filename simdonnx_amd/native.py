@@ -228,6 +228,19 @@ BACKEND_API = {
                                                 ctypes.POINTER(c_int32)]),
     "sox_image_session_run": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_int32,
                                         c_int32]),
+    "sox_unit_runner_create": (c_int32, [c_void_p, c_int32, ctypes.POINTER(c_void_p)]),
+    "sox_unit_runner_destroy": (None, [c_void_p]),
+    "sox_unit_runner_clear": (c_int32, [c_void_p]),
+    "sox_unit_runner_add": (c_int32, [c_void_p, c_void_p, ctypes.POINTER(c_int32)]),
+    "sox_unit_runner_cut": (c_int32, [c_void_p]),
+    "sox_unit_runner_waves": (c_int32, [c_void_p]),
+    "sox_unit_runner_wave_end": (c_int32, [c_void_p, c_int32]),
+    "sox_unit_runner_input": (c_int32, [c_void_p, c_int32, ctypes.POINTER(ctypes.POINTER(c_float)),
+                                        ctypes.POINTER(c_int64)]),
+    "sox_unit_runner_output": (c_int32, [c_void_p, c_int32, ctypes.POINTER(ctypes.POINTER(c_float)),
+                                         ctypes.POINTER(c_int64)]),
+    "sox_unit_runner_submit": (c_int32, [c_void_p]),
+    "sox_unit_runner_wait": (c_int32, [c_void_p, c_int32]),
     "sox_ctc_create": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, ctypes.POINTER(c_void_p)]),
     "sox_ctc_destroy": (None, [c_void_p]),
     "sox_ctc_is_fused": (c_int32, [c_void_p]),
