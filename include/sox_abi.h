@@ -405,6 +405,22 @@ typedef struct sox_nhwc2img_args {
     float scale;
 } sox_nhwc2img_args;
 
+/* Fused transformer MLP (mlp.hip): y = act2(GELU(rstd (x . W1 - mean c1) + b1) . W2 + b2 + res), the
+ * LayerNorm folded into W1 / b1 / c1 at graph creation. One 512-thread workgroup per 32 rows. */
+typedef struct sox_mlp_args {
+    const void* x;      /* fp16 [m][k1] */
+    const void* w1;     /* fp16 gamma-scaled [k1][h] in 32x32x16 fragment order (32 columns x 16 k per KiB) */
+    const float* b1;    /* [h]: b + beta W */
+    const float* c1;    /* [h]: column sums of w1 as rounded */
+    const void* w2;     /* fp16 [h][n2] in the same fragment order */
+    const float* b2;    /* [n2] (flags bit0) */
+    const void* res;    /* fp16 [m][n2] (flags bit1) */
+    void* y;            /* fp16 [m][n2] */
+    int32_t m, k1, h, n2, ldw1, ldw2;
+    float eps;
+    int32_t flags;      /* bit0 b2, bit1 residual, act2 << 4 */
+} sox_mlp_args;
+
 #ifdef __cplusplus
 }
 #endif

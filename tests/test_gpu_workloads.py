@@ -93,3 +93,40 @@ def test_detector_replay_is_bitwise_stable(hip):
         for _ in range(3):
             s.set_input(ins[0])
             assert np.array_equal(s.run(), direct)
+
+
+@pytest.mark.parametrize("rows,dim,hidden,residual", [(2560, 192, 768, True), (333, 128, 512, True), (70, 64, 256, False)])
+def test_fused_mlp_matches_unfused_and_oracle(hip, rows, dim, hidden, residual, monkeypatch):
+    """LayerNorm -> fc1 (+GELU) -> fc2 (+ residual Add) runs as one dispatch (mlp.hip) and agrees with
+    the two LDS-DMA Gemms it replaces (SIMDONNX_HIP_NO_MLP_FUSE) within the fp16 contract and with the
+    oracle on the unfused plan."""
+    import numpy as np
+    from oracle.interp import run_plan
+    from simdonnx_amd import synth
+    from simdonnx_amd.backend import HipInferenceSession
+    from simdonnx_amd.plan import PlanBuilder
+    from tests.conftest import max_rel
+    pb = PlanBuilder()
+    x = pb.input((rows, dim), None, "x")
+    hn = pb.layer_norm(x, 1.0 + synth.uniform(91, 1, (dim,), -0.1, 0.1), synth.uniform(91, 2, (dim,), -0.1, 0.1), 1e-6,
+                       name="ln")
+    f1 = pb.gemm(hn, synth.normal(91, 3, (dim, hidden), 0.05), synth.uniform(91, 4, (hidden,), -0.1, 0.1), act="gelu",
+                 name="fc1")
+    f2 = pb.gemm(f1, synth.normal(91, 5, (hidden, dim), 0.05), synth.uniform(91, 6, (dim,), -0.1, 0.1), name="fc2")
+    y = pb.add(x, f2, name="res") if residual else f2
+    plan = pb.build(y)
+    xin = synth.normal(91, 7, (rows, dim), 1.0)
+    g = hip.graph(plan, True)
+    assert [d[0] for d in g.dispatches] == ["mlp"]
+    with HipInferenceSession(g) as s:
+        s.set_input(xin)
+        fused = s.run().copy()
+    monkeypatch.setenv("SIMDONNX_HIP_NO_MLP_FUSE", "1")
+    g2 = hip.graph(plan, True)
+    assert [d[0] for d in g2.dispatches] == ["gemm_ln", "gemm"]
+    with HipInferenceSession(g2) as s:
+        s.set_input(xin)
+        unfused = s.run().copy()
+    assert max_rel(fused, unfused) < 2e-3
+    want = run_plan(plan, [xin], f16_storage=True)
+    assert max_rel(fused, want) < 2e-2
