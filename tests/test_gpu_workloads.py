@@ -130,3 +130,32 @@ def test_fused_mlp_matches_unfused_and_oracle(hip, rows, dim, hidden, residual, 
     assert max_rel(fused, unfused) < 2e-3
     want = run_plan(plan, [xin], f16_storage=True)
     assert max_rel(fused, want) < 2e-2
+
+
+def test_fused_mlp_not_taken_when_hidden_is_read_twice(hip):
+    """The hidden activation also read by another node (here an Add of it with itself, then concat into
+    the output path) keeps the two Gemms apart: the fusion needs fc2 to be the hidden's only reader."""
+    from simdonnx_amd import synth
+    from simdonnx_amd.backend import HipInferenceSession
+    from simdonnx_amd.plan import PlanBuilder
+    from oracle.interp import run_plan
+    from tests.conftest import max_rel
+    rows, dim, hidden = 256, 192, 768
+    pb = PlanBuilder()
+    x = pb.input((rows, dim), None, "x")
+    hn = pb.layer_norm(x, 1.0 + synth.uniform(92, 1, (dim,), -0.1, 0.1), synth.uniform(92, 2, (dim,), -0.1, 0.1), 1e-6,
+                       name="ln")
+    f1 = pb.gemm(hn, synth.normal(92, 3, (dim, hidden), 0.05), synth.uniform(92, 4, (hidden,), -0.1, 0.1), act="gelu",
+                 name="fc1")
+    f2 = pb.gemm(f1, synth.normal(92, 5, (hidden, dim), 0.05), None, name="fc2")
+    f3 = pb.gemm(f1, synth.normal(92, 6, (hidden, dim), 0.05), None, name="fc3")  # a second reader of the hidden
+    y = pb.add(f2, f3, name="sum")
+    plan = pb.build(y)
+    g = hip.graph(plan, True)
+    names = [d[0] for d in g.dispatches]
+    assert "mlp" not in names, names
+    xin = synth.normal(92, 7, (rows, dim), 1.0)
+    with HipInferenceSession(g) as s:
+        s.set_input(xin)
+        got = s.run().copy()
+    assert max_rel(got, run_plan(plan, [xin], f16_storage=True)) < 2e-2
