@@ -175,8 +175,11 @@ SOX_DEV void store_tile_lds(half_t* __restrict__ Y, int ldy, int M, int N, int m
         constexpr int JG = j0 + 1 < TJ ? 2 : 1, CH = JG * 4;  // blocks staged together, 16-byte chunks per row
         static_for<0, CH>([&](auto cc) {
             constexpr int c = decltype(cc)::value, j = j0 + c / 4, q = c % 4;
-            half4 h;
-            static_for<0, 4>([&](auto ee) { h[decltype(ee)::value] = (half_t)fin(acc[j][i][4 * q + decltype(ee)::value]); });
+            float4v f;
+            static_for<0, 4>([&](auto ee) { f[decltype(ee)::value] = fin(acc[j][i][4 * q + decltype(ee)::value]); });
+            // a vector conversion: two v_cvt_pk_f16_f32 (round to nearest even) instead of four
+            // conversions and the packing moves
+            const half4 h = __builtin_convertvector(f, half4);
             *(half4*)(stg + l32 * CH * 16 + ((c ^ (l32 % CH)) << 4) + hl * 8) = h;
         });
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // other lanes' rows are read back
