@@ -386,7 +386,8 @@ typedef struct sox_uphead_args {
 
 /* Image session input (img2nhwc.comp): interleaved u8 pixels (bpp 3 or 4, rows `stride` bytes apart)
  * -> NHWC [oh][ow][3], tensor channel c = lut[c * 256 + byte], the image at (pt, pl) with its edge
- * repeated around it; swap = 1: tensor channel 0 is byte 2 of a pixel. Grid (ceil(ow / 256), oh). */
+ * repeated around it; swap = 1: tensor channel 0 is byte 2 of a pixel. Two flat tensor pixels per
+ * thread, grid ceil(oh * ow / 512). */
 typedef struct sox_img2nhwc_args {
     const uint8_t* src;
     void* y;

@@ -558,15 +558,32 @@ extern "C" __global__ void __launch_bounds__(256) sox_uphead_f32_v(sox_uphead_ar
 // ------------------------------------------------------------------------------------------
 template <typename T>
 __device__ __forceinline__ void img2nhwc_body(const sox_img2nhwc_args& p) {
-    const int ox = blockIdx.x * blockDim.x + threadIdx.x, oy = blockIdx.y;
-    if (ox >= p.ow) return;
-    const int sy = min(max(oy - p.pt, 0), p.ih - 1), sx = min(max(ox - p.pl, 0), p.iw - 1);
-    const uint8_t* px = p.src + (long)sy * p.stride + (long)sx * p.bpp;
+    // flat tensor pixels 2t and 2t + 1 per thread: their 6 values leave as 3 aligned 2-element words
+    // (element offset 6t) instead of 6 separate stores; an odd last pixel alone
+    const long total = (long)p.oh * p.ow;
+    const long p0 = 2 * ((long)blockIdx.x * blockDim.x + threadIdx.x);
+    if (p0 >= total) return;
     const int ob = p.swap * 2;
-    T* o = (T*)p.y + ((long)oy * p.ow + ox) * 3;
-    o[0] = (T)p.lut[px[ob]];
-    o[1] = (T)p.lut[256 + px[1]];
-    o[2] = (T)p.lut[512 + px[2 - ob]];
+    T v[6];
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const long pi = min(p0 + k, total - 1);
+        const int oy = (int)(pi / p.ow), ox = (int)(pi - (long)oy * p.ow);
+        const int sy = min(max(oy - p.pt, 0), p.ih - 1), sx = min(max(ox - p.pl, 0), p.iw - 1);
+        const uint8_t* px = p.src + (long)sy * p.stride + (long)sx * p.bpp;
+        v[3 * k] = (T)p.lut[px[ob]];
+        v[3 * k + 1] = (T)p.lut[256 + px[1]];
+        v[3 * k + 2] = (T)p.lut[512 + px[2 - ob]];
+    }
+    T* o = (T*)p.y + p0 * 3;
+    if (p0 + 1 < total) {
+        typedef T T2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+        for (int k = 0; k < 3; k++) ((T2*)o)[k] = T2{v[2 * k], v[2 * k + 1]};
+    } else {
+#pragma unroll
+        for (int k = 0; k < 3; k++) o[k] = v[k];
+    }
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_img2nhwc_f16(sox_img2nhwc_args p) { img2nhwc_body<half_t>(p); }
