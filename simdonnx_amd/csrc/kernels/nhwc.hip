@@ -1240,6 +1240,72 @@ __device__ __forceinline__ void conv_direct_333_body(const sox_igemm_args& p) {
     *(Vec*)((T*)p.y + o) = out;
 }
 
+// Direct conv for few OUTPUT channels (oc < 8: a final 3x3 conv to an image or a probability map),
+// fp16 with ic % 8 == 0: a 32-channel matrix tile would leave most of its columns empty. One work
+// item = one output pixel x all OC channels (one instance per OC, so no FMA is spent on padding);
+// the weights are staged once per workgroup in LDS as fp32, k-major and padded to 8 channels
+// ([K][8], zeros past OC), so each input value meets its weights in one or two broadcast 16-byte
+// LDS reads; the input comes in 16-byte runs of 8 channels.
+template <int OC>
+__device__ __forceinline__ void conv_narrow_body(const sox_igemm_args& p) {
+    extern __shared__ float wl[];  // [K][8]
+    const int K = p.k;
+    for (int i = threadIdx.x; i < K * 8; i += blockDim.x) {
+        const int kk = i >> 3, o = i & 7;
+        wl[i] = o < OC ? (float)((const half_t*)p.w)[(long)o * p.kpad + kk] : 0.0f;
+    }
+    __syncthreads();
+    const long m = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (m >= p.m) return;
+    const int ohw = p.oh * p.ow;
+    const int b = (int)(m / ohw), r = (int)(m - (long)b * ohw);
+    const int oy = r / p.ow, ox = r - oy * p.ow;
+    const bool reflect = (p.flags & SOX_F_REFLECT) != 0;
+    const half_t* __restrict__ x = (const half_t*)p.x + (long)b * p.ih * p.iw * p.ic;
+    float acc[OC];
+#pragma unroll
+    for (int e = 0; e < OC; e++) acc[e] = (p.flags & SOX_F_BIAS) ? p.bias[e] : 0.0f;
+    const half_t pv = (half_t)p.pad_value;
+    const half8 pad8v = {pv, pv, pv, pv, pv, pv, pv, pv};
+    for (int ky = 0; ky < p.kh; ky++) {
+        const int iy = sox_src_index(oy * p.sh + ky - p.pt, p.ih, reflect);
+        for (int kx = 0; kx < p.kw; kx++) {
+            const int ix = sox_src_index(ox * p.sw + kx - p.pl, p.iw, reflect);
+            const bool in = iy >= 0 && ix >= 0;
+            const half_t* xr = x + ((long)(in ? iy : 0) * p.iw + (in ? ix : 0)) * p.ic;
+            const float* wk = wl + (ky * p.kw + kx) * p.ic * 8;
+            for (int c = 0; c < p.ic; c += 8) {
+                const half8 xv = in ? *(const half8*)(xr + c) : pad8v;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float xf = (float)xv[j];
+                    const float4v w0 = *(const float4v*)(wk + (c + j) * 8);
+#pragma unroll
+                    for (int e = 0; e < (OC < 4 ? OC : 4); e++) acc[e] = __builtin_fmaf(xf, w0[e], acc[e]);
+                    if constexpr (OC > 4) {
+                        const float4v w1 = *(const float4v*)(wk + (c + j) * 8 + 4);
+#pragma unroll
+                        for (int e = 4; e < OC; e++) acc[e] = __builtin_fmaf(xf, w1[e - 4], acc[e]);
+                    }
+                }
+            }
+        }
+    }
+    const int act = (p.flags & SOX_F_ACT_MASK) >> SOX_F_ACT_SHIFT;
+    const long o = m * p.ldy;
+#pragma unroll
+    for (int e = 0; e < OC; e++) {
+        float v = acc[e];
+        if (p.flags & SOX_F_RESIDUAL) v += (float)((const half_t*)p.add)[o + e];
+        ((half_t*)p.y)[o + e] = (half_t)act_fast(v, act);
+    }
+}
+
+#define SOX_CONV_NARROW(OC) \
+    extern "C" __global__ void __launch_bounds__(256) sox_conv_narrow_f16_o##OC(sox_igemm_args p) { conv_narrow_body<OC>(p); }
+SOX_CONV_NARROW(1) SOX_CONV_NARROW(2) SOX_CONV_NARROW(3) SOX_CONV_NARROW(4)
+SOX_CONV_NARROW(5) SOX_CONV_NARROW(6) SOX_CONV_NARROW(7)
+
 extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_333_f16(sox_igemm_args p) { conv_direct_333_body<half_t, 8>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_333_f32(sox_igemm_args p) { conv_direct_333_body<float, 4>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_f16(sox_igemm_args p) { conv_direct_body<half_t, 8>(p); }

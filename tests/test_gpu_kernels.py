@@ -56,13 +56,14 @@ def conv_plan(x, w, b, add, stride, pads, act, pad_mode, pad_value, group=1):
                          ids=["f32", "f16", "f16-ring", "f16-igemm"])
 @pytest.mark.parametrize("i", range(int(G["conv_n"][0])))
 def test_conv_matches_oracle(hip, i, half, path, monkeypatch):
-    """Every golden conv case; fp16 through the default route (the LDS halo kernel for 3x3 convs with
-    few output channels, else the LDS-DMA implicit-GEMM ring when ic % 8 == 0), through the ring
+    """Every golden conv case; fp16 through the default route (the direct kernel below 8 output
+    channels, the LDS halo kernel for other 3x3 convs with few output channels, else the LDS-DMA implicit-GEMM ring when ic % 8 == 0), through the ring
     alone and through the register-staged implicit-GEMM kernel."""
     if path == "igemm":
         monkeypatch.setenv("SIMDONNX_HIP_IGEMM", "1")
     if path == "ring":
         monkeypatch.setenv("SIMDONNX_HIP_NOHALO", "1")
+        monkeypatch.setenv("SIMDONNX_HIP_NONARROW", "1")
     ic, oc, k, s, h, w, mode, act, res = [int(v) for v in G[f"conv{i}_meta"]]
     pv = float(G[f"conv{i}_pv"][0])
     cv = f16 if half else (lambda a: a)
@@ -470,3 +471,29 @@ def test_gemm_residual_add_fused(hip, m, k, n, act, half):
     g1 = O.gemm(a, w, b)
     want = O.ew2(O.round_f16(g1) if half else g1, r, op=0, act=1 if act == "relu" else 0)
     assert max_rel(got, want) < (2e-2 if half else 1e-4)
+
+
+# (batch, ic, oc, k, stride, h, w, act, residual, pad_mode, pad_value): fp16 convs with fewer than 8
+# output channels take the one-pixel-per-item direct kernel; K = 9 * 128 is its largest reduction
+NARROW_CASES = [(1, 8, 3, 3, 1, 37, 61, "none", False, 0, 0.0), (2, 16, 1, 3, 1, 20, 18, "sigmoid", True, 0, 0.0),
+                (1, 24, 5, 3, 2, 33, 29, "relu", False, 0, 0.0), (1, 8, 7, 5, 1, 15, 22, "hardswish", True, 1, 0.0),
+                (1, 128, 2, 3, 1, 9, 10, "gelu", False, 0, 0.0), (1, 8, 4, 3, 1, 11, 13, "none", False, 0, -0.5)]
+
+
+@pytest.mark.parametrize("case", NARROW_CASES, ids=lambda c: "x".join(str(v) for v in c))
+def test_conv_narrow_route(hip, case):
+    n, ic, oc, k, s, h, w, act, res, mode, pv = case
+    x = f16(synth.uniform(19, 1, (n, h, w, ic), -1, 1))
+    wt = f16(synth.normal(19, 2, (oc, ic, k, k), 0.15))
+    b = synth.uniform(19, 3, (oc,), -0.2, 0.2)
+    p = k // 2
+    pads = (p, p, p, p)
+    oh, ow = (h + 2 * p - k) // s + 1, (w + 2 * p - k) // s + 1
+    add = f16(synth.uniform(19, 4, (n, oh, ow, oc), -1, 1)) if res else None
+    plan, ins = conv_plan(x, wt, b, add, (s, s), pads, act, mode, pv)
+    g = hip.graph(plan, True)
+    assert [d[0] for d in g.dispatches] == ["conv_narrow"]
+    got = run(hip, plan, ins, True)
+    want = O.conv(x, wt, b, add, stride=(s, s), pads=pads, act=act, pad_mode=mode, pad_value=pv)
+    assert got.shape == want.shape
+    assert max_rel(got, want) < TOL[True]
