@@ -100,9 +100,12 @@ def bench_conv(steps: int):
 
 
 NETWORKS = {
-    "mobilenetv3": ("mobilenetv3_small", "MobileNetV3-small block stack, 1x3x640x640", 1),
-    "detector": ("dbnet", "DBNet-style detector (MobileNetV3-small + FPN + ConvT head), 1x3x960x960", 1),
-    "recognizer": ("svtr", "SVTR-style recognizer, 32x3x48x320", 32),
+    "mobilenetv3": ("mobilenetv3_small", "MobileNetV3-small block stack, 1x3x640x640, fp16 storage", 1, True),
+    "detector": ("dbnet", "DBNet-style detector (MobileNetV3-small + FPN + ConvT head), 1x3x960x960, fp16 storage",
+                 1, True),
+    "detector_fp32": ("dbnet", "DBNet-style detector (MobileNetV3-small + FPN + ConvT head), 1x3x960x960, fp32 "
+                      "storage", 1, False),
+    "recognizer": ("svtr", "SVTR-style recognizer, 32x3x48x320, fp16 storage", 32, True),
 }
 
 
@@ -112,10 +115,10 @@ def bench_network(key: str, steps: int, replay: bool = True):
     per-dispatch event profile."""
     from simdonnx_amd import graphs
     from simdonnx_amd.backend import HipBackend, HipInferenceSession
-    fn, desc, images = NETWORKS[key]
+    fn, desc, images, half = NETWORKS[key]
     hip = HipBackend.default()
     plan, ins = getattr(graphs, fn)()
-    g = hip.graph(plan, True)
+    g = hip.graph(plan, half)
     with HipInferenceSession(g) as s:
         s.set_input(ins[0])
         s.set_replay(replay)
@@ -131,8 +134,9 @@ def bench_network(key: str, steps: int, replay: bool = True):
         per_node.setdefault(node, [name, 0.0])[1] += t
     classes = {}
     tot_fl = tot_by = 0
+    peak = PEAK_FP16_TFLOPS if half else PEAK_FP32_TFLOPS
     for node, (name, t) in per_node.items():
-        fl, by = graphs.node_cost(plan, plan.nodes[node])
+        fl, by = graphs.node_cost(plan, plan.nodes[node], 2 if half else 4)
         tot_fl += fl
         tot_by += by
         c = classes.setdefault(name, dict(ms=0.0, n=0, flops=0, bytes=0))
@@ -144,8 +148,8 @@ def bench_network(key: str, steps: int, replay: bool = True):
     for name, c in sorted(classes.items(), key=lambda kv: -kv[1]["ms"]):
         gbs = c["bytes"] / (c["ms"] * 1e-3) / 1e9
         tfl = c["flops"] / (c["ms"] * 1e-3) / 1e12
-        bound = "mfma" if name in ("conv", "gemm", "gemm_ln") and c["flops"] / max(c["bytes"], 1) > 313 else "hbm"
-        frac = tfl / PEAK_FP16_TFLOPS if bound == "mfma" else gbs / PEAK_HBM_GBS
+        bound = "mfma" if name in ("conv", "gemm", "gemm_ln") and c["flops"] / max(c["bytes"], 1) > peak / 8 else "hbm"
+        frac = tfl / peak if bound == "mfma" else gbs / PEAK_HBM_GBS
         out.append(dict(kernel=name, nodes=c["n"], ms=round(c["ms"], 4), gb_s=round(gbs, 1), tflop_s=round(tfl, 2),
                         bound=bound, frac=round(frac, 4)))
     return dict(workload=desc, ms_per_image=round(ms / images, 4), images_per_s=round(images / (ms * 1e-3), 1),
@@ -429,7 +433,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-replay", action="store_true",
                     help="launch network dispatches one by one instead of replaying a HIP graph (profiler runs)")
-    ap.add_argument("--only", choices=["gemm", "conv", "detector", "recognizer", "mobilenetv3", "copy", "ops",
+    ap.add_argument("--only", choices=["gemm", "conv", "detector", "detector_fp32", "recognizer", "mobilenetv3", "copy", "ops",
                                        "recognizer_ctc", "image", "runner"],
                     help="run one workload only (profiling runs); prints its own JSON line")
     args = ap.parse_args()
@@ -470,7 +474,7 @@ def main():
                      "frac": round(tflops / PEAK_FP16_TFLOPS, 4),
                      "traffic": traffic_from_profiles("matmul_bias_gelu")},
     }
-    for key in ("detector", "recognizer", "mobilenetv3"):
+    for key in ("detector", "detector_fp32", "recognizer", "mobilenetv3"):
         try:
             out[key] = bench_network(key, 200, not args.no_replay)
             log(f"{key}: {out[key]['ms_per_image']} ms/image")

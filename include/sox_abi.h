@@ -33,6 +33,10 @@ enum sox_act { SOX_ACT_NONE = 0, SOX_ACT_RELU = 1, SOX_ACT_SIGMOID = 2, SOX_ACT_
 #define SOX_F_DENSE_A 0x100 /* A is a plain row-major [M][lda] matrix (Gemm), not an NHWC image */
 #define SOX_F_PAD_ROWS 0x400 /* LDS-DMA Gemm: output rows are padded to ldy >= N rounded up to 4, so the N tail
                                  is stored as whole 4-element groups (the pad columns take junk) */
+#define SOX_F_POOL 0x800      /* direct conv kernels: 2x2/2 max pool of the (activated) conv output fused in
+                                 (ConvP.Pool, Kernels/Nhwc.cs:661-727); m counts pooled pixels, oh / ow
+                                 stay the conv output's size */
+#define SOX_F_POOL_RELU 0x1000 /* with SOX_F_POOL: relu after the max (PoolP.FuseRelu) */
 #define SOX_F_CONVT 0x200   /* LDS-DMA conv kernels: column n = tap * ct_oc + o of input pixel m is
                                ConvTranspose output (y * ct_kh + dy, x * ct_kw + dx, o), tap = dy * ct_kw + dx */
 

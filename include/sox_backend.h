@@ -97,7 +97,7 @@ typedef struct sox_tanh_p { float in_scale, out_scale; } sox_tanh_p;         /* 
 typedef struct sox_clip_p { float min, max; } sox_clip_p;                    /* ClipP :134-138 */
 typedef struct sox_depth_to_space_p { int32_t block, crd; } sox_depth_to_space_p; /* DepthToSpaceP :139-145 */
 
-/* Records of the built-in extension ops (ExecOp.Ext with these names; Engine/Fusions/*.cs). */
+/* Records of the built-in extension ops (ExecOp.Ext with these names; Engine/Fusions/SafeDivOp.cs, ChannelShiftOp.cs, UpHeadOp.cs). */
 typedef struct sox_safediv_p { float eps, lo, hi; } sox_safediv_p;      /* SafeDivP, SafeDivOp.cs:9-13 */
 typedef struct sox_shift_p {                                               /* ShiftP, ChannelShiftOp.cs:9-14 */
     int32_t axis;                    /* logical spatial axis: 2 = H, 3 = W */
@@ -154,6 +154,10 @@ int sox_graph_dispatch(sox_graph* graph, int32_t node, void* module, const char*
                        int32_t nbinds, const void* params, size_t params_bytes, const uint32_t grid[3],
                        const uint32_t block[3], uint32_t lds_bytes);
 int sox_graph_node_info(sox_graph* graph, int32_t node, int32_t* op, const void** params, size_t* params_bytes);
+/* ExecNode.In / ExecNode.Out (ExecPlan.cs:235-276) of a node: up to in_cap / out_cap value ids are
+ * written, *nin / *nout receive the full counts. */
+int sox_graph_node_values(sox_graph* graph, int32_t node, int32_t* in, int32_t in_cap, int32_t* nin, int32_t* out,
+                          int32_t out_cap, int32_t* nout);
 int sox_graph_value_shape(sox_graph* graph, int32_t value, int32_t* phys_shape, int32_t cap, int32_t* rank);
 int sox_graph_is_f16(sox_graph* graph);
 
@@ -211,9 +215,11 @@ int sox_ctc_is_fused(sox_ctc* ctc);
 /* ArgMax (CtcProjection.cs:44-58) over the activation `feature_value` of a session of an fp16 graph
  * ([batch * rows, inner], after sox_session_run / _wait): indices[r] = the largest logit's column
  * (ties keep the first), probabilities[r] = its softmax probability in (0, 1]. Runs on the
- * session's stream and returns when the host arrays are written. SOX_E_UNSUPPORTED when the head
- * is not fused (nothing written, the reference's false), SOX_E_INVALID for a non-finite logit
- * ("Recognizer output is invalid."). */
+ * session's stream and returns when the host arrays are written. SOX_E_UNSUPPORTED only when the
+ * head is not fused (nothing written, the reference's false); SOX_E_INVALID for a non-finite logit
+ * ("Recognizer output is invalid."), an fp32 session, a feature value that is not a dense
+ * [batch * rows, inner] activation still intact after the run (a later node's output overlapping
+ * it in the arena), or too many rows. */
 int sox_ctc_argmax(sox_ctc* ctc, sox_session* session, int32_t feature_value, int32_t batch, int32_t rows,
                    int32_t* indices, float* probabilities);
 

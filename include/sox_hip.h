@@ -8,7 +8,9 @@
  *   - handles are opaque pointers; sizes are size_t; no C++ or torch types appear.
  *   - a device-lost class error (launch failure, illegal address, ECC) latches a process-wide
  *     "lost" flag (the analogue of VkDevice.Lost, VkDevice.cs:18, 885-899); sox_device_lost()
- *     reports it, sox_device_reset_lost() clears it after the host has re-created its objects.
+ *     reports it, sox_device_reset_lost() clears it after the host has re-created its objects,
+ *     and sox_device_mark_lost() sets it from the host (the settable VkDevice.Lost that
+ *     tests/Sdcb.SimdOnnx.Tests/VkDeviceLossTests.cs:33 uses to exercise recovery without a fault).
  */
 #ifndef SOX_HIP_H
 #define SOX_HIP_H
@@ -44,6 +46,7 @@ int sox_init(int device, sox_device_info* info);
 const char* sox_error_string(int status);
 int sox_device_lost(void);
 void sox_device_reset_lost(void);
+void sox_device_mark_lost(void); /* VkDevice.Lost = true (VkDevice.cs:18): every later launch returns SOX_E_LOST */
 int sox_device_sync(void); /* vkDeviceWaitIdle, Vk.cs:474 */
 
 /* Memory (vkCreateBuffer/AllocateMemory/MapMemory, Vk.cs:401-413): device slabs and pinned staging. */
@@ -79,7 +82,10 @@ int sox_event_sync(void* ev);
 int sox_event_elapsed_ms(float* ms, void* start, void* stop);
 
 /* Replay: capture a stream's work into a graph and relaunch it (the analogue of the
- * pre-recorded command buffer, VkSession.cs:139-140). */
+ * pre-recorded command buffer, VkSession.cs:139-140). A sox_launch into a stream between
+ * sox_graph_begin and sox_graph_end copies its kernarg block (and the launch's `extra` array) into
+ * storage the graph owns until sox_graph_destroy, so the caller's kernarg memory may be reused at
+ * once. Only streams created by sox_stream_create can be captured. */
 int sox_graph_begin(void* stream);
 int sox_graph_end(void* stream, void** graph_exec);
 int sox_graph_launch(void* graph_exec, void* stream);

@@ -304,6 +304,21 @@ def pad_nhwc(x, pad_t, pad_l, pad_b, pad_r, mode=0, value=0.0):
     return out
 
 
+def max_pool(x, kernel, stride, pads, relu=False):
+    """Nhwc.MaxPool (Kernels/Nhwc.cs:729-769), NHWC batch, pads (t, l, b, r), PoolP.FuseRelu."""
+    x = _f32(x)
+    n, ih, iw, c = x.shape
+    oh = conv_out_size(ih, kernel[0], stride[0], pads[0], pads[2])
+    ow = conv_out_size(iw, kernel[1], stride[1], pads[1], pads[3])
+    out = np.empty((n, oh, ow, c), np.float32)
+    for i in range(n):
+        oi = np.empty((oh, ow, c), np.float32)
+        _check(lib().ora_max_pool_nhwc(_p(np.ascontiguousarray(x[i])), ih, iw, c, _p(oi), oh, ow, kernel[0],
+                                       kernel[1], stride[0], stride[1], pads[0], pads[1], int(relu)), "max_pool")
+        out[i] = oi
+    return out
+
+
 def avg_pool(x, kernel, stride, pads, count_include_pad=False):
     """Nhwc.AvgPool (Kernels/Ops.Seq.cs:180-215), NHWC batch, pads (t, l, b, r)."""
     x = _f32(x)

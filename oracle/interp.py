@@ -157,6 +157,8 @@ def run_plan(plan, inputs, keep=False, f16_storage=False):
             y = O.unary2(get(node.ins[0]), node.op, *((p.a, p.b) if p is not None else (0.0, 0.0)))
         elif node.op in ("DepthToSpace", "SpaceToDepth"):
             y = O.depth_to_space(get(node.ins[0]), p.block, p.crd, node.op == "SpaceToDepth")
+        elif node.op == "MaxPool":
+            y = O.max_pool(get(node.ins[0]), p.kernel, p.strides, p.pads, p.relu)
         elif node.op == "AvgPool":
             y = O.avg_pool(get(node.ins[0]), p.kernel, p.strides, p.pads, p.count_include_pad)
         elif node.op == "GlobalAvgPool":

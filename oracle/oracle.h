@@ -122,6 +122,10 @@ int ora_resize_bilinear(const float* src, int ih, int iw, int c, float* dst, int
 int ora_pad_nhwc(const float* src, int ih, int iw, int c, float* dst, int oh, int ow, int pad_t, int pad_l,
                  int mode, float value);
 /* Nhwc.AvgPool (Kernels/Ops.Seq.cs:180-215), one image. */
+/* Nhwc.MaxPool (Kernels/Nhwc.cs:729-769), one image: taps outside the image skipped, an empty window
+ * is 0, relu (PoolP.FuseRelu) last. */
+int ora_max_pool_nhwc(const float* src, int ih, int iw, int c, float* dst, int oh, int ow, int kh, int kw, int sh,
+                      int sw, int pad_t, int pad_l, int relu);
 int ora_avg_pool_nhwc(const float* src, int ih, int iw, int c, float* dst, int oh, int ow, int kh, int kw, int sh,
                       int sw, int pad_t, int pad_l, int count_include_pad);
 /* Nhwc.DepthToSpace (dir 0) / SpaceToDepth (dir 1), NHWC, one image (Kernels/Nhwc.Det.cs:210-282). */

@@ -944,6 +944,40 @@ int ora_pad_nhwc(const float* src, int ih, int iw, int c, float* dst, int oh, in
     return 0;
 }
 
+// Nhwc.MaxPool (Kernels/Nhwc.cs:729-769): out-of-image taps are skipped (constant pad map), the
+// first in-image tap is copied and the rest folded in with max in (ky, kx) order; a window with no
+// in-image tap is 0; the fused relu (PoolP.FuseRelu) is applied last.
+int ora_max_pool_nhwc(const float* src, int ih, int iw, int c, float* dst, int oh, int ow, int kh, int kw, int sh,
+                      int sw, int pad_t, int pad_l, int relu) {
+    std::vector<int> rm = make_map(oh, kh, sh, pad_t, ih, 0), cm = make_map(ow, kw, sw, pad_l, iw, 0);
+#pragma omp parallel for schedule(static) num_threads(threads())
+    for (int y = 0; y < oh; y++)
+        for (int x = 0; x < ow; x++) {
+            float* o = dst + ((long)y * ow + x) * c;
+            bool any = false;
+            for (int ky = 0; ky < kh; ky++) {
+                int r = rm[(long)y * kh + ky];
+                if (r < 0) continue;
+                for (int kx = 0; kx < kw; kx++) {
+                    int cc = cm[(long)x * kw + kx];
+                    if (cc < 0) continue;
+                    const float* s = src + ((long)r * iw + cc) * c;
+                    if (!any) {
+                        memcpy(o, s, sizeof(float) * c);
+                        any = true;
+                        continue;
+                    }
+                    for (int ch = 0; ch < c; ch++) o[ch] = fmaxf(o[ch], s[ch]);
+                }
+            }
+            if (!any)
+                for (int ch = 0; ch < c; ch++) o[ch] = 0.0f;
+            else if (relu)
+                for (int ch = 0; ch < c; ch++) o[ch] = fmaxf(o[ch], 0.0f);
+        }
+    return 0;
+}
+
 // Nhwc.AvgPool (Kernels/Ops.Seq.cs:180-215): taps summed in (ky, kx) order, then one multiply by
 // 1 / count (kh*kw with count_include_pad, else the in-bounds taps).
 int ora_avg_pool_nhwc(const float* src, int ih, int iw, int c, float* dst, int oh, int ow, int kh, int kw, int sh,

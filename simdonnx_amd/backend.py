@@ -67,6 +67,13 @@ class HipBackend:
     def is_lost(self) -> bool:
         return bool(N.backend().sox_backend_is_lost(self.h))
 
+    @staticmethod
+    def mark_lost():
+        """Sets the process-wide lost flag from the host (VkDevice.Lost = true, the hook
+        VkDeviceLossTests.cs:33 uses): every later submit returns DeviceLostError and ``default()``
+        builds a new backend."""
+        N.thin().sox_device_mark_lost()
+
     def graph(self, plan: ExecPlan, f16: bool = True) -> "HipGraphModel":
         return HipGraphModel(self, plan, f16)
 
@@ -87,7 +94,14 @@ class HipBackend:
 
     def register_ext(self, name: str, emit, consts=None):
         """Registers an extension op's HIP emitter (the ExtOp.EmitHip hook)."""
-        emit_fn = N.EXT_EMIT_FN(lambda user, g, node: emit(HipGraphView(g), node))
+        def _emit(user, g, node):
+            try:
+                rc = emit(HipGraphView(g), node)
+                return N.SOX_OK if rc is None else int(rc)
+            except Exception as e:  # an exception must not cross the C ABI: the build fails with it
+                print(f"extension {name} emit failed: {e!r}", flush=True)
+                return N.SOX_E_INVALID
+        emit_fn = N.EXT_EMIT_FN(_emit)
         if consts is None:
             consts_fn = N.EXT_CONSTS_FN(lambda *a: 0)
         else:
@@ -117,6 +131,23 @@ class HipGraphView:
         N.check(N.backend().sox_graph_bind(self.h, value, N.CK[kind] if isinstance(kind, str) else kind,
                                            ctypes.byref(b)), "Bind")
         return b
+
+    def node_values(self, node: int):
+        """(input value ids, output value ids) of a plan node (sox_graph_node_values)."""
+        ins, outs = (N.c_int32 * 16)(), (N.c_int32 * 16)()
+        ni, no = N.c_int32(), N.c_int32()
+        N.check(N.backend().sox_graph_node_values(self.h, node, ins, 16, ctypes.byref(ni), outs, 16, ctypes.byref(no)),
+                "node_values")
+        return list(ins[: ni.value]), list(outs[: no.value])
+
+    def node(self, node: int):
+        """(ExecOp, params bytes) of a plan node (sox_graph_node_info)."""
+        op = N.c_int32()
+        pp = N.c_void_p()
+        nb = N.c_size_t()
+        N.check(N.backend().sox_graph_node_info(self.h, node, ctypes.byref(op), ctypes.byref(pp), ctypes.byref(nb)),
+                "node_info")
+        return op.value, ctypes.string_at(pp.value, nb.value) if nb.value else b""
 
     def shape(self, value: int):
         s = (N.c_int32 * 8)()

@@ -5,7 +5,9 @@
      the backend loads with ``sox_module_load`` = hipModuleLoadData, as the reference embeds its
      shaders, Sdcb.SimdOnnx.Sources.props:21-31);
   3. ``lib/libsoxhip.so``      - the thin C ABI over libamdhip64 (include/sox_hip.h);
-     ``lib/libsoxbackend.so``  - HipBackend / HipGraphModel / HipInferenceSession (include/sox_backend.h).
+     ``lib/libsoxbackend.so``  - HipBackend / HipGraphModel / HipInferenceSession (include/sox_backend.h);
+  4. ``csrc/ext_example/*.hip`` -> ``_build/ext/<name>.hsaco``: an extension operator's kernels in a
+     code object of their own (not embedded), loaded at run time with ``sox_backend_load_module``.
 
 Run ``python -m simdonnx_amd.build`` (or ``__graft_entry__.build()``). Compiles every time it is called.
 """
@@ -20,8 +22,10 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 KDIR = os.path.join(HERE, "csrc", "kernels")
+EXT_DIR = os.path.join(HERE, "csrc", "ext_example")
 HDIR = os.path.join(HERE, "csrc", "host")
 BUILD = os.path.join(HERE, "_build")
+EXT_BUILD = os.path.join(BUILD, "ext")
 LIB = os.path.join(HERE, "lib")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
@@ -60,6 +64,25 @@ def build_code_objects(verbose=False):
 
     with ThreadPoolExecutor(max_workers=min(4, len(srcs))) as ex:
         return list(ex.map(one, srcs))
+
+
+def build_ext_examples(verbose=False):
+    """Extension code objects: built like the embedded ones, but left as files for their owner to load."""
+    os.makedirs(EXT_BUILD, exist_ok=True)
+    outs = []
+    for src in sorted(f for f in os.listdir(EXT_DIR) if f.endswith(".hip")):
+        out = os.path.join(EXT_BUILD, src[:-4] + ".hsaco")
+        _run([_hipcc(), "--genco", "--no-gpu-bundle-output", f"--offload-arch={ARCH}", *HIP_FLAGS, "-o", out,
+              os.path.join(EXT_DIR, src)])
+        if verbose:
+            print("built", out, os.path.getsize(out), "bytes", flush=True)
+        outs.append(out)
+    return outs
+
+
+def ext_example_path(name: str) -> str:
+    """Path of a built extension code object (``build_ext_examples``)."""
+    return os.path.join(EXT_BUILD, name + ".hsaco")
 
 
 def write_resources(objs):
@@ -101,6 +124,7 @@ def build_libs(verbose=False):
 def build(verbose=False):
     objs = build_code_objects(verbose)
     write_resources(objs)
+    build_ext_examples(verbose)
     return build_libs(verbose)
 
 

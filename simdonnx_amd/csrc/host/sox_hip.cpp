@@ -7,10 +7,29 @@
 #include <string.h>
 
 #include <atomic>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <vector>
 
 namespace {
 
 std::atomic<int> g_lost{0};
+
+// A launch recorded into a graph: the `extra` array hipModuleLaunchKernel is given, the size it
+// points at and a copy of the kernarg block, at addresses that stay valid for as long as the graph
+// (and the executable instantiated from it) exists. A launch outside capture passes the same three
+// from its own stack frame; a captured kernel node may keep the `extra` pointers it was given, so a
+// captured launch never hands the runtime anything on the stack.
+struct LaunchRecord {
+    void* config[5];
+    size_t size = 0;
+    std::vector<uint8_t> args;
+};
+using RecordList = std::vector<std::unique_ptr<LaunchRecord>>;
+std::mutex g_rec_mu;
+std::map<void*, RecordList> g_capturing;  // stream -> records of the capture in progress
+std::map<void*, RecordList> g_exec_recs;  // graph exec -> the records its kernel nodes point at
 
 bool is_lost_error(hipError_t e) {
     return e == hipErrorLaunchFailure || e == hipErrorIllegalAddress || e == hipErrorECCNotCorrectable ||
@@ -68,6 +87,7 @@ const char* sox_error_string(int status) {
 
 int sox_device_lost(void) { return g_lost.load(); }
 void sox_device_reset_lost(void) { g_lost.store(0); }
+void sox_device_mark_lost(void) { g_lost.store(1); }
 int sox_device_sync(void) { return st(hipDeviceSynchronize()); }
 
 int sox_malloc(void** ptr, size_t bytes) { return st(hipMalloc(ptr, bytes ? bytes : 256)); }
@@ -101,6 +121,22 @@ int sox_launch(void* fn, const uint32_t grid[3], const uint32_t block[3], uint32
                const void* kernarg, size_t kernarg_bytes) {
     if (g_lost.load()) return SOX_E_LOST;
     if (!fn || grid[0] == 0 || grid[1] == 0 || grid[2] == 0) return SOX_E_INVALID;
+    {
+        std::lock_guard<std::mutex> lk(g_rec_mu);
+        auto it = g_capturing.find(stream);
+        if (it != g_capturing.end()) {
+            auto rec = std::make_unique<LaunchRecord>();
+            rec->size = kernarg_bytes;
+            rec->args.assign((const uint8_t*)kernarg, (const uint8_t*)kernarg + kernarg_bytes);
+            void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, rec->args.data(), HIP_LAUNCH_PARAM_BUFFER_SIZE,
+                              &rec->size, HIP_LAUNCH_PARAM_END};
+            memcpy(rec->config, config, sizeof config);
+            void** extra = rec->config;
+            it->second.push_back(std::move(rec));
+            return st(hipModuleLaunchKernel((hipFunction_t)fn, grid[0], grid[1], grid[2], block[0], block[1],
+                                            block[2], lds_bytes, (hipStream_t)stream, nullptr, extra));
+        }
+    }
     size_t size = kernarg_bytes;
     void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, const_cast<void*>(kernarg), HIP_LAUNCH_PARAM_BUFFER_SIZE,
                       &size, HIP_LAUNCH_PARAM_END};
@@ -120,19 +156,53 @@ int sox_event_elapsed_ms(float* ms, void* start, void* stop) {
     return st(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
 }
 
-int sox_graph_begin(void* stream) { return st(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal)); }
+int sox_graph_begin(void* stream) {
+    if (!stream) return SOX_E_INVALID;  // the legacy default stream cannot be captured
+    {
+        std::lock_guard<std::mutex> lk(g_rec_mu);
+        if (g_capturing.count(stream)) return SOX_E_INVALID;
+        g_capturing[stream];
+    }
+    int rc = st(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal));
+    if (rc) {
+        std::lock_guard<std::mutex> lk(g_rec_mu);
+        g_capturing.erase(stream);
+    }
+    return rc;
+}
 int sox_graph_end(void* stream, void** graph_exec) {
+    RecordList recs;
+    {
+        std::lock_guard<std::mutex> lk(g_rec_mu);
+        auto it = g_capturing.find(stream);
+        if (it != g_capturing.end()) {
+            recs = std::move(it->second);
+            g_capturing.erase(it);
+        }
+    }
+    *graph_exec = nullptr;
     hipGraph_t g = nullptr;
     int rc = st(hipStreamEndCapture((hipStream_t)stream, &g));
     if (rc) return rc;
-    rc = st(hipGraphInstantiate((hipGraphExec_t*)graph_exec, g, nullptr, nullptr, 0));
+    hipGraphExec_t ex = nullptr;
+    rc = st(hipGraphInstantiate(&ex, g, nullptr, nullptr, 0));
     (void)hipGraphDestroy(g);
-    return rc;
+    if (rc) return rc;
+    *graph_exec = ex;
+    std::lock_guard<std::mutex> lk(g_rec_mu);
+    g_exec_recs[ex] = std::move(recs);
+    return SOX_OK;
 }
 int sox_graph_launch(void* graph_exec, void* stream) {
     if (g_lost.load()) return SOX_E_LOST;
     return st(hipGraphLaunch((hipGraphExec_t)graph_exec, (hipStream_t)stream));
 }
-int sox_graph_destroy(void* graph_exec) { return graph_exec ? st(hipGraphExecDestroy((hipGraphExec_t)graph_exec)) : SOX_OK; }
+int sox_graph_destroy(void* graph_exec) {
+    if (!graph_exec) return SOX_OK;
+    int rc = st(hipGraphExecDestroy((hipGraphExec_t)graph_exec));
+    std::lock_guard<std::mutex> lk(g_rec_mu);
+    g_exec_recs.erase(graph_exec);
+    return rc;
+}
 
 }  // extern "C"

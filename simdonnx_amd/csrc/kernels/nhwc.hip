@@ -1126,8 +1126,14 @@ SOX_ATTN_MFMA(128, 64)
 // one work item = one output pixel x OCV output channels; the packed [oc][kpad] weights are
 // staged once per workgroup in LDS as fp32. acc = bias + sum over taps, channels (FMA), then
 // residual and activation, one 16-byte store.
+// POOL (SOX_F_POOL, ConvP.Pool of a small-ic stem, Kernels/Nhwc.cs:661-727 / convpool.comp): the work
+// item is one pixel of the 2x2/2 max pool over the conv output instead. It computes the four conv
+// pixels of its quad (top-left, top-right, bottom-left, bottom-right, each with its bias and
+// activation, as the separate Conv node would), folds them with max in that order (PoolBand), then
+// the pool's relu, and stores only the pooled pixel: the full-resolution conv is never written.
+// p.m counts output (pooled) pixels, p.oh / p.ow stay the conv output's size (twice the pooled one).
 // ------------------------------------------------------------------------------------------
-template <typename T, int OCV>
+template <typename T, int OCV, bool POOL>
 __device__ __forceinline__ void conv_direct_body(const sox_igemm_args& p) {
     extern __shared__ float wl[];  // [oc][K]
     const int K = p.k;
@@ -1141,46 +1147,67 @@ __device__ __forceinline__ void conv_direct_body(const sox_igemm_args& p) {
     if (idx >= (long)p.m * ocg) return;
     const int og = (int)(idx % ocg);
     const long m = idx / ocg;
-    const int ohw = p.oh * p.ow;
+    const int yh = POOL ? p.oh / 2 : p.oh, yw = POOL ? p.ow / 2 : p.ow;  // output grid
+    const int ohw = yh * yw;
     const int b = (int)(m / ohw), r = (int)(m - (long)b * ohw);
-    const int oy = r / p.ow, ox = r - oy * p.ow;
+    const int py = r / yw, px = r - py * yw;
     const bool reflect = (p.flags & SOX_F_REFLECT) != 0;
+    const int act = (p.flags & SOX_F_ACT_MASK) >> SOX_F_ACT_SHIFT;
     const T* __restrict__ x = (const T*)p.x + (long)b * p.ih * p.iw * p.ic;
-    float acc[OCV];
-#pragma unroll
-    for (int e = 0; e < OCV; e++) acc[e] = (p.flags & SOX_F_BIAS) ? p.bias[og * OCV + e] : 0.0f;
     const float* w0 = wl + (long)og * OCV * K;
-    for (int ky = 0; ky < p.kh; ky++) {
-        int iy = sox_src_index(oy * p.sh + ky - p.pt, p.ih, reflect);
-        for (int kx = 0; kx < p.kw; kx++) {
-            int ix = sox_src_index(ox * p.sw + kx - p.pl, p.iw, reflect);
-            const int k0 = (ky * p.kw + kx) * p.ic;
-            for (int c = 0; c < p.ic; c++) {
-                float xv = iy < 0 || ix < 0 ? p.pad_value : to_f(x[((long)iy * p.iw + ix) * p.ic + c]);
+    // bias + taps of conv pixel (oy, ox)
+    auto conv_at = [&](int oy, int ox, float (&acc)[OCV]) __attribute__((always_inline)) {
 #pragma unroll
-                for (int e = 0; e < OCV; e++) acc[e] = __builtin_fmaf(xv, w0[e * K + k0 + c], acc[e]);
+        for (int e = 0; e < OCV; e++) acc[e] = (p.flags & SOX_F_BIAS) ? p.bias[og * OCV + e] : 0.0f;
+        for (int ky = 0; ky < p.kh; ky++) {
+            int iy = sox_src_index(oy * p.sh + ky - p.pt, p.ih, reflect);
+            for (int kx = 0; kx < p.kw; kx++) {
+                int ix = sox_src_index(ox * p.sw + kx - p.pl, p.iw, reflect);
+                const int k0 = (ky * p.kw + kx) * p.ic;
+                for (int c = 0; c < p.ic; c++) {
+                    float xv = iy < 0 || ix < 0 ? p.pad_value : to_f(x[((long)iy * p.iw + ix) * p.ic + c]);
+#pragma unroll
+                    for (int e = 0; e < OCV; e++) acc[e] = __builtin_fmaf(xv, w0[e * K + k0 + c], acc[e]);
+                }
             }
         }
-    }
-    const int act = (p.flags & SOX_F_ACT_MASK) >> SOX_F_ACT_SHIFT;
+    };
     typedef typename VecT<T, OCV>::Vec Vec;
     const long o = m * p.ldy + og * OCV;
-    if (p.flags & SOX_F_RESIDUAL) {
-        Vec av = *(const Vec*)((const T*)p.add + o);
-#pragma unroll
-        for (int e = 0; e < OCV; e++) acc[e] = acc[e] + to_f(av[e]);
-    }
     Vec out;
+    if constexpr (POOL) {
+        float best[OCV];
 #pragma unroll
-    for (int e = 0; e < OCV; e++) out[e] = (T)sox_act(acc[e], act);
+        for (int q = 0; q < 4; q++) {
+            float acc[OCV];
+            conv_at(2 * py + (q >> 1), 2 * px + (q & 1), acc);
+#pragma unroll
+            for (int e = 0; e < OCV; e++) {
+                const float v = sox_act(acc[e], act);
+                best[e] = q == 0 ? v : fmaxf(best[e], v);
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < OCV; e++) out[e] = (T)((p.flags & SOX_F_POOL_RELU) ? fmaxf(best[e], 0.0f) : best[e]);
+    } else {
+        float acc[OCV];
+        conv_at(py, px, acc);
+        if (p.flags & SOX_F_RESIDUAL) {
+            Vec av = *(const Vec*)((const T*)p.add + o);
+#pragma unroll
+            for (int e = 0; e < OCV; e++) acc[e] = acc[e] + to_f(av[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < OCV; e++) out[e] = (T)sox_act(acc[e], act);
+    }
     *(Vec*)((T*)p.y + o) = out;
 }
 
 // 3x3 taps over 3 channels (the RGB stems): all 27 input values of a pixel are loaded up front
 // (out-of-image taps read pixel 0 and take the pad value) instead of one dependent load per term.
 // The weights are staged k-major ([K][oc]), so a thread's OCV weights of one term are OCV / 4
-// 16-byte LDS reads.
-template <typename T, int OCV>
+// 16-byte LDS reads. POOL as conv_direct_body.
+template <typename T, int OCV, bool POOL>
 __device__ __forceinline__ void conv_direct_333_body(const sox_igemm_args& p) {
     constexpr int KH = 3, KW = 3, IC = 3, K = KH * KW * IC;
     extern __shared__ float wl[];  // [K][oc]
@@ -1193,50 +1220,70 @@ __device__ __forceinline__ void conv_direct_333_body(const sox_igemm_args& p) {
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;  // m * ocg < 2^31 (the launcher checks)
     if (idx >= p.m * ocg) return;
     const int m = idx / ocg, og = idx - m * ocg;
-    const int ohw = p.oh * p.ow;
+    const int yh = POOL ? p.oh / 2 : p.oh, yw = POOL ? p.ow / 2 : p.ow;
+    const int ohw = yh * yw;
     const int b = m / ohw, r = m - b * ohw;
-    const int oy = r / p.ow, ox = r - oy * p.ow;
+    const int py = r / yw, px = r - py * yw;
     const bool reflect = (p.flags & SOX_F_REFLECT) != 0;
+    const int act = (p.flags & SOX_F_ACT_MASK) >> SOX_F_ACT_SHIFT;
     const T* __restrict__ x = (const T*)p.x + (long)b * p.ih * p.iw * IC;
-    float xv[K];
+    const float* w0 = wl + og * OCV;  // oc % 4 == 0: 16-byte aligned rows
+    auto conv_at = [&](int oy, int ox, float (&acc)[OCV]) __attribute__((always_inline)) {
+        float xv[K];
 #pragma unroll
-    for (int ky = 0; ky < KH; ky++) {
-        const int iy = sox_src_index(oy * p.sh + ky - p.pt, p.ih, reflect);
+        for (int ky = 0; ky < KH; ky++) {
+            const int iy = sox_src_index(oy * p.sh + ky - p.pt, p.ih, reflect);
 #pragma unroll
-        for (int kx = 0; kx < KW; kx++) {
-            const int ix = sox_src_index(ox * p.sw + kx - p.pl, p.iw, reflect);
-            const bool in = iy >= 0 && ix >= 0;
-            const T* px = x + (in ? ((long)iy * p.iw + ix) * IC : 0);
+            for (int kx = 0; kx < KW; kx++) {
+                const int ix = sox_src_index(ox * p.sw + kx - p.pl, p.iw, reflect);
+                const bool in = iy >= 0 && ix >= 0;
+                const T* px_ = x + (in ? ((long)iy * p.iw + ix) * IC : 0);
 #pragma unroll
-            for (int c = 0; c < IC; c++) {
-                const float v = to_f(px[c]);  // always a valid address: issued with the others
-                xv[(ky * KW + kx) * IC + c] = in ? v : p.pad_value;
+                for (int c = 0; c < IC; c++) {
+                    const float v = to_f(px_[c]);  // always a valid address: issued with the others
+                    xv[(ky * KW + kx) * IC + c] = in ? v : p.pad_value;
+                }
             }
         }
-    }
-    float acc[OCV];
 #pragma unroll
-    for (int e = 0; e < OCV; e++) acc[e] = (p.flags & SOX_F_BIAS) ? p.bias[og * OCV + e] : 0.0f;
-    const float* w0 = wl + og * OCV;  // oc % 4 == 0: 16-byte aligned rows
+        for (int e = 0; e < OCV; e++) acc[e] = (p.flags & SOX_F_BIAS) ? p.bias[og * OCV + e] : 0.0f;
 #pragma unroll
-    for (int kk = 0; kk < K; kk++) {
-        float4v wv[OCV / 4];
+        for (int kk = 0; kk < K; kk++) {
+            float4v wv[OCV / 4];
 #pragma unroll
-        for (int v = 0; v < OCV / 4; v++) wv[v] = *(const float4v*)(w0 + kk * p.n + 4 * v);
+            for (int v = 0; v < OCV / 4; v++) wv[v] = *(const float4v*)(w0 + kk * p.n + 4 * v);
 #pragma unroll
-        for (int e = 0; e < OCV; e++) acc[e] = __builtin_fmaf(xv[kk], wv[e / 4][e % 4], acc[e]);
-    }
-    const int act = (p.flags & SOX_F_ACT_MASK) >> SOX_F_ACT_SHIFT;
+            for (int e = 0; e < OCV; e++) acc[e] = __builtin_fmaf(xv[kk], wv[e / 4][e % 4], acc[e]);
+        }
+    };
+    auto fin = [&](float v) __attribute__((always_inline)) {
+        return sizeof(T) == 2 ? act_fast(v, act) : sox_act(v, act);
+    };
     typedef typename VecT<T, OCV>::Vec Vec;
     const long o = (long)m * p.ldy + og * OCV;
-    if (p.flags & SOX_F_RESIDUAL) {
-        const Vec av = *(const Vec*)((const T*)p.add + o);
-#pragma unroll
-        for (int e = 0; e < OCV; e++) acc[e] = acc[e] + to_f(av[e]);
-    }
     Vec out;
+    if constexpr (POOL) {
+        float best[OCV];
 #pragma unroll
-    for (int e = 0; e < OCV; e++) out[e] = (T)(sizeof(T) == 2 ? act_fast(acc[e], act) : sox_act(acc[e], act));
+        for (int q = 0; q < 4; q++) {
+            float acc[OCV];
+            conv_at(2 * py + (q >> 1), 2 * px + (q & 1), acc);
+#pragma unroll
+            for (int e = 0; e < OCV; e++) best[e] = q == 0 ? fin(acc[e]) : fmaxf(best[e], fin(acc[e]));
+        }
+#pragma unroll
+        for (int e = 0; e < OCV; e++) out[e] = (T)((p.flags & SOX_F_POOL_RELU) ? fmaxf(best[e], 0.0f) : best[e]);
+    } else {
+        float acc[OCV];
+        conv_at(py, px, acc);
+        if (p.flags & SOX_F_RESIDUAL) {
+            const Vec av = *(const Vec*)((const T*)p.add + o);
+#pragma unroll
+            for (int e = 0; e < OCV; e++) acc[e] = acc[e] + to_f(av[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < OCV; e++) out[e] = (T)fin(acc[e]);
+    }
     *(Vec*)((T*)p.y + o) = out;
 }
 
@@ -1265,8 +1312,6 @@ __device__ __forceinline__ void conv_narrow_body(const sox_igemm_args& p) {
     float acc[OC];
 #pragma unroll
     for (int e = 0; e < OC; e++) acc[e] = (p.flags & SOX_F_BIAS) ? p.bias[e] : 0.0f;
-    const half_t pv = (half_t)p.pad_value;
-    const half8 pad8v = {pv, pv, pv, pv, pv, pv, pv, pv};
     for (int ky = 0; ky < p.kh; ky++) {
         const int iy = sox_src_index(oy * p.sh + ky - p.pt, p.ih, reflect);
         for (int kx = 0; kx < p.kw; kx++) {
@@ -1275,10 +1320,10 @@ __device__ __forceinline__ void conv_narrow_body(const sox_igemm_args& p) {
             const half_t* xr = x + ((long)(in ? iy : 0) * p.iw + (in ? ix : 0)) * p.ic;
             const float* wk = wl + (ky * p.kw + kx) * p.ic * 8;
             for (int c = 0; c < p.ic; c += 8) {
-                const half8 xv = in ? *(const half8*)(xr + c) : pad8v;
+                const half8 xv = *(const half8*)(xr + c);  // pixel 0 for a padding tap (not used)
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
-                    const float xf = (float)xv[j];
+                    const float xf = in ? (float)xv[j] : p.pad_value;  // the pad value stays fp32
                     const float4v w0 = *(const float4v*)(wk + (c + j) * 8);
 #pragma unroll
                     for (int e = 0; e < (OC < 4 ? OC : 4); e++) acc[e] = __builtin_fmaf(xf, w0[e], acc[e]);
@@ -1306,7 +1351,12 @@ __device__ __forceinline__ void conv_narrow_body(const sox_igemm_args& p) {
 SOX_CONV_NARROW(1) SOX_CONV_NARROW(2) SOX_CONV_NARROW(3) SOX_CONV_NARROW(4)
 SOX_CONV_NARROW(5) SOX_CONV_NARROW(6) SOX_CONV_NARROW(7)
 
-extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_333_f16(sox_igemm_args p) { conv_direct_333_body<half_t, 8>(p); }
-extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_333_f32(sox_igemm_args p) { conv_direct_333_body<float, 4>(p); }
-extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_f16(sox_igemm_args p) { conv_direct_body<half_t, 8>(p); }
-extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_f32(sox_igemm_args p) { conv_direct_body<float, 4>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_333_f16(sox_igemm_args p) { conv_direct_333_body<half_t, 8, false>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_333_f32(sox_igemm_args p) { conv_direct_333_body<float, 4, false>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_f16(sox_igemm_args p) { conv_direct_body<half_t, 8, false>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_f32(sox_igemm_args p) { conv_direct_body<float, 4, false>(p); }
+// with the fused 2x2/2 max pool (SOX_F_POOL)
+extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_333_pool_f16(sox_igemm_args p) { conv_direct_333_body<half_t, 8, true>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_333_pool_f32(sox_igemm_args p) { conv_direct_333_body<float, 4, true>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_pool_f16(sox_igemm_args p) { conv_direct_body<half_t, 8, true>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_pool_f32(sox_igemm_args p) { conv_direct_body<float, 4, true>(p); }

@@ -13,6 +13,9 @@ cannot be reproduced outside .NET). Workloads:
 """
 from __future__ import annotations
 
+import functools
+import os
+
 import numpy as np
 
 from . import synth
@@ -87,6 +90,46 @@ MBV3_SMALL = [
 MBV3_TAPS = (0, 2, 7, 10)
 
 
+# ---------------------------------------------------------------------------------------------
+# BatchNorm folds of the random weights (configs 3 and 4). A trained MobileNetV3 / DBNet has a
+# BatchNorm after every conv, which OnnxRewrites.FoldConvBatchNorm (Onnx/OnnxRewrites.cs:71-111)
+# folds into the conv: per output channel, w' = w s and b' = b s + t. With He-normal weights and no
+# BatchNorm the detector's activations grow through the residual and FPN sums to logits of |70|,
+# where fp16 storage by itself moves the sigmoid output by 5e-2, so no fp16 engine could meet 2e-2.
+# Here every conv carries the fold of a BatchNorm (gamma 1, beta 0) whose statistics were measured
+# once with the CPU reference on the seeded N(0, 1) calibration image at the config's size: the
+# pre-activation of each output channel (the conv part of a residual projection, the detector's
+# logit) has mean 0 and standard deviation 1. The (s, t) pairs are
+# committed in data/bn_calibration.npz, keyed "<model>/<layer>/s|t", by
+# tests/golden/make_bn_calibration.py; the weights stay the seeded He-normal draws, rescaled.
+# ---------------------------------------------------------------------------------------------
+_CAL_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "data", "bn_calibration.npz")
+
+
+@functools.lru_cache(maxsize=1)
+def _bn_calibration() -> dict:
+    with np.load(_CAL_PATH, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def _bn_scale(scales, model: str, layer: str, w, b, transpose=False):
+    """(w, b) with the layer's folded BatchNorm (w s, b s + t per output channel: axis 0 of a Conv
+    weight, axis 1 of a ConvTranspose weight). scales None: the committed calibration; a dict: the
+    calibration in progress (a missing layer is left as it is)."""
+    key = f"{model}/{layer}"
+    cal = _bn_calibration() if scales is None else scales
+    if key + "/s" not in cal:
+        if scales is None:
+            raise KeyError(f"no BatchNorm calibration for {key}")
+        return w, b
+    sc = np.asarray(cal[key + "/s"], np.float64)
+    sh = np.asarray(cal[key + "/t"], np.float64)
+    shape = (1, -1, 1, 1) if transpose else (-1, 1, 1, 1)
+    w2 = (w.astype(np.float64) * sc.reshape(shape)).astype(np.float32)
+    b64 = np.zeros(len(sc)) if b is None else b.astype(np.float64)
+    return w2, (b64 * sc + sh).astype(np.float32)
+
+
 def _make_divisible(v, d=8):
     return max(d, int(v + d / 2) // d * d)
 
@@ -95,21 +138,27 @@ def _bias(seed, ids, c):
     return synth.uniform(seed, ids(), (c,), -0.1, 0.1)
 
 
-def mobilenetv3_backbone(pb: PlanBuilder, x: int, seed: int, ids: _Ids, name="mbv3"):
-    """Emits the stem + 11 inverted-residual blocks; returns (last output, [tap outputs])."""
+def mobilenetv3_backbone(pb: PlanBuilder, x: int, seed: int, ids: _Ids, name="mbv3", model="mbv3", scales=None):
+    """Emits the stem + 11 inverted-residual blocks; returns (last output, [tap outputs]). Every conv
+    carries its folded BatchNorm (_bn_scale of `model`'s calibration)."""
+
+    def conv(h, w, b, *, name, **kw):
+        w, b = _bn_scale(scales, model, name, w, b)
+        return pb.conv(h, w, b, name=name, **kw)
+
     c_in = 3
-    y = pb.conv(x, synth.he_normal(seed, ids(), (16, c_in, 3, 3)), _bias(seed, ids, 16), stride=2, pad=1,
-                act="hardswish", name=f"{name}.stem")
+    y = conv(x, synth.he_normal(seed, ids(), (16, c_in, 3, 3)), _bias(seed, ids, 16), stride=2, pad=1,
+             act="hardswish", name=f"{name}.stem")
     c_in = 16
     taps = []
     for bi, (k, exp, out, se, act, s) in enumerate(MBV3_SMALL):
         bname = f"{name}.b{bi}"
         h = y
         if exp != c_in:
-            h = pb.conv(h, synth.he_normal(seed, ids(), (exp, c_in, 1, 1)), _bias(seed, ids, exp), stride=1, pad=0,
-                        act=act, name=f"{bname}.expand")
-        h = pb.conv(h, synth.he_normal(seed, ids(), (exp, 1, k, k)), _bias(seed, ids, exp), stride=s, pad=k // 2,
-                    group=exp, act=act, name=f"{bname}.dw")
+            h = conv(h, synth.he_normal(seed, ids(), (exp, c_in, 1, 1)), _bias(seed, ids, exp), stride=1, pad=0,
+                     act=act, name=f"{bname}.expand")
+        h = conv(h, synth.he_normal(seed, ids(), (exp, 1, k, k)), _bias(seed, ids, exp), stride=s, pad=k // 2,
+                 group=exp, act=act, name=f"{bname}.dw")
         if se:
             r = _make_divisible(exp // 4)
             w1 = synth.he_normal(seed, ids(), (r, exp, 1, 1))
@@ -118,61 +167,73 @@ def mobilenetv3_backbone(pb: PlanBuilder, x: int, seed: int, ids: _Ids, name="mb
                                    alpha=1.0 / 6.0, beta=0.5, name=f"{bname}.se")
             h = pb.mul(h, gate, name=f"{bname}.se_scale")
         residual = y if (s == 1 and c_in == out) else None
-        y = pb.conv(h, synth.he_normal(seed, ids(), (out, exp, 1, 1)), _bias(seed, ids, out), stride=1, pad=0,
-                    act="none", add=residual, name=f"{bname}.project")
+        y = conv(h, synth.he_normal(seed, ids(), (out, exp, 1, 1)), _bias(seed, ids, out), stride=1, pad=0,
+                 act="none", add=residual, name=f"{bname}.project")
         c_in = out
         if bi in MBV3_TAPS:
             taps.append(y)
     return y, taps
 
 
-def mobilenetv3_small(seed: int = 3, n=1, size=640):
-    """Config 3: the MobileNetV3-small block stack at 3 x size x size, input ~ N(0,1)."""
+def mobilenetv3_small(seed: int = 3, n=1, size=640, scales=None):
+    """Config 3: the MobileNetV3-small block stack at 3 x size x size, input ~ N(0,1), He-normal
+    weights with folded BatchNorms (scales: see _bn_scale)."""
     pb = PlanBuilder()
     ids = _Ids()
     x = pb.input((n, 3, size, size), NHWC, "image")
-    y, _ = mobilenetv3_backbone(pb, x, seed, ids)
+    y, _ = mobilenetv3_backbone(pb, x, seed, ids, model="mbv3", scales=scales)
     plan = pb.build(y)
     xin = synth.normal(seed, 10_000, (n, size, size, 3), 1.0)
     return plan, [xin]
 
 
-def dbnet(seed: int = 4, n=1, size=960):
+def dbnet(seed: int = 4, n=1, size=960, scales=None, logit=False):
     """Config 4: DBNet-style detector - MobileNetV3-small backbone, 4-level FPN (1x1 laterals to 96,
     nearest x2 + add top-down, 3x3 convs 96->24 per level, upsample + concat to 96 at 1/4 scale), head
     conv3x3 + BN + ReLU, ConvT 2x2 s2 + BN + ReLU, ConvT 2x2 s2 + bias + Sigmoid -> 1 x size x size.
     The BatchNormalization after the first ConvTranspose is not foldable (OnnxRewrites.cs:78-82) and
-    lowers to per-channel Mul + Add(+ReLU) (GraphCompiler.cs:1898-1923)."""
+    lowers to per-channel Mul + Add(+ReLU) (GraphCompiler.cs:1898-1923). He-normal weights with the
+    folded BatchNorms of every other conv (scales: see _bn_scale); logit=True ends at the logit (no
+    sigmoid), for calibration."""
     pb = PlanBuilder()
     ids = _Ids()
     x = pb.input((n, 3, size, size), NHWC, "image")
-    _, (c2, c3, c4, c5) = mobilenetv3_backbone(pb, x, seed, ids)
+    _, (c2, c3, c4, c5) = mobilenetv3_backbone(pb, x, seed, ids, model="dbnet", scales=scales)
     chans = [pb.values[v].phys[3] for v in (c2, c3, c4, c5)]
     oc = 96
-    lat = [pb.conv(v, synth.he_normal(seed, ids(), (oc, c, 1, 1)), None, stride=1, pad=0, name=f"fpn.lat{i}")
+
+    def conv(h, w, b, *, name, **kw):
+        w, b = _bn_scale(scales, "dbnet", name, w, b)
+        return pb.conv(h, w, b, name=name, **kw)
+
+    def convt(h, w, b, *, name, **kw):
+        w, b = _bn_scale(scales, "dbnet", name, w, b, transpose=True)
+        return pb.conv_transpose(h, w, b, name=name, **kw)
+
+    lat = [conv(v, synth.he_normal(seed, ids(), (oc, c, 1, 1)), None, stride=1, pad=0, name=f"fpn.lat{i}")
            for i, (v, c) in enumerate(zip((c2, c3, c4, c5), chans))]
     in2, in3, in4, in5 = lat
     out4 = pb.resize_nearest(in5, 2, add=in4, name="fpn.up5")
     out3 = pb.resize_nearest(out4, 2, add=in3, name="fpn.up4")
     out2 = pb.resize_nearest(out3, 2, add=in2, name="fpn.up3")
     q = oc // 4
-    p5 = pb.conv(in5, synth.he_normal(seed, ids(), (q, oc, 3, 3)), None, pad=1, name="fpn.p5")
-    p4 = pb.conv(out4, synth.he_normal(seed, ids(), (q, oc, 3, 3)), None, pad=1, name="fpn.p4")
-    p3 = pb.conv(out3, synth.he_normal(seed, ids(), (q, oc, 3, 3)), None, pad=1, name="fpn.p3")
-    p2 = pb.conv(out2, synth.he_normal(seed, ids(), (q, oc, 3, 3)), None, pad=1, name="fpn.p2")
+    p5 = conv(in5, synth.he_normal(seed, ids(), (q, oc, 3, 3)), None, pad=1, name="fpn.p5")
+    p4 = conv(out4, synth.he_normal(seed, ids(), (q, oc, 3, 3)), None, pad=1, name="fpn.p4")
+    p3 = conv(out3, synth.he_normal(seed, ids(), (q, oc, 3, 3)), None, pad=1, name="fpn.p3")
+    p2 = conv(out2, synth.he_normal(seed, ids(), (q, oc, 3, 3)), None, pad=1, name="fpn.p2")
     p5 = pb.resize_nearest(p5, 8, name="fpn.p5_up")
     p4 = pb.resize_nearest(p4, 4, name="fpn.p4_up")
     p3 = pb.resize_nearest(p3, 2, name="fpn.p3_up")
     fuse = pb.concat_channels([p5, p4, p3, p2], name="fpn.concat")
-    h = pb.conv(fuse, synth.he_normal(seed, ids(), (q, oc, 3, 3)), _bias(seed, ids, q), pad=1, act="relu",
-                name="head.conv")
-    h = pb.conv_transpose(h, synth.he_normal(seed, ids(), (q, q, 2, 2)), _bias(seed, ids, q), name="head.convt1")
+    h = conv(fuse, synth.he_normal(seed, ids(), (q, oc, 3, 3)), _bias(seed, ids, q), pad=1, act="relu",
+             name="head.conv")
+    h = convt(h, synth.he_normal(seed, ids(), (q, q, 2, 2)), _bias(seed, ids, q), name="head.convt1")
     bn_s = pb.const(synth.uniform(seed, ids(), (q, 1, 1), 0.5, 1.5), "head.bn_scale")
     bn_t = pb.const(synth.uniform(seed, ids(), (q, 1, 1), -0.1, 0.1), "head.bn_shift")
     h = pb.ew(h, bn_s, 2, name="head.bn_mul")
     h = pb.ew(h, bn_t, 0, act="relu", name="head.bn_add")
-    y = pb.conv_transpose(h, synth.he_normal(seed, ids(), (q, 1, 2, 2)), _bias(seed, ids, 1), act="sigmoid",
-                          name="head.convt2")
+    y = convt(h, synth.he_normal(seed, ids(), (q, 1, 2, 2)), _bias(seed, ids, 1), act="none" if logit else "sigmoid",
+              name="head.convt2")
     plan = pb.build(y)
     xin = synth.normal(seed, 10_000, (n, size, size, 3), 1.0)
     return plan, [xin]

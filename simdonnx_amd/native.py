@@ -148,6 +148,7 @@ THIN_API = {
     "sox_error_string": (ctypes.c_char_p, [c_int32]),
     "sox_device_lost": (c_int32, []),
     "sox_device_reset_lost": (None, []),
+    "sox_device_mark_lost": (None, []),
     "sox_device_sync": (c_int32, []),
     "sox_malloc": (c_int32, [ctypes.POINTER(c_void_p), c_size_t]),
     "sox_free": (c_int32, [c_void_p]),
@@ -196,6 +197,8 @@ BACKEND_API = {
                                      c_uint32]),
     "sox_graph_node_info": (c_int32, [c_void_p, c_int32, ctypes.POINTER(c_int32), ctypes.POINTER(c_void_p),
                                       ctypes.POINTER(c_size_t)]),
+    "sox_graph_node_values": (c_int32, [c_void_p, c_int32, ctypes.POINTER(c_int32), c_int32, ctypes.POINTER(c_int32),
+                                        ctypes.POINTER(c_int32), c_int32, ctypes.POINTER(c_int32)]),
     "sox_graph_value_shape": (c_int32, [c_void_p, c_int32, ctypes.POINTER(c_int32), c_int32,
                                         ctypes.POINTER(c_int32)]),
     "sox_graph_is_f16": (c_int32, [c_void_p]),

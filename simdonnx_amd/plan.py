@@ -536,6 +536,12 @@ class PlanBuilder:
         y = self.activation(val.shape, val.layout, name)
         return self._node(op, [x], [y], None, name)
 
+    def hard_sigmoid(self, x, alpha=0.2, beta=0.5, name=""):
+        """HardSigmoid: clamp(alpha x + beta, 0, 1) (HardSigmoidP, ExecPlan.cs:103-106)."""
+        val = self.values[x]
+        y = self.activation(val.shape, val.layout, name)
+        return self._node("HardSigmoid", [x], [y], HardSigmoidP(alpha, beta), name)
+
     def attention(self, qkv, heads, head_dim, scale, name=""):
         """Fused attention over a packed [N, T, 3*H*D] QKV tensor viewed as [N, T, 3, H, D]
         (AttentionP with FixAxis 2 = 0/1/2); output [N, H, T, D] stored as [N, T, H, D]."""
@@ -596,6 +602,15 @@ class PlanBuilder:
         else:
             y = self.image(n, c // (block * block), h * block, w * block, name)
         return self._node("SpaceToDepth" if inverse else "DepthToSpace", [x], [y], DepthToSpaceP(block, crd), name)
+
+    def max_pool(self, x, kernel, stride, pads, relu=False, name=""):
+        """MaxPool of an NHWC image, pads (t, l, b, r), PoolP.FuseRelu (GraphCompiler.EmitPool,
+        GraphCompiler.cs:1805-1825; the Relu fold of :312-315)."""
+        n, h, w, c = self.values[x].phys
+        oh = _out_size(h, kernel[0], stride[0], pads[0], pads[2])
+        ow = _out_size(w, kernel[1], stride[1], pads[1], pads[3])
+        y = self.image(n, c, oh, ow, name)
+        return self._node("MaxPool", [x], [y], PoolP(tuple(kernel), tuple(stride), tuple(pads), relu), name)
 
     def avg_pool(self, x, kernel, stride, pads, count_include_pad=False, name=""):
         """AveragePool of an NHWC image, pads (t, l, b, r) (PoolP)."""

@@ -22,8 +22,10 @@ def max_rel(got, want):
     return float(np.abs(got - want).max()) / scale
 
 
-@pytest.fixture(scope="session")
+@pytest.fixture
 def hip():
-    """The default HIP backend; GPU tests fail loudly (not skip) when the native library is missing."""
+    """The default HIP backend; GPU tests fail loudly (not skip) when the native library is missing.
+    Looked up per test: a test that marks the device lost leaves the next one a new backend, as
+    HipBackend.Default does after a loss."""
     from simdonnx_amd.backend import HipBackend
     return HipBackend.default()

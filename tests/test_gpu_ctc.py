@@ -91,3 +91,43 @@ def test_recognizer_features_to_ctc(hip):
         feats = s.read_value(plan.output).reshape(-1, hw.shape[0])
         idx, prob = ctc.argmax(s, plan.output, 32, feats.shape[0] // 32)
     check(feats, f16(hw), hb, idx, prob)
+
+
+def test_ctc_few_rows_many_columns(hip):
+    """One short line against the full 6625-class head: the column ranges are capped at 64 (one merge
+    wave per row) instead of one per CU."""
+    x = f16(synth.normal(43, 1, (40, 192), 1.0))
+    w = f16(synth.normal(43, 2, (192, 6625), 0.1))
+    b = synth.uniform(43, 3, (6625,), -0.5, 0.5)
+    ctc = HipCtcProjection(hip, w, b, 192, 6625)
+    s, xv = features_session(hip, x)
+    with s:
+        res = ctc.argmax(s, xv, 1, 40)
+    assert res is not None
+    check(x, w, b, *res)
+
+
+def test_ctc_rejects_overwritten_and_fp32_features(hip):
+    """A mid-graph value whose arena range a later node reuses, and an fp32 session, are errors
+    (SOX_E_INVALID), not the unfused head's None."""
+    x = f16(synth.normal(44, 1, (64, 64), 1.0))
+    w = f16(synth.normal(44, 2, (64, 1100), 0.1))
+    ctc = HipCtcProjection(hip, w, None, 64, 1100)
+    pb = PlanBuilder()
+    xv = pb.input(x.shape, None, "x")
+    a = pb.unary("Relu", xv, name="a")
+    bb = pb.unary("Sigmoid", a, name="b")
+    c = pb.unary("Copy", bb, name="c")  # reuses a's buffer once a is dead
+    plan = pb.build(c)
+    assert plan.buf_offset[plan.values[a].buf] == plan.buf_offset[plan.values[c].buf]
+    with HipInferenceSession(hip.graph(plan, True)) as s:
+        s.set_input(x)
+        s.run()
+        with pytest.raises(SoxError, match="overwrites"):
+            ctc.argmax(s, a, 1, 64)
+        assert ctc.argmax(s, c, 1, 64) is not None
+    with HipInferenceSession(hip.graph(plan, False)) as s:
+        s.set_input(x)
+        s.run()
+        with pytest.raises(SoxError, match="fp16"):
+            ctc.argmax(s, c, 1, 64)

@@ -477,7 +477,8 @@ def test_gemm_residual_add_fused(hip, m, k, n, act, half):
 # output channels take the one-pixel-per-item direct kernel; K = 9 * 128 is its largest reduction
 NARROW_CASES = [(1, 8, 3, 3, 1, 37, 61, "none", False, 0, 0.0), (2, 16, 1, 3, 1, 20, 18, "sigmoid", True, 0, 0.0),
                 (1, 24, 5, 3, 2, 33, 29, "relu", False, 0, 0.0), (1, 8, 7, 5, 1, 15, 22, "hardswish", True, 1, 0.0),
-                (1, 128, 2, 3, 1, 9, 10, "gelu", False, 0, 0.0), (1, 8, 4, 3, 1, 11, 13, "none", False, 0, -0.5)]
+                (1, 128, 2, 3, 1, 9, 10, "gelu", False, 0, 0.0), (1, 8, 4, 3, 1, 11, 13, "none", False, 0, -0.5),
+                (1, 16, 3, 3, 1, 21, 17, "none", False, 0, 0.1)]
 
 
 @pytest.mark.parametrize("case", NARROW_CASES, ids=lambda c: "x".join(str(v) for v in c))
@@ -497,3 +498,23 @@ def test_conv_narrow_route(hip, case):
     want = O.conv(x, wt, b, add, stride=(s, s), pads=pads, act=act, pad_mode=mode, pad_value=pv)
     assert got.shape == want.shape
     assert max_rel(got, want) < TOL[True]
+
+
+def test_conv_narrow_pad_value_is_fp32(hip):
+    """The constant pad value enters the narrow kernel's FMAs in fp32, as in the other routes and the
+    oracle: two pad values inside one fp16 rounding interval (0.09996 and 0.1 both round to
+    0.0999756) must still give different border outputs, each within the fp16 bar of the oracle."""
+    x = f16(synth.uniform(20, 1, (1, 24, 20, 16), -1, 1))
+    wt = f16(synth.normal(20, 2, (3, 16, 3, 3), 0.15))
+    b = synth.uniform(20, 3, (3,), -0.2, 0.2)
+    assert np.float16(0.09996) == np.float16(0.1)
+    outs = []
+    for pv in (0.09996, 0.1):
+        plan, ins = conv_plan(x, wt, b, None, (1, 1), (1, 1, 1, 1), "none", 0, pv)
+        assert [d[0] for d in hip.graph(plan, True).dispatches] == ["conv_narrow"]
+        got = run(hip, plan, ins, True)
+        want = O.conv(x, wt, b, stride=(1, 1), pads=(1, 1, 1, 1), pad_value=pv)
+        assert max_rel(got, want) < TOL[True]
+        outs.append(got)
+    assert not np.array_equal(outs[0], outs[1])
+    assert np.array_equal(outs[0][:, 1:-1, 1:-1], outs[1][:, 1:-1, 1:-1])  # interior pixels see no padding

@@ -232,3 +232,72 @@ def test_up_head(hip, c, oc, act, skip_conv, hw, half):
     got = run(hip, pb.build(y), [x, sk], half, "uphead")
     want = O.up_head(x, skip, f16(wh) if half else wh, bh, 2, resize_relu=True, skip_relu=True, act=act)
     assert max_rel(got, want) < TOL[half]
+
+
+@HALF
+@pytest.mark.parametrize("op", ["Relu", "Sigmoid", "Gelu", "HardSwish", "Swish", "HardSigmoid", "Copy"])
+@pytest.mark.parametrize("shape", [(1, 17, 23, 24), (2, 5, 7, 3)], ids=["vec", "tail"])
+def test_standalone_activation(hip, op, shape, half):
+    """The activation ops that stay nodes of their own (not folded into a producer's epilogue),
+    VkGraph.cs:495-553 (unary.comp / hsig.comp / copy): per element, fp32 math."""
+    n, h, w, c = shape
+    x = img(31, shape, half) * 4.0
+    pb = PlanBuilder()
+    xv = pb.input((n, c, h, w), NHWC, "x")
+    if op == "HardSigmoid":
+        y = pb.hard_sigmoid(xv, 0.25, 0.4, name="hsig")
+    else:
+        y = pb.unary(op, xv, name=op.lower())
+    got = run(hip, pb.build(y), [x], half, "unary")
+    if op == "Copy":
+        assert np.array_equal(got, x)
+        return
+    want = O.hard_sigmoid(x, 0.25, 0.4) if op == "HardSigmoid" else O.activation(x, op.lower())
+    assert max_rel(got, want) < TOL[half]
+
+
+@HALF
+@pytest.mark.parametrize("n,h,w,c,k,s,pads,relu", [
+    (1, 32, 40, 16, 2, 2, (0, 0, 0, 0), False), (2, 15, 13, 24, 3, 2, (1, 1, 1, 1), True),
+    (1, 9, 11, 3, 3, 1, (1, 1, 1, 1), False), (1, 12, 10, 8, 2, 2, (0, 0, 1, 1), True)])
+def test_maxpool(hip, n, h, w, c, k, s, pads, relu, half):
+    """MaxPool (+ the folded Relu, PoolP.FuseRelu) as its own node (maxpool.comp, VkGraph.cs:705-717):
+    a max selects one of its inputs, so the result is bit-exact in both storage modes."""
+    x = img(33, (n, h, w, c), half)
+    pb = PlanBuilder()
+    xv = pb.input((n, c, h, w), NHWC, "x")
+    y = pb.max_pool(xv, (k, k), (s, s), pads, relu=relu, name="pool")
+    got = run(hip, pb.build(y), [x], half, "maxpool")
+    want = O.max_pool(x, (k, k), (s, s), pads, relu)
+    assert got.shape == want.shape
+    assert np.array_equal(got, f16(want) if half else want)
+
+
+@HALF
+@pytest.mark.parametrize("ic,oc,k,h,w,act,pool_relu", [
+    (3, 16, 3, 64, 48, "relu", False), (3, 32, 3, 31, 40, "none", True), (4, 8, 3, 20, 18, "relu", True),
+    (1, 16, 5, 24, 24, "none", False), (3, 64, 1, 16, 22, "relu", True)])
+def test_conv_pool_fused(hip, ic, oc, k, h, w, act, pool_relu, half):
+    """ConvP.Pool on a small-ic stem (the reference's GPU ConvPool, GraphCompiler.GpuSmallConv +
+    VkGraph.cs:559-575; Nhwc.ConvPool, Kernels/Nhwc.cs:661-727): one dispatch that never stores the
+    full-resolution conv, against the oracle's ConvPool. An odd conv height (31) floors the pool."""
+    x = img(35, (1, h, w, ic), half)
+    wt = synth.uniform(35, 2, (oc, ic, k, k), -0.5, 0.5)
+    wt = f16(wt) if half else wt
+    b = synth.uniform(35, 3, (oc,), -0.1, 0.1)
+    pb = PlanBuilder()
+    xv = pb.input((1, ic, h, w), NHWC, "x")
+    y = pb.conv(xv, wt, b, stride=1, pad=k // 2, act=act, pool="relu" if pool_relu else True, name="stem")
+    plan = pb.build(y)
+    g = hip.graph(plan, half)
+    names = [d[0] for d in g.dispatches]
+    fused = ic % (8 if half else 4) != 0 and h % 2 == 0 and w % 2 == 0  # else conv to scratch + pool pass
+    print(f"[gpu] convpool ic={ic} oc={oc} k={k} {h}x{w} f16={half} dispatches={names}", flush=True)
+    if fused:
+        assert names == ["convpool"], names
+    with HipInferenceSession(g) as s:
+        s.set_input(x)
+        got = s.run().copy()
+    want = O.conv(x, wt, b, stride=(1, 1), pads=(k // 2,) * 4, act=act, pool=True, pool_relu=pool_relu)
+    assert got.shape == want.shape == (1, h // 2, w // 2, oc)
+    assert max_rel(got, want) < TOL[half]

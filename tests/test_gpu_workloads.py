@@ -57,20 +57,18 @@ def test_dbnet_detector_fp32(hip):
 
 
 def test_dbnet_detector_fp16(hip):
-    """fp16 storage on this synthetic He-normal detector cannot reach 2e-2 against the fp32 CPU
-    reference: the same rounding applied on the CPU (oracle with f16_storage) already deviates
-    ~5e-2 (logits up to |72|, 39% of pixels on the sigmoid's steep part). The GPU must stay within
-    the reference's fp16 debug threshold (6e-2, VkDebugTests.cs) and within 1.25x of that inherent
-    contract error; the mean error must stay at fp16 level."""
+    """The fp16 detector (the benchmarked one) within 2e-2 of the fp32 CPU reference, and within 2e-2
+    of the CPU's emulation of the fp16 storage contract (the same roundings at the same points; it
+    pins the kernels to the contract rather than to the tolerance)."""
     plan, ins = graphs.dbnet()
     got = run_gpu(hip, plan, ins, True)
     want = run_plan(plan, ins)
     emu = run_plan(plan, ins, f16_storage=True)
-    inherent = max_rel(emu, want)
-    err = max_rel(got, want)
-    print(f"[gpu] detector fp16 max-rel {err:.4f}, CPU fp16-contract emulation {inherent:.4f}", flush=True)
-    assert err <= 6e-2 and err <= max(2e-2, 1.25 * inherent)
-    assert float(np.abs(got - want).mean()) <= 2e-3
+    err, err_emu = max_rel(got, want), max_rel(got, emu)
+    print(f"[gpu] detector fp16 max-rel {err:.4f} vs fp32, {err_emu:.4f} vs the fp16-contract emulation", flush=True)
+    assert got.shape == (1, 960, 960, 1)
+    assert err <= 2e-2
+    assert err_emu <= 2e-2
 
 
 def test_svtr_recognizer_fp16(hip):

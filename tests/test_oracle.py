@@ -176,3 +176,31 @@ def test_activation_kinds_closed_forms():
     for act, w in want.items():
         got = O.activation(x, act).astype(np.float64)
         assert np.max(np.abs(got - w)) <= 4e-6 * max(1.0, np.max(np.abs(w))), act
+
+
+def test_bn_calibration_normalises_preactivations():
+    """The committed BatchNorm folds of configs 3 / 4 (simdonnx_amd/data/bn_calibration.npz, from
+    tests/golden/make_bn_calibration.py) do what they claim: at the calibration size every conv's
+    pre-activation channels have mean ~0 and std ~1 (bar the epsilon-floored near-constant ones), and
+    the fp16 storage contract emulated on the CPU stays within the 2e-2 bar of the fp32 detector."""
+    import sys
+    sys.path.insert(0, os.path.join(os.path.dirname(__file__), "golden"))
+    import make_bn_calibration as M
+    from oracle.interp import run_plan
+    from simdonnx_amd import graphs
+    for build in (lambda: graphs.mobilenetv3_small(size=640), lambda: graphs.dbnet(size=960, logit=True)):
+        plan, ins = build()
+        _, env = run_plan(plan, ins, keep=True)
+        stds = []
+        for nd in plan.nodes:
+            if nd.op in ("Conv", "ConvTranspose"):
+                y = M.preactivation(plan, env, nd).astype(np.float64)
+                y = y.reshape(-1, y.shape[-1])
+                assert np.abs(y.mean(axis=0)).max() < 2e-3, nd.name
+                stds.append(y.std(axis=0))
+        stds = np.concatenate(stds)
+        assert np.abs(stds - 1.0).max() < 2e-3 or (np.abs(stds - 1.0) > 2e-3).mean() < 0.02
+    plan, ins = graphs.dbnet()
+    want = run_plan(plan, ins)
+    emu = run_plan(plan, ins, f16_storage=True)
+    assert max_rel(emu, want) < 2e-2

@@ -139,3 +139,30 @@ def test_pixels_tensor_round_trip_and_channel_order():
     # ToByte rounds half up and clamps: 0.5/255 -> 1 (0.5 + 0.5), -0.1 -> 0, 1.2 -> 255
     t = np.array([[[0.5 / 255, -0.1, 1.2]]], np.float32)
     assert O.to_pixels(t, 1, 1, 3, 0).tolist() == [[1, 0, 255]]
+
+
+@pytest.mark.parametrize("k,s,pads,relu", [((2, 2), (2, 2), (0, 0, 0, 0), False), ((3, 3), (2, 2), (1, 1, 1, 1), True),
+                                           ((3, 3), (1, 1), (1, 1, 1, 1), False), ((2, 3), (2, 1), (0, 1, 1, 1), True)])
+def test_max_pool_matches_torch(k, s, pads, relu):
+    """Nhwc.MaxPool against torch's max_pool2d in float64 over an explicit -inf padding (taps outside
+    the image never win), then the fused relu."""
+    import torch
+    x = np.random.default_rng(5).standard_normal((2, 13, 11, 24)).astype(np.float32)
+    got = O.max_pool(x, k, s, pads, relu)
+    t = torch.from_numpy(x.astype(np.float64)).permute(0, 3, 1, 2)
+    t = torch.nn.functional.pad(t, (pads[1], pads[3], pads[0], pads[2]), value=float("-inf"))
+    want = torch.nn.functional.max_pool2d(t, k, s).permute(0, 2, 3, 1).numpy()
+    if relu:
+        want = np.maximum(want, 0.0)
+    assert got.shape == want.shape
+    assert np.array_equal(got, want.astype(np.float32))  # a max selects one of its inputs
+
+
+def test_max_pool_empty_window_is_zero():
+    """A window lying wholly in the padding outputs 0 (Nhwc.cs:765), not -inf: a 1x1 pool with pad 1
+    gives a zero border around the (relu'd) image, checked element by element."""
+    x = np.random.default_rng(6).standard_normal((1, 4, 5, 3)).astype(np.float32)
+    got = O.max_pool(x, (1, 1), (1, 1), (1, 1, 1, 1), relu=True)
+    want = np.zeros((1, 6, 7, 3), np.float32)
+    want[:, 1:5, 1:6] = np.maximum(x, 0.0)
+    assert np.array_equal(got, want)
