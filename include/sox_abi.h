@@ -336,6 +336,7 @@ typedef struct sox_ctc_args {
     const void* w;      /* weights fp16 [columns][ldw], the inner values of a column contiguous */
     const float* bias;  /* [columns] when has_bias */
     float* part;        /* [splits][rows][3]: max, sum (NaN: a non-finite logit), argmax (int bits) */
+    int32_t* status;    /* cleared to 0 by workgroup (0, 0) (pass 2 sets it on a non-finite logit) */
     int32_t rows, inner, columns, ldw, cols_per_split, has_bias;
 } sox_ctc_args;
 

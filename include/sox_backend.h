@@ -222,6 +222,17 @@ int sox_ctc_is_fused(sox_ctc* ctc);
  * it in the arena), or too many rows. */
 int sox_ctc_argmax(sox_ctc* ctc, sox_session* session, int32_t feature_value, int32_t batch, int32_t rows,
                    int32_t* indices, float* probabilities);
+/* No counterpart in the reference: sox_ctc_argmax for callers that cannot allocate (code under HIP
+ * graph capture, a serving loop, a harness that forbids hipMalloc). The same kernels on the same
+ * checks, but no allocation, no copy home and no wait: the work is enqueued on the session's stream
+ * and d_indices / d_probabilities (device arrays of batch * rows) and *d_status (device int32: 0, or
+ * 1 for a non-finite logit, the reference's "Recognizer output is invalid.") are written when the
+ * stream gets there. The column-range partials (column ranges x batch x rows x 12 bytes) go to the
+ * GPU's static scratch (sox_scratch, SOX_SCRATCH_BYTES); a larger call returns SOX_E_INVALID.
+ * Every call on one GPU shares that scratch: calls that overlap on one GPU (other streams, other
+ * threads) race. */
+int sox_ctc_argmax_noalloc(sox_ctc* ctc, sox_session* session, int32_t feature_value, int32_t batch, int32_t rows,
+                           int32_t* d_indices, float* d_probabilities, int32_t* d_status);
 
 /* ---- image session (VkImageSession, Backends/Vulkan/VkImageSession.cs:7-297) ----
  * Image-to-image inference with the pixel conversions on the device, in the same stream as the model:

@@ -91,6 +91,15 @@ int sox_graph_end(void* stream, void** graph_exec);
 int sox_graph_launch(void* graph_exec, void* stream);
 int sox_graph_destroy(void* graph_exec);
 
+/* Device scratch of the allocation-free entry points (no counterpart in the reference: it serves
+ * callers that cannot allocate, such as code under HIP graph capture or a serving loop). Every GPU
+ * holds one static array of SOX_SCRATCH_BYTES bytes from its first use until the process ends;
+ * sox_scratch returns this device's copy (device = the current device; call it once per device, e.g.
+ * at initialisation) and its size. Kernels get the address as an argument; every user of a GPU shares
+ * that GPU's array, so calls that use it concurrently on one GPU race. */
+#define SOX_SCRATCH_BYTES (8u << 20)
+int sox_scratch(int device, void** ptr, size_t* bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -111,8 +111,14 @@ def build_libs(verbose=False):
     common = ["-O2", "-fPIC", "-std=c++17", "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", "-Wall",
               "-Wno-unused-result"]
     thin = os.path.join(LIB, "libsoxhip.so")
-    _run([cxx, *common, "-shared", "-o", thin, os.path.join(HDIR, "sox_hip.cpp"), f"-L{ROCM}/lib", "-lamdhip64",
-          f"-Wl,-rpath,{ROCM}/lib"])
+    # the static device scratch (sox_scratch.hip) is the one host-library source compiled as HIP: its
+    # array needs the device code object the HIP runtime registers with the library
+    os.makedirs(BUILD, exist_ok=True)
+    scratch_o = os.path.join(BUILD, "sox_scratch.o")
+    _run([_hipcc(), "-c", "-fPIC", f"--offload-arch={ARCH}", *HIP_FLAGS, "-o", scratch_o,
+          os.path.join(HDIR, "sox_scratch.hip")])
+    _run([cxx, *common, "-shared", "-o", thin, os.path.join(HDIR, "sox_hip.cpp"), scratch_o, f"-L{ROCM}/lib",
+          "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib"])
     be = os.path.join(LIB, "libsoxbackend.so")
     _run([cxx, *common, f"-I{BUILD}", "-shared", "-o", be, os.path.join(HDIR, "backend.cpp"),
           os.path.join(BUILD, "resources.S"), f"-L{LIB}", "-lsoxhip", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{ROCM}/lib"])

@@ -13,7 +13,7 @@
 // (max, sum, argmax) of this column range goes to part[split][row].
 // Pass 2 (sox_ctc_merge): per row (one wave) the splits merge in a butterfly (ties keep the lower column);
 // probability = min(1, 1 / sum). A non-finite logit anywhere sets *status (the reference throws
-// "Recognizer output is invalid.").
+// "Recognizer output is invalid."), which pass 1 cleared.
 #include "sox_device.h"
 
 SOX_DEV void ctc_fold(float& m, float& s, int& idx, float m2, float s2, int i2) {
@@ -45,6 +45,7 @@ __device__ __forceinline__ void ctc_part_body(const sox_ctc_args& p) {
     const int ncols = c_end - c_beg;
     const half_t* __restrict__ X = (const half_t*)p.x;
     const half_t* __restrict__ W = (const half_t*)p.w;
+    if (blockIdx.x == 0 && blockIdx.y == 0 && t == 0) *p.status = 0;  // pass 2 runs after every pass-1 store
 
     // every W column of the range global -> LDS at once: 1 KiB DMA instructions dealt round-robin to
     // the 8 waves; lane l of instruction i fills bytes i * 1024 + 16 l = column n, slot j, which

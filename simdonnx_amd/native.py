@@ -174,6 +174,7 @@ THIN_API = {
     "sox_graph_end": (c_int32, [c_void_p, ctypes.POINTER(c_void_p)]),
     "sox_graph_launch": (c_int32, [c_void_p, c_void_p]),
     "sox_graph_destroy": (c_int32, [c_void_p]),
+    "sox_scratch": (c_int32, [c_int32, ctypes.POINTER(c_void_p), ctypes.POINTER(c_size_t)]),
 }
 
 BACKEND_API = {
@@ -248,6 +249,8 @@ BACKEND_API = {
     "sox_ctc_destroy": (None, [c_void_p]),
     "sox_ctc_is_fused": (c_int32, [c_void_p]),
     "sox_ctc_argmax": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p]),
+    "sox_ctc_argmax_noalloc": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p,
+                                         c_void_p]),
 }
 
 _thin = None
