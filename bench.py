@@ -13,6 +13,9 @@ Also reported on the same line:
                 its HBM traffic per launch from the committed rocprofv3 counter summary
   cpu_baseline  the CPU oracle (a C++ restatement of the reference's AVX-512/AVX2 Gemm micro-kernel
                 + GELU epilogue) on the same workload, all host cores
+  gemm_bf16     the same Gemm with bf16 storage (bf16 matrix cores, fp32 accumulation)
+  detector / detector_fp32 / recognizer / recognizer_bf16 / mobilenetv3
+                ms per image of the whole networks (HIP-graph replay), per-kernel-class roofline
   conv3x3       the fp32 Conv3x3 + bias + ReLU 1x64x64x64 kernel (us, TFLOP/s)
   ops           the kernels of the rest of the ExecOp surface (resize, pad, transpose, slice, unary,
                 depth-space, pools, MatMul) at detector / recognizer sizes, GB/s vs the HBM peak
@@ -55,7 +58,7 @@ def traffic_from_profiles(workload: str):
     return d.get("bytes_per_launch")
 
 
-def bench_gemm(steps: int, warmup: int):
+def bench_gemm(steps: int, warmup: int, storage="f16"):
     from simdonnx_amd import graphs
     from simdonnx_amd.backend import HipBackend, HipInferenceSession
     from simdonnx_amd import native as N
@@ -63,7 +66,7 @@ def bench_gemm(steps: int, warmup: int):
     hip = HipBackend.default()
     plan, ins = graphs.matmul_bias_gelu()
     flops = graphs.matmul_flops()
-    g = hip.graph(plan, True)
+    g = hip.graph(plan, storage)
     names = [d[0] for d in g.dispatches]
     with HipInferenceSession(g) as s:
         s.set_input(ins[0])
@@ -106,6 +109,7 @@ NETWORKS = {
     "detector_fp32": ("dbnet", "DBNet-style detector (MobileNetV3-small + FPN + ConvT head), 1x3x960x960, fp32 "
                       "storage", 1, False),
     "recognizer": ("svtr", "SVTR-style recognizer, 32x3x48x320, fp16 storage", 32, True),
+    "recognizer_bf16": ("svtr", "SVTR-style recognizer, 32x3x48x320, bf16 storage", 32, "bf16"),
 }
 
 
@@ -134,7 +138,7 @@ def bench_network(key: str, steps: int, replay: bool = True):
         per_node.setdefault(node, [name, 0.0])[1] += t
     classes = {}
     tot_fl = tot_by = 0
-    peak = PEAK_FP16_TFLOPS if half else PEAK_FP32_TFLOPS
+    peak = PEAK_FP16_TFLOPS if half else PEAK_FP32_TFLOPS  # the bf16 dense peak equals fp16's
     for node, (name, t) in per_node.items():
         fl, by = graphs.node_cost(plan, plan.nodes[node], 2 if half else 4)
         tot_fl += fl
@@ -433,7 +437,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-replay", action="store_true",
                     help="launch network dispatches one by one instead of replaying a HIP graph (profiler runs)")
-    ap.add_argument("--only", choices=["gemm", "conv", "detector", "detector_fp32", "recognizer", "mobilenetv3", "copy", "ops",
+    ap.add_argument("--only", choices=["gemm", "gemm_bf16", "conv", "detector", "detector_fp32", "recognizer",
+                                       "recognizer_bf16", "mobilenetv3", "copy", "ops",
                                        "recognizer_ctc", "image", "runner"],
                     help="run one workload only (profiling runs); prints its own JSON line")
     args = ap.parse_args()
@@ -443,6 +448,7 @@ def main():
         sys.exit(2)
     if args.only:
         fn = {"gemm": lambda: bench_gemm(args.steps, args.warmup), "conv": lambda: bench_conv(args.steps),
+              "gemm_bf16": lambda: bench_gemm(args.steps, args.warmup, "bf16"),
               "copy": lambda: bench_copy(args.steps),
               "ops": lambda: {"ops": bench_ops(args.steps)},
               "recognizer_ctc": lambda: bench_recognizer_ctc(args.steps, not args.no_replay),
@@ -474,7 +480,16 @@ def main():
                      "frac": round(tflops / PEAK_FP16_TFLOPS, 4),
                      "traffic": traffic_from_profiles("matmul_bias_gelu")},
     }
-    for key in ("detector", "detector_fp32", "recognizer", "mobilenetv3"):
+    try:
+        rb = bench_gemm(max(args.steps // 4, 1), min(args.warmup, 500), "bf16")
+        tb = rb["flops"] / (rb["per_launch_ms"] * 1e-3) / 1e12
+        out["gemm_bf16"] = {"workload": "matmul_bias_gelu with bf16 storage (v_mfma_f32_32x32x16_bf16, fp32 accum)",
+                            "us_per_launch": round(rb["per_launch_ms"] * 1e3, 2), "tflop_s": round(tb, 2),
+                            "frac_of_peak": round(tb / PEAK_FP16_TFLOPS, 4), "dispatches": rb["dispatches"]}
+        log(f"gemm bf16: {rb['per_launch_ms']*1e3:.1f} us/launch, {tb:.1f} TFLOP/s")
+    except Exception as e:
+        out["gemm_bf16"] = {"error": repr(e)}
+    for key in ("detector", "detector_fp32", "recognizer", "recognizer_bf16", "mobilenetv3"):
         try:
             out[key] = bench_network(key, 200, not args.no_replay)
             log(f"{key}: {out[key]['ms_per_image']} ms/image")

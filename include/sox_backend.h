@@ -159,11 +159,14 @@ int sox_graph_node_info(sox_graph* graph, int32_t node, int32_t* op, const void*
 int sox_graph_node_values(sox_graph* graph, int32_t node, int32_t* in, int32_t in_cap, int32_t* nin, int32_t* out,
                           int32_t out_cap, int32_t* nout);
 int sox_graph_value_shape(sox_graph* graph, int32_t value, int32_t* phys_shape, int32_t cap, int32_t* rank);
-int sox_graph_is_f16(sox_graph* graph);
+int sox_graph_is_f16(sox_graph* graph); /* the storage mode: SOX_STORAGE_F32 / _F16 / _BF16 (0 / 1 / 2) */
 
 /* ---- graph model (VkGraphModel) ---- */
-/* Builds the dispatch list of a plan: f16 = fp16 activation/weight storage with fp32 math (the
- * reference GPU contract, Backends/Vulkan/VkGraph.cs:33-43), else fp32 storage. */
+/* Builds the dispatch list of a plan. f16 = the storage mode: SOX_STORAGE_F16 (1) = fp16 activation /
+ * weight storage with fp32 math (the reference GPU contract, Backends/Vulkan/VkGraph.cs:33-43),
+ * SOX_STORAGE_BF16 (2) = the same with bfloat16 storage (rounded to nearest even; bf16 matrix-core
+ * instructions with fp32 accumulation; no reference counterpart), SOX_STORAGE_F32 (0) = fp32. */
+enum { SOX_STORAGE_F32 = 0, SOX_STORAGE_F16 = 1, SOX_STORAGE_BF16 = 2 };
 int sox_graph_create(sox_backend* backend, const sox_plan* plan, int32_t f16, sox_graph** graph);
 void sox_graph_release(sox_graph* graph);
 int sox_graph_dispatch_count(sox_graph* graph);

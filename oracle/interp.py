@@ -42,17 +42,27 @@ def _f16(a):
     return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
 
 
+def _bf16(a):
+    """IEEE fp32 -> bfloat16 round to nearest even -> fp32 (the bf16 storage contract)."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = np.where(nan, u | 0x400000, r)
+    return (r & 0xFFFFFFFF).astype(np.uint32).view(np.float32).reshape(np.shape(a))
+
+
 def run_plan(plan, inputs, keep=False, f16_storage=False):
     """Returns the output (physical layout); with keep=True also the dict of every value.
 
     f16_storage=True applies the reference GPU numeric contract on the CPU: graph inputs, weights
     and every stored activation are rounded to IEEE fp16 (round to nearest even) at the points the
     GPU stores them (Backends/Vulkan/VkGraph.cs:33-43, Engine/Extensions.cs:311-316), while bias /
-    norm / SE parameters stay fp32 and all math stays fp32."""
+    norm / SE parameters stay fp32 and all math stays fp32. f16_storage="bf16" rounds to bfloat16
+    at the same points instead (the bf16 graph mode)."""
     env = {}
     vals = plan.values
     keep32 = f32_params(plan) if f16_storage else set()
-    rnd = _f16 if f16_storage else (lambda a: a)
+    rnd = _bf16 if f16_storage == "bf16" else _f16 if f16_storage else (lambda a: a)
     consts = {}
 
     def get(vid):
@@ -60,7 +70,7 @@ def run_plan(plan, inputs, keep=False, f16_storage=False):
         if v.is_const:
             if f16_storage and vid not in keep32:
                 if vid not in consts:
-                    consts[vid] = _f16(v.data)
+                    consts[vid] = rnd(v.data)
                 return consts[vid]
             return v.data
         if vid in env:

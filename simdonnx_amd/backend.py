@@ -16,6 +16,16 @@ from . import native as N
 from .plan import ExecPlan
 
 
+STORAGE = {"f32": 0, "f16": 1, "bf16": 2}  # SOX_STORAGE_* of include/sox_backend.h
+
+
+def storage_mode(f16) -> int:
+    """The storage mode of a graph: True / "f16" = fp16, "bf16" = bfloat16, False / "f32" = fp32."""
+    if isinstance(f16, str):
+        return STORAGE[f16]
+    return STORAGE["f16"] if f16 else STORAGE["f32"]
+
+
 class GpuDeviceInfo:
     """GpuDeviceInfo (Backends/GpuDeviceInfo.cs:12-20)."""
 
@@ -74,10 +84,11 @@ class HipBackend:
         builds a new backend."""
         N.thin().sox_device_mark_lost()
 
-    def graph(self, plan: ExecPlan, f16: bool = True) -> "HipGraphModel":
+    def graph(self, plan: ExecPlan, f16=True) -> "HipGraphModel":
+        """f16: True / "f16" (fp16 storage), "bf16" (bfloat16 storage) or False / "f32"."""
         return HipGraphModel(self, plan, f16)
 
-    def new_session(self, plan: ExecPlan, f16: bool = True) -> "HipInferenceSession":
+    def new_session(self, plan: ExecPlan, f16=True) -> "HipInferenceSession":
         """NewSession(model, shape, opt) (VkBackend.cs:238-243) for an already compiled plan."""
         g = self.graph(plan, f16)
         s = HipInferenceSession(g)
@@ -124,7 +135,13 @@ class HipGraphView:
 
     @property
     def f16(self) -> bool:
+        """16-bit storage (fp16 or bf16)."""
         return bool(N.backend().sox_graph_is_f16(self.h))
+
+    @property
+    def storage(self) -> str:
+        """"f32", "f16" or "bf16" (sox_graph_is_f16's storage mode)."""
+        return {v: k for k, v in STORAGE.items()}[N.backend().sox_graph_is_f16(self.h)]
 
     def bind(self, value: int, kind="raw") -> N.Bind:
         b = N.Bind()
@@ -167,14 +184,14 @@ class HipGraphView:
 class HipGraphModel:
     """VkGraphModel analogue: packed consts + the dispatch list of one plan."""
 
-    def __init__(self, backend: HipBackend, plan: ExecPlan, f16: bool = True):
+    def __init__(self, backend: HipBackend, plan: ExecPlan, f16=True):
         self.backend = backend
         self.plan = plan
         self.f16 = f16
         ph = plan.to_native()
         try:
             h = N.c_void_p()
-            N.check(N.backend().sox_graph_create(backend.h, ph, int(f16), ctypes.byref(h)), "HipGraphModel")
+            N.check(N.backend().sox_graph_create(backend.h, ph, storage_mode(f16), ctypes.byref(h)), "HipGraphModel")
             self.h = h
         finally:
             N.backend().sox_plan_destroy(ph)

@@ -50,7 +50,9 @@ def _run(cmd):
 
 def build_code_objects(verbose=False):
     os.makedirs(BUILD, exist_ok=True)
-    srcs = sorted(f for f in os.listdir(KDIR) if f.endswith(".hip"))
+    # the large ring instantiations first, so the parallel build ends with the short files
+    srcs = sorted((f for f in os.listdir(KDIR) if f.endswith(".hip")),
+                  key=lambda f: (-os.path.getsize(os.path.join(KDIR, f)) if f.startswith(("gemm", "conv_ring")) else 0, f))
     hipcc = _hipcc()
 
     def one(src):
@@ -62,8 +64,8 @@ def build_code_objects(verbose=False):
             print("built", out, os.path.getsize(out), "bytes", flush=True)
         return name, out
 
-    with ThreadPoolExecutor(max_workers=min(4, len(srcs))) as ex:
-        return list(ex.map(one, srcs))
+    with ThreadPoolExecutor(max_workers=min(max(2, (os.cpu_count() or 4)), 8, len(srcs))) as ex:
+        return sorted(ex.map(one, srcs))
 
 
 def build_ext_examples(verbose=False):

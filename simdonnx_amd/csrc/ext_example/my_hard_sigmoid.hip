@@ -20,12 +20,19 @@ __device__ __forceinline__ float my_hsig(float v, float alpha, float beta) {
     return fminf(fmaxf(v * alpha + beta, 0.0f), 1.0f);
 }
 
-// fp16 graphs store activations as fp16; the math is fp32 (the reference GPU contract)
+// fp16 / bf16 graphs store activations as 16-bit floats; the math is fp32 (the reference GPU contract)
 extern "C" __global__ void __launch_bounds__(256) my_hsig_f16(my_hsig_args a) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= a.count) return;
     const _Float16 v = ((const _Float16*)a.x)[i];
     ((_Float16*)a.y)[i] = (_Float16)my_hsig((float)v, a.alpha, a.beta);
+}
+
+extern "C" __global__ void __launch_bounds__(256) my_hsig_bf16(my_hsig_args a) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= a.count) return;
+    const __bf16 v = ((const __bf16*)a.x)[i];
+    ((__bf16*)a.y)[i] = (__bf16)my_hsig((float)v, a.alpha, a.beta);
 }
 
 extern "C" __global__ void __launch_bounds__(256) my_hsig_f32(my_hsig_args a) {

@@ -2,13 +2,13 @@
 #include "gemm_ring.h"
 
 // implicit-GEMM Conv2d on the same ring (fp16 NHWC, ic % 8 == 0, constant-0 or reflect padding)
-SOX_CONV(sox_conv_f16_128x32_k32s4, 128, 32, 32, 32, 32, 4, 4, 2, 4)
-SOX_CONV(sox_conv_f16_64x64_k32s4, 64, 64, 32, 32, 32, 4, 4, 2, 4)
-SOX_CONV(sox_conv_f16_128x64_k32s4, 128, 64, 32, 64, 32, 4, 4, 2, 4)
-SOX_CONV(sox_conv_f16_128x128_k32s4, 128, 128, 32, 64, 64, 4, 4, 2, 4)
-SOX_CONV(sox_conv_f16_64x64_k64s4, 64, 64, 64, 32, 32, 4, 4, 2, 4)
-SOX_CONV(sox_conv_f16_128x64_k64s3, 128, 64, 64, 64, 32, 3, 4, 1, 4)
+SOX_CONV(sox_conv_f16_128x32_k32s4, half_t, 128, 32, 32, 32, 32, 4, 4, 2, 4)
+SOX_CONV(sox_conv_f16_64x64_k32s4, half_t, 64, 64, 32, 32, 32, 4, 4, 2, 4)
+SOX_CONV(sox_conv_f16_128x64_k32s4, half_t, 128, 64, 32, 64, 32, 4, 4, 2, 4)
+SOX_CONV(sox_conv_f16_128x128_k32s4, half_t, 128, 128, 32, 64, 64, 4, 4, 2, 4)
+SOX_CONV(sox_conv_f16_64x64_k64s4, half_t, 64, 64, 64, 32, 32, 4, 4, 2, 4)
+SOX_CONV(sox_conv_f16_128x64_k64s3, half_t, 128, 64, 64, 64, 32, 3, 4, 1, 4)
 // deep K (3x3 convs over many channels): more slices in flight per workgroup
-SOX_CONV(sox_conv_f16_128x32_k64s6, 128, 32, 64, 32, 32, 6, 4, 1, 4)
-SOX_CONV(sox_conv_f16_64x64_k64s8, 64, 64, 64, 32, 32, 8, 4, 1, 4)
-SOX_CONV(sox_conv_f16_128x64_k64s5, 128, 64, 64, 64, 32, 5, 4, 1, 4)
+SOX_CONV(sox_conv_f16_128x32_k64s6, half_t, 128, 32, 64, 32, 32, 6, 4, 1, 4)
+SOX_CONV(sox_conv_f16_64x64_k64s8, half_t, 64, 64, 64, 32, 32, 8, 4, 1, 4)
+SOX_CONV(sox_conv_f16_128x64_k64s5, half_t, 128, 64, 64, 64, 32, 5, 4, 1, 4)

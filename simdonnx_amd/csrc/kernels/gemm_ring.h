@@ -64,10 +64,11 @@ struct ConvtOut {
     const float* bias;
 };
 
-template <int ACT, int TJ, int TI>
-SOX_DEV void store_tile(half_t* __restrict__ Y, const half_t* __restrict__ R, int ldy, int M, int N, int m0, int n0,
+template <typename T, int ACT, int TJ, int TI>
+SOX_DEV void store_tile(T* __restrict__ Y, const T* __restrict__ R, int ldy, int M, int N, int m0, int n0,
                         const float16v (&acc)[TJ][TI], int act = 0, bool convt = false, ConvtOut ctv = {},
                         bool pad_rows = false) {
+    typedef vec_t<T, 4> T4;
     const int lane = threadIdx.x & 63, l32 = lane & 31, hl = lane >> 5;
     // whole 4-element groups: rows of a multiple of 4 elements, or rows padded past the N tail
     const bool aligned = pad_rows ? (ldy & 3) == 0 : ((ldy | N) & 3) == 0;
@@ -86,12 +87,12 @@ SOX_DEV void store_tile(half_t* __restrict__ Y, const half_t* __restrict__ R, in
                     if (ct->oc % 4 == 0) {  // the group's four channels share one tap
                         if (n < N) {
                             const int t = n / ct->oc, o = n - t * ct->oc, dy = t / ct->kw, dx = t - dy * ct->kw;
-                            half4 h;
+                            T4 h;
                             static_for<0, 4>([&](auto ee) {
                                 constexpr int e = decltype(ee)::value;
-                                h[e] = (half_t)fin(acc[j][i][4 * q + e] + (ct->bias ? ct->bias[o + e] : 0.0f));
+                                h[e] = (T)fin(acc[j][i][4 * q + e] + (ct->bias ? ct->bias[o + e] : 0.0f));
                             });
-                            *(half4*)(Y + (base + (long)dy * ow + dx) * ct->oc + o) = h;
+                            *(T4*)(Y + (base + (long)dy * ow + dx) * ct->oc + o) = h;
                         }
                     } else {
                         static_for<0, 4>([&](auto ee) {
@@ -99,7 +100,7 @@ SOX_DEV void store_tile(half_t* __restrict__ Y, const half_t* __restrict__ R, in
                             if (n + e < N) {
                                 const int t = (n + e) / ct->oc, o = n + e - t * ct->oc, dy = t / ct->kw, dx = t - dy * ct->kw;
                                 Y[(base + (long)dy * ow + dx) * ct->oc + o] =
-                                    (half_t)fin(acc[j][i][4 * q + e] + (ct->bias ? ct->bias[o] : 0.0f));
+                                    (T)fin(acc[j][i][4 * q + e] + (ct->bias ? ct->bias[o] : 0.0f));
                             }
                         });
                     }
@@ -115,14 +116,14 @@ SOX_DEV void store_tile(half_t* __restrict__ Y, const half_t* __restrict__ R, in
         constexpr int j = decltype(ji)::value / TI, i = decltype(ji)::value % TI;
         const int m = m0 + i * 32 + l32;
         // residual (the next node's Add, fused): the block's four 8-byte groups load together
-        half4 rv[4];
+        T4 rv[4];
         if (R) {
             static_for<0, 4>([&](auto qq) {
                 constexpr int q = decltype(qq)::value;
                 const int n = n0 + j * 32 + 8 * q + 4 * hl;
                 const long o = (m < M && n < N) ? (long)m * ldy + n : 0;
                 if (aligned) {
-                    rv[q] = *(const half4*)(R + o);
+                    rv[q] = *(const T4*)(R + o);
                 } else {
 #pragma unroll
                     for (int e = 0; e < 4; e++) rv[q][e] = R[o + (n + e < N ? e : 0)];
@@ -136,17 +137,17 @@ SOX_DEV void store_tile(half_t* __restrict__ Y, const half_t* __restrict__ R, in
         static_for<0, 4>([&](auto qq) {
             constexpr int q = decltype(qq)::value;
             const int n = n0 + j * 32 + 8 * q + 4 * hl;
-            half4 h;
+            T4 h;
             static_for<0, 4>([&](auto ee) {
                 constexpr int e = decltype(ee)::value;
                 float v = acc[j][i][4 * q + e];
                 if (R) v += (float)rv[q][e];
-                h[e] = (half_t)(ACT == SOX_ACT_GELU ? gelu_fast(v) : ACT >= 0 ? sox_act(v, ACT) : act_fast(v, act));
+                h[e] = (T)(ACT == SOX_ACT_GELU ? gelu_fast(v) : ACT >= 0 ? sox_act(v, ACT) : act_fast(v, act));
             });
             if (m < M && n < N) {
-                half_t* yp = Y + (long)m * ldy + n;
+                T* yp = Y + (long)m * ldy + n;
                 if (aligned) {
-                    *(half4*)yp = h;  // 8-byte aligned rows, whole groups of 4
+                    *(T4*)yp = h;  // 8-byte aligned rows, whole groups of 4
                 } else {
 #pragma unroll
                     for (int e = 0; e < 4; e++)
@@ -165,9 +166,11 @@ SOX_DEV void store_tile(half_t* __restrict__ Y, const half_t* __restrict__ R, in
 // pieces. The staged rows hold 16-byte chunks XOR-swizzled
 // by row (slot = chunk ^ row % chunks), which spreads both the 8-byte writes (one row per lane) and
 // the 16-byte reads (one row per 8 lanes) evenly over the banks.
-template <int ACT, int TJ, int TI>
-SOX_DEV void store_tile_lds(half_t* __restrict__ Y, int ldy, int M, int N, int m0, int n0,
+template <typename T, int ACT, int TJ, int TI>
+SOX_DEV void store_tile_lds(T* __restrict__ Y, int ldy, int M, int N, int m0, int n0,
                             const float16v (&acc)[TJ][TI], int act, unsigned char* stg) {
+    typedef vec_t<T, 4> T4;
+    typedef vec_t<T, 8> T8;
     const int lane = threadIdx.x & 63, l32 = lane & 31, hl = lane >> 5;
     auto fin = [&](float a) { return ACT == SOX_ACT_GELU ? gelu_fast(a) : ACT >= 0 ? sox_act(a, ACT) : act_fast(a, act); };
     static_for<0, TI * ((TJ + 1) / 2)>([&](auto ip) {
@@ -177,19 +180,19 @@ SOX_DEV void store_tile_lds(half_t* __restrict__ Y, int ldy, int M, int N, int m
             constexpr int c = decltype(cc)::value, j = j0 + c / 4, q = c % 4;
             float4v f;
             static_for<0, 4>([&](auto ee) { f[decltype(ee)::value] = fin(acc[j][i][4 * q + decltype(ee)::value]); });
-            // a vector conversion: two v_cvt_pk_f16_f32 (round to nearest even) instead of four
-            // conversions and the packing moves
-            const half4 h = __builtin_convertvector(f, half4);
-            *(half4*)(stg + l32 * CH * 16 + ((c ^ (l32 % CH)) << 4) + hl * 8) = h;
+            // a vector conversion: two v_cvt_pk_f16_f32 / v_cvt_pk_bf16_f32 (round to nearest even)
+            // instead of four conversions and the packing moves
+            const T4 h = __builtin_convertvector(f, T4);
+            *(T4*)(stg + l32 * CH * 16 + ((c ^ (l32 % CH)) << 4) + hl * 8) = h;
         });
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // other lanes' rows are read back
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         static_for<0, CH / 2>([&](auto tt) {
             const int idx = decltype(tt)::value * 64 + lane, r = idx / CH, c = idx % CH;
-            const half8 v = *(const half8*)(stg + r * CH * 16 + ((c ^ (r % CH)) << 4));
+            const T8 v = *(const T8*)(stg + r * CH * 16 + ((c ^ (r % CH)) << 4));
             const int m = m0 + i * 32 + r, n = n0 + j0 * 32 + c * 8;
-            if (m < M && n < N) *(half8*)(Y + (long)m * ldy + n) = v;
+            if (m < M && n < N) *(T8*)(Y + (long)m * ldy + n) = v;
         });
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the next group overwrites the stage
         __builtin_amdgcn_wave_barrier();
@@ -211,9 +214,11 @@ constexpr int dma_chunk(int share) {
 // is its row's offset + the tap's offset + its channel. Channels past ic (the last block of a tap
 // when BK does not divide ic) and zero-padding taps are fetched from p.zeros; ic % 8 == 0. Rows past
 // M re-read row M - 1 (never stored).
-template <int BM, int BN, int BK, int WM, int WN, int STAGES, int NW, int GM, bool CONV = false, bool EPI_LDS = false,
-          bool LN = false>
+template <typename T, int BM, int BN, int BK, int WM, int WN, int STAGES, int NW, int GM, bool CONV = false,
+          bool EPI_LDS = false, bool LN = false>
 __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
+    typedef vec_t<T, 8> T8;
+    typedef vec_t<T, 2> T2;
     constexpr int CPR = BK / 8;                 // 16-byte chunks per LDS row
     constexpr int ROWB = BK * 2;                // LDS row bytes
     constexpr int KS = BK / 16;                 // MFMA k-steps per slice
@@ -244,11 +249,11 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
     const int M = p.m, N = p.n, K = p.k;
     const int tiles_n = p.tiles_n, tiles_m = (M + BM - 1) / BM, ntiles = tiles_m * tiles_n;
     const int wm0 = (wave / WAVES_N) * WM, wn0 = (wave % WAVES_N) * WN;
-    const half_t* __restrict__ A = (const half_t*)p.x;
-    const half_t* __restrict__ W = (const half_t*)p.w;
-    const half_t* __restrict__ Z = (const half_t*)p.zeros;
-    half_t* __restrict__ Y = (half_t*)p.y;
-    const half_t* __restrict__ R = (p.flags & SOX_F_RESIDUAL) ? (const half_t*)p.add : nullptr;  // [M][ldy]
+    const T* __restrict__ A = (const T*)p.x;
+    const T* __restrict__ W = (const T*)p.w;
+    const T* __restrict__ Z = (const T*)p.zeros;
+    T* __restrict__ Y = (T*)p.y;
+    const T* __restrict__ R = (p.flags & SOX_F_RESIDUAL) ? (const T*)p.add : nullptr;  // [M][ldy]
     const int act = (p.flags & SOX_F_ACT_MASK) >> SOX_F_ACT_SHIFT;
     static_assert(!LN || !CONV, "LayerNorm-folded A: dense Gemm only");
     // a ConvTranspose's bias is per output channel, added in its scatter epilogue, not per column;
@@ -277,10 +282,10 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
     // holds global chunk slot ^ swz(r). Rows past M / N re-read the last row (never stored).
     const bool a_lane = lane * 16 < CH_A, b_lane = lane * 16 < CH_B;
     int a_chunk[A_IT], b_chunk[B_IT];  // global chunk (k / 8 within the slice) of each instruction
-    const half_t* a_src[A_IT];         // dense A: row base + chunk; conv: image base of the row's batch
+    const T* a_src[A_IT];              // dense A: row base + chunk; conv: image base of the row's batch
     int a_iy0[A_IT], a_ix0[A_IT];      // conv: the row's receptive-field origin
     int a_off0[A_IT];                  // conv: (iy0 * iw + ix0) * ic, the origin's offset in its image
-    const half_t* b_src[B_IT];
+    const T* b_src[B_IT];
     const float* c_src;  // this lane's 4 bias floats (a duplicate A chunk when there is no bias)
 #pragma unroll
     for (int i = 0; i < A_IT; i++) {
@@ -324,8 +329,8 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
     // prep computes a slice's DMA sources (calling set_sources at a tile's first slice), fire issues
     // the DMAs.
     struct Src {
-        const half_t* a[A_IT];
-        const half_t* b[B_IT];
+        const T* a[A_IT];
+        const T* b[B_IT];
         const float* c;
     };
     auto prep = [&](int gs, Src& q) __attribute__((always_inline)) {
@@ -405,14 +410,14 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
     tile_origin(vid, bm_cur, bn_cur);
 
     float16v acc[TJ][TI];
-    half8 fa0[TI], fb0[TJ], fa1[TI], fb1[TJ];
+    T8 fa0[TI], fb0[TJ], fa1[TI], fb1[TJ];
     float ls1[TI], ls2[TI];  // LN: this lane's share of its rows' sum and sum of squares
-    auto read_step = [&](int gs, int s, half8 (&fa)[TI], half8 (&fb)[TJ]) __attribute__((always_inline)) {
+    auto read_step = [&](int gs, int s, T8 (&fa)[TI], T8 (&fb)[TJ]) __attribute__((always_inline)) {
         const unsigned char* st = smem + (gs % STAGES) * STAGE_BYTES;
 #pragma unroll
-        for (int j = 0; j < TJ; j++) fb[j] = *(const half8*)(st + (b_off[j] ^ (s << 5)));
+        for (int j = 0; j < TJ; j++) fb[j] = *(const T8*)(st + (b_off[j] ^ (s << 5)));
 #pragma unroll
-        for (int i = 0; i < TI; i++) fa[i] = *(const half8*)(st + (a_off[i] ^ (s << 5)));
+        for (int i = 0; i < TI; i++) fa[i] = *(const T8*)(st + (a_off[i] ^ (s << 5)));
     };
     // accumulators of a new tile = its bias (from the LDS stage of the tile's first slice)
     auto init_acc = [&](int gs) __attribute__((always_inline)) {
@@ -475,9 +480,9 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
             if (lds_ok) {
                 unsigned char* stg = smem + STAGE_BYTES * STAGES + wave * EPI_WAVE;
                 switch (act) {
-                case SOX_ACT_NONE: store_tile_lds<SOX_ACT_NONE>(Y, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, stg); break;
-                case SOX_ACT_GELU: store_tile_lds<SOX_ACT_GELU>(Y, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, stg); break;
-                default: store_tile_lds<-1>(Y, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, act, stg); break;
+                case SOX_ACT_NONE: store_tile_lds<T, SOX_ACT_NONE>(Y, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, stg); break;
+                case SOX_ACT_GELU: store_tile_lds<T, SOX_ACT_GELU>(Y, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, stg); break;
+                default: store_tile_lds<T, -1>(Y, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, act, stg); break;
                 }
                 if (gs + 1 < total) {
                     tile_origin(vid + (gs + 1) / nk * G, bm_cur, bn_cur);
@@ -487,10 +492,10 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
             }
         }
         switch (act) {
-        case SOX_ACT_NONE: store_tile<SOX_ACT_NONE>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, ctp, cto, pad_rows); break;
-        case SOX_ACT_RELU: store_tile<SOX_ACT_RELU>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, ctp, cto, pad_rows); break;
-        case SOX_ACT_GELU: store_tile<SOX_ACT_GELU>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, ctp, cto, pad_rows); break;
-        default: store_tile<-1>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, act, ctp, cto, pad_rows); break;
+        case SOX_ACT_NONE: store_tile<T, SOX_ACT_NONE>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, ctp, cto, pad_rows); break;
+        case SOX_ACT_RELU: store_tile<T, SOX_ACT_RELU>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, ctp, cto, pad_rows); break;
+        case SOX_ACT_GELU: store_tile<T, SOX_ACT_GELU>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, ctp, cto, pad_rows); break;
+        default: store_tile<T, -1>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, act, ctp, cto, pad_rows); break;
         }
         if (gs + 1 < total) {
             tile_origin(vid + (gs + 1) / nk * G, bm_cur, bn_cur);
@@ -507,10 +512,10 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
     for (int gs = 0; gs < total; gs++) {
         static_for<0, KS>([&](auto step) {
             constexpr int s = decltype(step)::value;
-            half8(&ca)[TI] = (s & 1) ? fa1 : fa0;
-            half8(&cb)[TJ] = (s & 1) ? fb1 : fb0;
-            half8(&na)[TI] = (s & 1) ? fa0 : fa1;
-            half8(&nb)[TJ] = (s & 1) ? fb0 : fb1;
+            T8(&ca)[TI] = (s & 1) ? fa1 : fa0;
+            T8(&cb)[TJ] = (s & 1) ? fb1 : fb0;
+            T8(&na)[TI] = (s & 1) ? fa0 : fa1;
+            T8(&nb)[TJ] = (s & 1) ? fb0 : fb1;
             if constexpr (s == KS - 1) {
                 // slice gs+1 landed (this wave's loads; later slices may stay in flight) and every read
                 // of slice gs done; after the barrier both hold for all waves
@@ -524,15 +529,20 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
             }
             static_for<0, TJ * TI>([&](auto ji) {
                 constexpr int j = decltype(ji)::value / TI, i = decltype(ji)::value % TI;
-                acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cb[j], ca[i], acc[j][i], 0, 0, 0);
+                acc[j][i] = mfma32x32x16(cb[j], ca[i], acc[j][i]);
             });
             if constexpr (LN) {  // the step's 8 values of each of the lane's rows, by fp32 dot2
-                const half2v one = {(half_t)1.0f, (half_t)1.0f};
+                const T2 one = {(T)1.0f, (T)1.0f};
                 static_for<0, TI * 4>([&](auto ih) {
                     constexpr int i = decltype(ih)::value / 4, h = decltype(ih)::value % 4;
-                    const half2v v = {ca[i][2 * h], ca[i][2 * h + 1]};
-                    ls1[i] = __builtin_amdgcn_fdot2(v, one, ls1[i], false);
-                    ls2[i] = __builtin_amdgcn_fdot2(v, v, ls2[i], false);
+                    const T2 v = {ca[i][2 * h], ca[i][2 * h + 1]};
+                    if constexpr (std::is_same<T, half_t>::value) {
+                        ls1[i] = __builtin_amdgcn_fdot2(v, one, ls1[i], false);
+                        ls2[i] = __builtin_amdgcn_fdot2(v, v, ls2[i], false);
+                    } else {
+                        ls1[i] = __builtin_amdgcn_fdot2_f32_bf16(v, one, ls1[i], false);
+                        ls2[i] = __builtin_amdgcn_fdot2_f32_bf16(v, v, ls2[i], false);
+                    }
                 });
             }
             // MFMA, read, MFMA, read, ...: this step's operands were read one step earlier, and the
@@ -552,22 +562,22 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
     wait_vmcnt<0>();  // the trailing (unused) slices land before the workgroup's LDS is released
 }
 
-#define SOX_GEMM(NAME, BM, BN, BK, WM, WN, ST, NW, OCC, GM)                                         \
+// T: the 16-bit storage type (half_t or bf16_t)
+#define SOX_GEMM(NAME, T, BM, BN, BK, WM, WN, ST, NW, OCC, GM)                                      \
     extern "C" __global__ void __launch_bounds__(64 * NW, OCC) NAME(sox_igemm_args p) {           \
-        gemm_body<BM, BN, BK, WM, WN, ST, NW, GM>(p);                                             \
+        gemm_body<T, BM, BN, BK, WM, WN, ST, NW, GM>(p);                                          \
     }
 // epilogue staged through LDS (store_tile_lds)
-#define SOX_GEMM_E(NAME, BM, BN, BK, WM, WN, ST, NW, OCC, GM)                                       \
+#define SOX_GEMM_E(NAME, T, BM, BN, BK, WM, WN, ST, NW, OCC, GM)                                    \
     extern "C" __global__ void __launch_bounds__(64 * NW, OCC) NAME(sox_igemm_args p) {           \
-        gemm_body<BM, BN, BK, WM, WN, ST, NW, GM, false, true>(p);                             \
+        gemm_body<T, BM, BN, BK, WM, WN, ST, NW, GM, false, true>(p);                             \
     }
 // A rows LayerNorm'ed on the fly (the LayerNorm folded into the Gemm); E = epilogue through LDS
-#define SOX_GEMM_LN(NAME, BM, BN, BK, WM, WN, ST, NW, OCC, GM, E)                                  \
+#define SOX_GEMM_LN(NAME, T, BM, BN, BK, WM, WN, ST, NW, OCC, GM, E)                               \
     extern "C" __global__ void __launch_bounds__(64 * NW, OCC) NAME(sox_igemm_args p) {           \
-        gemm_body<BM, BN, BK, WM, WN, ST, NW, GM, false, E, true>(p);                             \
+        gemm_body<T, BM, BN, BK, WM, WN, ST, NW, GM, false, E, true>(p);                          \
     }
-#define SOX_CONV(NAME, BM, BN, BK, WM, WN, ST, NW, OCC, GM)                                         \
+#define SOX_CONV(NAME, T, BM, BN, BK, WM, WN, ST, NW, OCC, GM)                                      \
     extern "C" __global__ void __launch_bounds__(64 * NW, OCC) NAME(sox_igemm_args p) {           \
-        gemm_body<BM, BN, BK, WM, WN, ST, NW, GM, true>(p);                                       \
+        gemm_body<T, BM, BN, BK, WM, WN, ST, NW, GM, true>(p);                                    \
     }
-

@@ -17,8 +17,10 @@
 // the same number of loads per block and one static vmcnt covers them.
 #include "gemm_ring.h"
 
-template <int KH, int KW, int SH, int SW>
+template <typename T, int KH, int KW, int SH, int SW>
 __device__ __forceinline__ void halo_body(const sox_igemm_args& p) {
+    typedef vec_t<T, 8> T8;
+    typedef vec_t<T, 4> T4;
     constexpr int TW = 16, TH = 8, CB = 32, PITCH = 5;
     constexpr int HW = (TW - 1) * SW + KW, HH = (TH - 1) * SH + KH, HP = HH * HW, TAPS = KH * KW;
     constexpr int HALO_IT = (HP * PITCH + 255) / 256, W_IT = (TAPS * 32 * PITCH + 255) / 256;
@@ -36,14 +38,14 @@ __device__ __forceinline__ void halo_body(const sox_igemm_args& p) {
     const int n0 = blockIdx.y * 32;
     const int oy0 = ty * TH, ox0 = tx * TW;
     const int iy0 = oy0 * SH - p.pt, ix0 = ox0 * SW - p.pl;
-    const half_t* __restrict__ X = (const half_t*)p.x + (long)b * p.ih * p.iw * p.ic;
-    const half_t* __restrict__ W = (const half_t*)p.w;
-    const half_t* __restrict__ Z = (const half_t*)p.zeros;
+    const T* __restrict__ X = (const T*)p.x + (long)b * p.ih * p.iw * p.ic;
+    const T* __restrict__ W = (const T*)p.w;
+    const T* __restrict__ Z = (const T*)p.zeros;
     const int ncb = (p.ic + CB - 1) / CB;
 
     // this thread's DMA sources in channel block 0 (nullptr: the slot is padding and reads zeros);
     // block c adds c * CB channels, and a chunk past ic reads zeros too
-    const half_t* hsrc[HALO_IT];
+    const T* hsrc[HALO_IT];
     int hch[HALO_IT];
 #pragma unroll
     for (int i = 0; i < HALO_IT; i++) {
@@ -53,7 +55,7 @@ __device__ __forceinline__ void halo_body(const sox_igemm_args& p) {
         hsrc[i] = ok ? X + ((long)iy * p.iw + ix) * p.ic + sub * 8 : nullptr;
         hch[i] = sub * 8;
     }
-    const half_t* wsrc[W_IT];
+    const T* wsrc[W_IT];
     int wch[W_IT];
 #pragma unroll
     for (int i = 0; i < W_IT; i++) {
@@ -68,12 +70,12 @@ __device__ __forceinline__ void halo_body(const sox_igemm_args& p) {
         const int c0 = cb * CB;
 #pragma unroll
         for (int i = 0; i < HALO_IT; i++) {
-            const half_t* src = hsrc[i] && c0 + hch[i] < p.ic ? hsrc[i] + c0 : Z;
+            const T* src = hsrc[i] && c0 + hch[i] < p.ic ? hsrc[i] + c0 : Z;
             __builtin_amdgcn_global_load_lds(src, LDS_PTR(st + i * 256 * 16), 16, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < W_IT; i++) {
-            const half_t* src = wsrc[i] && c0 + wch[i] < p.ic ? wsrc[i] + c0 : Z;
+            const T* src = wsrc[i] && c0 + wch[i] < p.ic ? wsrc[i] + c0 : Z;
             __builtin_amdgcn_global_load_lds(src, LDS_PTR(st + (HALO_SLOTS + i * 256) * 16), 16, 0, 0);
         }
     };
@@ -101,9 +103,9 @@ __device__ __forceinline__ void halo_body(const sox_igemm_args& p) {
             constexpr int tap = decltype(ts)::value / 2, s = decltype(ts)::value % 2;
             constexpr int a_off = (((tap / KW) * HW + tap % KW) * PITCH + 2 * s) * 16;
             constexpr int b_off = (tap * 32 * PITCH + 2 * s) * 16;
-            const half8 wf = *(const half8*)(st + b_base + b_off);
-            const half8 af = *(const half8*)(st + a_base + a_off);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf, af, acc, 0, 0, 0);
+            const T8 wf = *(const T8*)(st + b_base + b_off);
+            const T8 af = *(const T8*)(st + a_base + a_off);
+            acc = mfma32x32x16(wf, af, acc);
         });
         wait_lgkmcnt0();
         __builtin_amdgcn_s_barrier();  // stage cb & 1 is refilled by the next iteration's issue
@@ -115,8 +117,8 @@ __device__ __forceinline__ void halo_body(const sox_igemm_args& p) {
     const long m = ((long)b * p.oh + oy) * p.ow + ox;
     if (m >= M) return;
     const int act = (p.flags & SOX_F_ACT_MASK) >> SOX_F_ACT_SHIFT;
-    const half_t* __restrict__ R = (p.flags & SOX_F_RESIDUAL) ? (const half_t*)p.add : nullptr;
-    half_t* __restrict__ Y = (half_t*)p.y + m * p.ldy;
+    const T* __restrict__ R = (p.flags & SOX_F_RESIDUAL) ? (const T*)p.add : nullptr;
+    T* __restrict__ Y = (T*)p.y + m * p.ldy;
     const bool aligned = ((p.ldy | N) & 3) == 0;
     static_for<0, 4>([&](auto qq) {
         constexpr int q = decltype(qq)::value;
@@ -130,21 +132,22 @@ __device__ __forceinline__ void halo_body(const sox_igemm_args& p) {
             v[e] = act_fast(v[e], act);
         }
         if (aligned) {
-            half4 h;
+            T4 h;
 #pragma unroll
-            for (int e = 0; e < 4; e++) h[e] = (half_t)v[e];
-            *(half4*)(Y + n) = h;
+            for (int e = 0; e < 4; e++) h[e] = (T)v[e];
+            *(T4*)(Y + n) = h;
         } else {
 #pragma unroll
             for (int e = 0; e < 4; e++)
-                if (n + e < N) Y[n + e] = (half_t)v[e];
+                if (n + e < N) Y[n + e] = (T)v[e];
         }
     });
 }
 
-#define SOX_HALO(NAME, KH, KW, SH, SW, OCC)                                                       \
+#define SOX_HALO(NAME, T, KH, KW, SH, SW, OCC)                                                    \
     extern "C" __global__ void __launch_bounds__(256, OCC) NAME(sox_igemm_args p) {            \
-        halo_body<KH, KW, SH, SW>(p);                                                          \
+        halo_body<T, KH, KW, SH, SW>(p);                                                       \
     }
 
-SOX_HALO(sox_conv_halo_f16_3x3s1, 3, 3, 1, 1, 2)
+SOX_HALO(sox_conv_halo_f16_3x3s1, half_t, 3, 3, 1, 1, 2)
+SOX_HALO(sox_conv_halo_bf16_3x3s1, bf16_t, 3, 3, 1, 1, 2)

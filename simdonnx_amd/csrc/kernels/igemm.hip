@@ -30,6 +30,15 @@ template <> struct Mfma<half_t> {
     }
 };
 
+template <> struct Mfma<bf16_t> {
+    static constexpr int KSTEP = 32;
+    static constexpr int KPL = 8;
+    typedef bf16x8 Frag;
+    SOX_DEV static float4v mma(Frag a, Frag b, float4v c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+};
+
 template <> struct Mfma<float> {
     static constexpr int KSTEP = 4;
     static constexpr int KPL = 1;
@@ -271,17 +280,30 @@ SOX_IGEMM(sox_igemm_f32_64x64_d, float, 64, 64, 32, 32, 32, A_DENSE)
 
 // fp16 storage, fp32 accumulation
 SOX_IGEMM(sox_igemm_f16_128x128_v, half_t, 128, 128, 64, 64, 32, A_IM2COL_VEC)
+SOX_IGEMM(sox_igemm_bf16_128x128_v, bf16_t, 128, 128, 64, 64, 32, A_IM2COL_VEC)
 SOX_IGEMM(sox_igemm_f16_128x128_s, half_t, 128, 128, 64, 64, 32, A_IM2COL_SCALAR)
+SOX_IGEMM(sox_igemm_bf16_128x128_s, bf16_t, 128, 128, 64, 64, 32, A_IM2COL_SCALAR)
 SOX_IGEMM(sox_igemm_f16_128x128_d, half_t, 128, 128, 64, 64, 32, A_DENSE)
+SOX_IGEMM(sox_igemm_bf16_128x128_d, bf16_t, 128, 128, 64, 64, 32, A_DENSE)
 SOX_IGEMM(sox_igemm_f16_64x64_v, half_t, 64, 64, 32, 32, 32, A_IM2COL_VEC)
+SOX_IGEMM(sox_igemm_bf16_64x64_v, bf16_t, 64, 64, 32, 32, 32, A_IM2COL_VEC)
 SOX_IGEMM(sox_igemm_f16_64x64_s, half_t, 64, 64, 32, 32, 32, A_IM2COL_SCALAR)
+SOX_IGEMM(sox_igemm_bf16_64x64_s, bf16_t, 64, 64, 32, 32, 32, A_IM2COL_SCALAR)
 SOX_IGEMM(sox_igemm_f16_64x64_d, half_t, 64, 64, 32, 32, 32, A_DENSE)
+SOX_IGEMM(sox_igemm_bf16_64x64_d, bf16_t, 64, 64, 32, 32, 32, A_DENSE)
 SOX_IGEMM(sox_igemm_f16_64x32_v, half_t, 64, 32, 32, 16, 32, A_IM2COL_VEC)
+SOX_IGEMM(sox_igemm_bf16_64x32_v, bf16_t, 64, 32, 32, 16, 32, A_IM2COL_VEC)
 SOX_IGEMM(sox_igemm_f16_64x32_s, half_t, 64, 32, 32, 16, 32, A_IM2COL_SCALAR)
+SOX_IGEMM(sox_igemm_bf16_64x32_s, bf16_t, 64, 32, 32, 16, 32, A_IM2COL_SCALAR)
 SOX_IGEMM(sox_igemm_f16_64x32_d, half_t, 64, 32, 32, 16, 32, A_DENSE)
+SOX_IGEMM(sox_igemm_bf16_64x32_d, bf16_t, 64, 32, 32, 16, 32, A_DENSE)
 // long-K variants (K = kh*kw*ic >= 128, e.g. 3x3 convs over 96 channels): 128-deep slices, a quarter
 // of the load round trips of the 32-deep ones
 SOX_IGEMM(sox_igemm_f16_64x64_vk, half_t, 64, 64, 32, 32, 128, A_IM2COL_VEC)
+SOX_IGEMM(sox_igemm_bf16_64x64_vk, bf16_t, 64, 64, 32, 32, 128, A_IM2COL_VEC)
 SOX_IGEMM(sox_igemm_f16_64x64_dk, half_t, 64, 64, 32, 32, 128, A_DENSE)
+SOX_IGEMM(sox_igemm_bf16_64x64_dk, bf16_t, 64, 64, 32, 32, 128, A_DENSE)
 SOX_IGEMM(sox_igemm_f16_64x32_vk, half_t, 64, 32, 32, 16, 128, A_IM2COL_VEC)
+SOX_IGEMM(sox_igemm_bf16_64x32_vk, bf16_t, 64, 32, 32, 16, 128, A_IM2COL_VEC)
 SOX_IGEMM(sox_igemm_f16_64x32_dk, half_t, 64, 32, 32, 16, 128, A_DENSE)
+SOX_IGEMM(sox_igemm_bf16_64x32_dk, bf16_t, 64, 32, 32, 16, 128, A_DENSE)

@@ -16,10 +16,15 @@
 //           its block loaded before the barrier, the hidden fragments read from LDS), then + b2 +
 //           residual, act2, fp16.
 // Rows past M re-read row M - 1 and are never stored.
+#include <type_traits>
+
 #include "sox_device.h"
 
-template <int KS1, int HB, int KS2>  // K1 / 16, H / 32, H / 16
+template <typename T, int KS1, int HB, int KS2>  // storage type, K1 / 16, H / 32, H / 16
 __device__ __forceinline__ void mlp_body(const sox_mlp_args& p) {
+    typedef vec_t<T, 8> T8;
+    typedef vec_t<T, 4> T4;
+    typedef vec_t<T, 2> T2;
     constexpr int H = HB * 32;
     constexpr int HROW = H * 2 + 16;  // LDS bytes per hidden row (16 bytes of padding: conflict-free reads)
     constexpr int PB1 = (HB + 7) / 8;  // hidden blocks per wave
@@ -27,32 +32,37 @@ __device__ __forceinline__ void mlp_body(const sox_mlp_args& p) {
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, l32 = lane & 31, hl = lane >> 5;
     const int m0 = blockIdx.x * 32;
     const int row = min(m0 + l32, p.m - 1);
-    const half_t* __restrict__ X = (const half_t*)p.x;
-    const half_t* __restrict__ W1 = (const half_t*)p.w1;
-    const half_t* __restrict__ W2 = (const half_t*)p.w2;
+    const T* __restrict__ X = (const T*)p.x;
+    const T* __restrict__ W1 = (const T*)p.w1;
+    const T* __restrict__ W2 = (const T*)p.w2;
 
     // ---- phase 1: hidden = GELU(rstd (x . W1 - mean c1) + b1) ----
-    half8 a[KS1];
+    T8 a[KS1];
 #pragma unroll
-    for (int s = 0; s < KS1; s++) a[s] = *(const half8*)(X + (long)row * p.k1 + 16 * s + 8 * hl);
-    half8 b[PB1][KS1];
+    for (int s = 0; s < KS1; s++) a[s] = *(const T8*)(X + (long)row * p.k1 + 16 * s + 8 * hl);
+    T8 b[PB1][KS1];
 #pragma unroll
     for (int i = 0; i < PB1; i++) {
         const int nb = min(wave + 8 * i, HB - 1);  // a wave past the last block re-reads it
 #pragma unroll
-        for (int s = 0; s < KS1; s++) b[i][s] = *(const half8*)(W1 + (((long)nb * KS1 + s) * 64 + lane) * 8);
+        for (int s = 0; s < KS1; s++) b[i][s] = *(const T8*)(W1 + (((long)nb * KS1 + s) * 64 + lane) * 8);
     }
     // the row's sum and sum of squares: this lane's k-half by fp32 dot2, then the other half's lane
     float s1 = 0.0f, s2 = 0.0f;
     {
-        const half2v one = {(half_t)1.0f, (half_t)1.0f};
+        const T2 one = {(T)1.0f, (T)1.0f};
 #pragma unroll
         for (int s = 0; s < KS1; s++)
 #pragma unroll
             for (int h = 0; h < 4; h++) {
-                const half2v v = {a[s][2 * h], a[s][2 * h + 1]};
-                s1 = __builtin_amdgcn_fdot2(v, one, s1, false);
-                s2 = __builtin_amdgcn_fdot2(v, v, s2, false);
+                const T2 v = {a[s][2 * h], a[s][2 * h + 1]};
+                if constexpr (std::is_same<T, half_t>::value) {
+                    s1 = __builtin_amdgcn_fdot2(v, one, s1, false);
+                    s2 = __builtin_amdgcn_fdot2(v, v, s2, false);
+                } else {
+                    s1 = __builtin_amdgcn_fdot2_f32_bf16(v, one, s1, false);
+                    s2 = __builtin_amdgcn_fdot2_f32_bf16(v, v, s2, false);
+                }
             }
         s1 += __shfl_xor(s1, 32);
         s2 += __shfl_xor(s2, 32);
@@ -67,7 +77,7 @@ __device__ __forceinline__ void mlp_body(const sox_mlp_args& p) {
 #pragma unroll
     for (int s = 0; s < KS1; s++)
 #pragma unroll
-        for (int i = 0; i < PB1; i++) acc1[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[i][s], a[s], acc1[i], 0, 0, 0);
+        for (int i = 0; i < PB1; i++) acc1[i] = mfma32x32x16(b[i][s], a[s], acc1[i]);
 #pragma unroll
     for (int i = 0; i < PB1; i++) {
         const int jb = wave + 8 * i;
@@ -78,21 +88,21 @@ __device__ __forceinline__ void mlp_body(const sox_mlp_args& p) {
             const int n = jb * 32 + 8 * q + 4 * hl;
             const float4v c4 = *(const float4v*)(p.c1 + n);
             const float4v b4 = *(const float4v*)(p.b1 + n);
-            half4 hv;
+            T4 hv;
 #pragma unroll
             for (int e = 0; e < 4; e++)
-                hv[e] = (half_t)gelu_fast(rstd * (acc[4 * q + e] - mean * c4[e]) + b4[e]);
-            *(half4*)(hs + l32 * HROW + n * 2) = hv;
+                hv[e] = (T)gelu_fast(rstd * (acc[4 * q + e] - mean * c4[e]) + b4[e]);
+            *(T4*)(hs + l32 * HROW + n * 2) = hv;
         }
     }
 
     // ---- phase 2: y = act2(hidden . W2 + b2 + r) ----
     const int ob = wave;  // output block of this wave (waves past N2 / 32 only help with phase 1)
     const bool out_wave = ob * 32 < p.n2;
-    half8 w2f[KS2];
+    T8 w2f[KS2];
     if (out_wave) {
 #pragma unroll
-        for (int s = 0; s < KS2; s++) w2f[s] = *(const half8*)(W2 + (((long)ob * KS2 + s) * 64 + lane) * 8);
+        for (int s = 0; s < KS2; s++) w2f[s] = *(const T8*)(W2 + (((long)ob * KS2 + s) * 64 + lane) * 8);
     }
     __syncthreads();  // every hidden column written
     if (!out_wave) return;
@@ -101,10 +111,10 @@ __device__ __forceinline__ void mlp_body(const sox_mlp_args& p) {
     const unsigned char* hr = hs + l32 * HROW + 16 * hl;
 #pragma unroll
     for (int s = 0; s < KS2; s += 2) {
-        const half8 hv = *(const half8*)(hr + 32 * s);
-        const half8 hv2 = *(const half8*)(hr + 32 * (s + 1));
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(w2f[s], hv, acc, 0, 0, 0);
-        acc_o = __builtin_amdgcn_mfma_f32_32x32x16_f16(w2f[s + 1], hv2, acc_o, 0, 0, 0);
+        const T8 hv = *(const T8*)(hr + 32 * s);
+        const T8 hv2 = *(const T8*)(hr + 32 * (s + 1));
+        acc = mfma32x32x16(w2f[s], hv, acc);
+        acc_o = mfma32x32x16(w2f[s + 1], hv2, acc_o);
     }
     acc += acc_o;
     const int m = m0 + l32;
@@ -114,23 +124,26 @@ __device__ __forceinline__ void mlp_body(const sox_mlp_args& p) {
     for (int q = 0; q < 4; q++) {
         const int n = ob * 32 + 8 * q + 4 * hl;
         const float4v b4 = (p.flags & 1) ? *(const float4v*)(p.b2 + n) : (float4v)0.0f;
-        half4 rv = {};
-        if (p.flags & 2) rv = *(const half4*)((const half_t*)p.res + (long)m * p.n2 + n);
-        half4 out;
+        T4 rv = {};
+        if (p.flags & 2) rv = *(const T4*)((const T*)p.res + (long)m * p.n2 + n);
+        T4 out;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             float v = acc[4 * q + e] + b4[e];
             if (p.flags & 2) v += (float)rv[e];
-            out[e] = (half_t)sox_act(v, act);
+            out[e] = (T)sox_act(v, act);
         }
-        *(half4*)((half_t*)p.y + (long)m * p.n2 + n) = out;
+        *(T4*)((T*)p.y + (long)m * p.n2 + n) = out;
     }
 }
 
 // name: K1 x H (inner dim x hidden width); N2 <= 256, a multiple of 32
 #define SOX_MLP(K1, H)                                                                                           \
     extern "C" __global__ void __launch_bounds__(512) sox_mlp_f16_k##K1##_h##H(sox_mlp_args p) {                 \
-        mlp_body<K1 / 16, H / 32, H / 16>(p);                                                                    \
+        mlp_body<half_t, K1 / 16, H / 32, H / 16>(p);                                                            \
+    }                                                                                                            \
+    extern "C" __global__ void __launch_bounds__(512) sox_mlp_bf16_k##K1##_h##H(sox_mlp_args p) {                \
+        mlp_body<bf16_t, K1 / 16, H / 32, H / 16>(p);                                                            \
     }
 SOX_MLP(192, 768)
 SOX_MLP(128, 512)

@@ -196,11 +196,15 @@ __device__ __forceinline__ void dw_body_k(const sox_dw_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_dw_f16_v3(sox_dw_args p) { dw_body_k<half_t, 8, 3>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_dw_bf16_v3(sox_dw_args p) { dw_body_k<bf16_t, 8, 3>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_dw_f16_v5(sox_dw_args p) { dw_body_k<half_t, 8, 5>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_dw_bf16_v5(sox_dw_args p) { dw_body_k<bf16_t, 8, 5>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_dw_f32_v3(sox_dw_args p) { dw_body_k<float, 4, 3>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_dw_f32_v5(sox_dw_args p) { dw_body_k<float, 4, 5>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_dw_f16_v(sox_dw_args p) { dw_body<half_t, 8>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_dw_bf16_v(sox_dw_args p) { dw_body<bf16_t, 8>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_dw_f16_s(sox_dw_args p) { dw_body<half_t, 1>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_dw_bf16_s(sox_dw_args p) { dw_body<bf16_t, 1>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_dw_f32_v(sox_dw_args p) { dw_body<float, 4>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_dw_f32_s(sox_dw_args p) { dw_body<float, 1>(p); }
 
@@ -235,6 +239,7 @@ __device__ __forceinline__ void convt_body(const sox_convt_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_convt_f16(sox_convt_args p) { convt_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_convt_bf16(sox_convt_args p) { convt_body<bf16_t>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_convt_f32(sox_convt_args p) { convt_body<float>(p); }
 
 // Pixel-major ConvTranspose for kh*kw <= 4 taps (the 2x2 stride-2 DBNet head): one work item = one
@@ -390,7 +395,9 @@ __device__ __forceinline__ void convt_one_body(const sox_convt_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_convt_pix_f16(sox_convt_args p) { convt_pix_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_convt_pix_bf16(sox_convt_args p) { convt_pix_body<bf16_t>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_convt_one_f16(sox_convt_args p) { convt_one_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_convt_one_bf16(sox_convt_args p) { convt_one_body<bf16_t>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_convt_one_f32(sox_convt_args p) { convt_one_body<float>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_convt_pix_f32(sox_convt_args p) { convt_pix_body<float>(p); }
 
@@ -454,7 +461,9 @@ __device__ __forceinline__ void gap_body(const sox_gap_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_gap_f16_v(sox_gap_args p) { gap_body<half_t, 8>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_gap_bf16_v(sox_gap_args p) { gap_body<bf16_t, 8>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_gap_f16_s(sox_gap_args p) { gap_body<half_t, 1>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_gap_bf16_s(sox_gap_args p) { gap_body<bf16_t, 1>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_gap_f32_v(sox_gap_args p) { gap_body<float, 4>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_gap_f32_s(sox_gap_args p) { gap_body<float, 1>(p); }
 
@@ -604,6 +613,7 @@ __device__ __forceinline__ void se_fc2_body(const sox_se_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_se_fc2_f16(sox_se_args p) { se_fc2_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_se_fc2_bf16(sox_se_args p) { se_fc2_body<bf16_t>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_se_fc2_f32(sox_se_args p) { se_fc2_body<float>(p); }
 
 // ------------------------------------------------------------------------------------------
@@ -632,7 +642,9 @@ __device__ __forceinline__ void chan_body(const sox_chan_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_chan_f16_v(sox_chan_args p) { chan_body<half_t, 8>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_chan_bf16_v(sox_chan_args p) { chan_body<bf16_t, 8>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_chan_f16_s(sox_chan_args p) { chan_body<half_t, 1>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_chan_bf16_s(sox_chan_args p) { chan_body<bf16_t, 1>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_chan_f32_v(sox_chan_args p) { chan_body<float, 4>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_chan_f32_s(sox_chan_args p) { chan_body<float, 1>(p); }
 
@@ -660,6 +672,7 @@ __device__ __forceinline__ void ew_body(const sox_ew_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_ew_f16(sox_ew_args p) { ew_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_ew_bf16(sox_ew_args p) { ew_body<bf16_t>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_ew_f32(sox_ew_args p) { ew_body<float>(p); }
 
 // ------------------------------------------------------------------------------------------
@@ -694,6 +707,7 @@ __device__ __forceinline__ void unary_body(const sox_unary_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_unary_f16(sox_unary_args p) { unary_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_unary_bf16(sox_unary_args p) { unary_body<bf16_t>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_unary_f32(sox_unary_args p) { unary_body<float>(p); }
 
 // ------------------------------------------------------------------------------------------
@@ -728,7 +742,9 @@ __device__ __forceinline__ void nearest_body(const sox_nearest_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_nearest_f16_v(sox_nearest_args p) { nearest_body<half_t, 8>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_nearest_bf16_v(sox_nearest_args p) { nearest_body<bf16_t, 8>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_nearest_f16_s(sox_nearest_args p) { nearest_body<half_t, 1>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_nearest_bf16_s(sox_nearest_args p) { nearest_body<bf16_t, 1>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_nearest_f32_v(sox_nearest_args p) { nearest_body<float, 4>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_nearest_f32_s(sox_nearest_args p) { nearest_body<float, 1>(p); }
 
@@ -747,40 +763,48 @@ __device__ __forceinline__ void slice_body(const sox_slice_copy_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_slice_f16_v(sox_slice_copy_args p) { slice_body<half_t, 8>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_slice_bf16_v(sox_slice_copy_args p) { slice_body<bf16_t, 8>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_slice_f16_s(sox_slice_copy_args p) { slice_body<half_t, 1>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_slice_bf16_s(sox_slice_copy_args p) { slice_body<bf16_t, 1>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_slice_f32_v(sox_slice_copy_args p) { slice_body<float, 4>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_slice_f32_s(sox_slice_copy_args p) { slice_body<float, 1>(p); }
 
 // ------------------------------------------------------------------------------------------
-// Staging conversions (f32to16.comp / f16to32.comp): fp16 RNE, as the (Half) cast.
+// Staging conversions (f32to16.comp / f16to32.comp): fp16 / bf16 round to nearest even, as the
+// (Half) cast.
 // ------------------------------------------------------------------------------------------
-extern "C" __global__ void __launch_bounds__(256) sox_f32_to_f16(sox_cvt_args p) {
+template <typename T>
+__device__ __forceinline__ void f32_to_body(const sox_cvt_args& p) {
+    typedef vec_t<T, 4> T4;
     const long i = ((long)blockIdx.x * blockDim.x + threadIdx.x) * 4;
     const float* x = (const float*)p.x;
-    half_t* y = (half_t*)p.y;
+    T* y = (T*)p.y;
     if (i + 4 <= p.count) {
-        float4v v = *(const float4v*)(x + i);
-        half4 h;
-        h[0] = (half_t)v[0]; h[1] = (half_t)v[1]; h[2] = (half_t)v[2]; h[3] = (half_t)v[3];
-        *(half4*)(y + i) = h;
+        const float4v v = *(const float4v*)(x + i);
+        *(T4*)(y + i) = __builtin_convertvector(v, T4);  // round to nearest even
     } else {
-        for (long j = i; j < p.count; j++) y[j] = (half_t)x[j];
+        for (long j = i; j < p.count; j++) y[j] = (T)x[j];
     }
 }
 
-extern "C" __global__ void __launch_bounds__(256) sox_f16_to_f32(sox_cvt_args p) {
+template <typename T>
+__device__ __forceinline__ void to_f32_body(const sox_cvt_args& p) {
+    typedef vec_t<T, 4> T4;
     const long i = ((long)blockIdx.x * blockDim.x + threadIdx.x) * 4;
-    const half_t* x = (const half_t*)p.x;
+    const T* x = (const T*)p.x;
     float* y = (float*)p.y;
     if (i + 4 <= p.count) {
-        half4 h = *(const half4*)(x + i);
-        float4v v;
-        v[0] = (float)h[0]; v[1] = (float)h[1]; v[2] = (float)h[2]; v[3] = (float)h[3];
-        *(float4v*)(y + i) = v;
+        const T4 h = *(const T4*)(x + i);
+        *(float4v*)(y + i) = __builtin_convertvector(h, float4v);
     } else {
         for (long j = i; j < p.count; j++) y[j] = (float)x[j];
     }
 }
+
+extern "C" __global__ void __launch_bounds__(256) sox_f32_to_f16(sox_cvt_args p) { f32_to_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_f32_to_bf16(sox_cvt_args p) { f32_to_body<bf16_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_f16_to_f32(sox_cvt_args p) { to_f32_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_bf16_to_f32(sox_cvt_args p) { to_f32_body<bf16_t>(p); }
 
 
 // ------------------------------------------------------------------------------------------
@@ -837,6 +861,7 @@ __device__ __forceinline__ void ln_body(const sox_ln_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_ln_f16(sox_ln_args p) { ln_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_ln_bf16(sox_ln_args p) { ln_body<bf16_t>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_ln_f32(sox_ln_args p) { ln_body<float>(p); }
 
 // ------------------------------------------------------------------------------------------
@@ -907,6 +932,7 @@ __device__ __forceinline__ void softmax_body(const sox_softmax_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_softmax_f16(sox_softmax_args p) { softmax_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_softmax_bf16(sox_softmax_args p) { softmax_body<bf16_t>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_softmax_f32(sox_softmax_args p) { softmax_body<float>(p); }
 
 // ------------------------------------------------------------------------------------------
@@ -957,7 +983,9 @@ __device__ __forceinline__ void attn_body(const sox_attn_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(128) sox_attn_f16_d32(sox_attn_args p) { attn_body<half_t, 32>(p); }
+extern "C" __global__ void __launch_bounds__(128) sox_attn_bf16_d32(sox_attn_args p) { attn_body<bf16_t, 32>(p); }
 extern "C" __global__ void __launch_bounds__(128) sox_attn_f16_d64(sox_attn_args p) { attn_body<half_t, 64>(p); }
+extern "C" __global__ void __launch_bounds__(128) sox_attn_bf16_d64(sox_attn_args p) { attn_body<bf16_t, 64>(p); }
 extern "C" __global__ void __launch_bounds__(128) sox_attn_f32_d32(sox_attn_args p) { attn_body<float, 32>(p); }
 extern "C" __global__ void __launch_bounds__(128) sox_attn_f32_d64(sox_attn_args p) { attn_body<float, 64>(p); }
 
@@ -994,6 +1022,7 @@ __device__ __forceinline__ void pool_body(const sox_pool_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_pool_f16(sox_pool_args p) { pool_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_pool_bf16(sox_pool_args p) { pool_body<bf16_t>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_pool_f32(sox_pool_args p) { pool_body<float>(p); }
 
 // ------------------------------------------------------------------------------------------
@@ -1009,33 +1038,35 @@ extern "C" __global__ void __launch_bounds__(256) sox_pool_f32(sox_pool_args p) 
 // the B operand (V) is read at the same key permutation (two 8-byte runs of V^T), which leaves the
 // sum over keys unchanged. Keys past S hold P = 0 and V = 0.
 // ------------------------------------------------------------------------------------------
-template <int NJ, int KD>
+template <typename T, int NJ, int KD>
 __device__ __forceinline__ void attn_mfma_body(const sox_attn_args& p) {
+    typedef vec_t<T, 8> T8;
+    typedef vec_t<T, 4> T4;
     constexpr int S = 16 * NJ, D = 32 * KD, NC = (NJ + 1) / 2, SP = 32 * NC, JD = 2 * KD;
     constexpr int KP = D + 8, VP = SP + 8;  // LDS row pitches in halves
-    __shared__ __attribute__((aligned(16))) half_t ks[S * KP];
-    __shared__ __attribute__((aligned(16))) half_t vt[D * VP];
+    __shared__ __attribute__((aligned(16))) T ks[S * KP];
+    __shared__ __attribute__((aligned(16))) T vt[D * VP];
     const int tid = threadIdx.x, nthr = blockDim.x, lane = tid & 63, wave = tid >> 6, nwaves = nthr >> 6;
     const int l16 = lane & 15, g = lane >> 4;
     const int bh = blockIdx.x;
     const int b = bh / p.heads, h = bh - b * p.heads;
-    const half_t* __restrict__ q = (const half_t*)p.q + b * p.q_sb + h * p.q_sh;
-    const half_t* __restrict__ k = (const half_t*)p.k + b * p.k_sb + h * p.k_sh;
-    const half_t* __restrict__ v = (const half_t*)p.v + b * p.v_sb + h * p.v_sh;
+    const T* __restrict__ q = (const T*)p.q + b * p.q_sb + h * p.q_sh;
+    const T* __restrict__ k = (const T*)p.k + b * p.k_sb + h * p.k_sh;
+    const T* __restrict__ v = (const T*)p.v + b * p.v_sb + h * p.v_sh;
     const int tblocks = (p.t + 15) / 16;
-    auto load_q = [&](int tb, half8 (&qf)[KD]) {
+    auto load_q = [&](int tb, T8 (&qf)[KD]) {
         const int t = tb * 16 + l16;
 #pragma unroll
         for (int kd = 0; kd < KD; kd++)
-            qf[kd] = t < p.t ? *(const half8*)(q + (long)t * p.q_st + 32 * kd + 8 * g) : (half8)(half_t)0;
+            qf[kd] = t < p.t ? *(const T8*)(q + (long)t * p.q_st + 32 * kd + 8 * g) : (T8)(T)0;
     };
-    half8 qf[KD];
+    T8 qf[KD];
     if (wave < tblocks) load_q(wave, qf);
     for (int i = tid; i < SP * (D / 8); i += nthr) {
         const int s = i / (D / 8), c = i - s * (D / 8);
-        const half8 zero = (half8)(half_t)0;
-        const half8 vv = s < p.s ? *(const half8*)(v + (long)s * p.v_st + 8 * c) : zero;
-        if (s < S) *(half8*)(ks + s * KP + 8 * c) = s < p.s ? *(const half8*)(k + (long)s * p.k_st + 8 * c) : zero;
+        const T8 zero = (T8)(T)0;
+        const T8 vv = s < p.s ? *(const T8*)(v + (long)s * p.v_st + 8 * c) : zero;
+        if (s < S) *(T8*)(ks + s * KP + 8 * c) = s < p.s ? *(const T8*)(k + (long)s * p.k_st + 8 * c) : zero;
 #pragma unroll
         for (int e = 0; e < 8; e++) vt[(8 * c + e) * VP + s] = vv[e];
     }
@@ -1048,8 +1079,8 @@ __device__ __forceinline__ void attn_mfma_body(const sox_attn_args& p) {
             float4v acc = (float4v)0.0f;
 #pragma unroll
             for (int kd = 0; kd < KD; kd++) {
-                const half8 kf = *(const half8*)(ks + (16 * j + l16) * KP + 32 * kd + 8 * g);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[kd], acc, 0, 0, 0);
+                const T8 kf = *(const T8*)(ks + (16 * j + l16) * KP + 32 * kd + 8 * g);
+                acc = mfma16x16x32(kf, qf[kd], acc);
             }
             sc[j] = acc;
         }
@@ -1082,35 +1113,38 @@ __device__ __forceinline__ void attn_mfma_body(const sox_attn_args& p) {
         for (int jd = 0; jd < JD; jd++) o[jd] = (float4v)0.0f;
 #pragma unroll
         for (int c = 0; c < NC; c++) {
-            half8 pa;
+            T8 pa;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                pa[i] = (half_t)sc[2 * c][i];
-                pa[4 + i] = 2 * c + 1 < NJ ? (half_t)sc[2 * c + 1][i] : (half_t)0;
+                pa[i] = (T)sc[2 * c][i];
+                pa[4 + i] = 2 * c + 1 < NJ ? (T)sc[2 * c + 1][i] : (T)0;
             }
 #pragma unroll
             for (int jd = 0; jd < JD; jd++) {
-                const half_t* row = vt + (16 * jd + l16) * VP + 32 * c + 4 * g;
-                const half4 lo = *(const half4*)row, hi = *(const half4*)(row + 16);
-                const half8 vb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                o[jd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o[jd], 0, 0, 0);
+                const T* row = vt + (16 * jd + l16) * VP + 32 * c + 4 * g;
+                const T4 lo = *(const T4*)row, hi = *(const T4*)(row + 16);
+                const T8 vb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                o[jd] = mfma16x16x32(pa, vb, o[jd]);
             }
         }
-        half_t* __restrict__ out = (half_t*)p.o + b * p.o_sb + h * p.o_sh;
+        T* __restrict__ out = (T*)p.o + b * p.o_sb + h * p.o_sh;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int tt = tb * 16 + 4 * g + i;
             const float inv = 1.0f / __shfl(sum, 4 * g + i, 64);
             if (tt < p.t)
 #pragma unroll
-                for (int jd = 0; jd < JD; jd++) out[(long)tt * p.o_st + 16 * jd + l16] = (half_t)(o[jd][i] * inv);
+                for (int jd = 0; jd < JD; jd++) out[(long)tt * p.o_st + 16 * jd + l16] = (T)(o[jd][i] * inv);
         }
     }
 }
 
 #define SOX_ATTN_MFMA(S, D)                                                                                  \
     extern "C" __global__ void __launch_bounds__(512) sox_attn_f16_mfma_s##S##_d##D(sox_attn_args p) {        \
-        attn_mfma_body<S / 16, D / 32>(p);                                                                   \
+        attn_mfma_body<half_t, S / 16, D / 32>(p);                                                           \
+    }                                                                                                        \
+    extern "C" __global__ void __launch_bounds__(512) sox_attn_bf16_mfma_s##S##_d##D(sox_attn_args p) {       \
+        attn_mfma_body<bf16_t, S / 16, D / 32>(p);                                                           \
     }
 SOX_ATTN_MFMA(32, 32)
 SOX_ATTN_MFMA(64, 32)
@@ -1293,13 +1327,14 @@ __device__ __forceinline__ void conv_direct_333_body(const sox_igemm_args& p) {
 // the weights are staged once per workgroup in LDS as fp32, k-major and padded to 8 channels
 // ([K][8], zeros past OC), so each input value meets its weights in one or two broadcast 16-byte
 // LDS reads; the input comes in 16-byte runs of 8 channels.
-template <int OC>
+template <typename T, int OC>
 __device__ __forceinline__ void conv_narrow_body(const sox_igemm_args& p) {
+    typedef vec_t<T, 8> T8;
     extern __shared__ float wl[];  // [K][8]
     const int K = p.k;
     for (int i = threadIdx.x; i < K * 8; i += blockDim.x) {
         const int kk = i >> 3, o = i & 7;
-        wl[i] = o < OC ? (float)((const half_t*)p.w)[(long)o * p.kpad + kk] : 0.0f;
+        wl[i] = o < OC ? (float)((const T*)p.w)[(long)o * p.kpad + kk] : 0.0f;
     }
     __syncthreads();
     const long m = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1308,7 +1343,7 @@ __device__ __forceinline__ void conv_narrow_body(const sox_igemm_args& p) {
     const int b = (int)(m / ohw), r = (int)(m - (long)b * ohw);
     const int oy = r / p.ow, ox = r - oy * p.ow;
     const bool reflect = (p.flags & SOX_F_REFLECT) != 0;
-    const half_t* __restrict__ x = (const half_t*)p.x + (long)b * p.ih * p.iw * p.ic;
+    const T* __restrict__ x = (const T*)p.x + (long)b * p.ih * p.iw * p.ic;
     float acc[OC];
 #pragma unroll
     for (int e = 0; e < OC; e++) acc[e] = (p.flags & SOX_F_BIAS) ? p.bias[e] : 0.0f;
@@ -1317,10 +1352,10 @@ __device__ __forceinline__ void conv_narrow_body(const sox_igemm_args& p) {
         for (int kx = 0; kx < p.kw; kx++) {
             const int ix = sox_src_index(ox * p.sw + kx - p.pl, p.iw, reflect);
             const bool in = iy >= 0 && ix >= 0;
-            const half_t* xr = x + ((long)(in ? iy : 0) * p.iw + (in ? ix : 0)) * p.ic;
+            const T* xr = x + ((long)(in ? iy : 0) * p.iw + (in ? ix : 0)) * p.ic;
             const float* wk = wl + (ky * p.kw + kx) * p.ic * 8;
             for (int c = 0; c < p.ic; c += 8) {
-                const half8 xv = *(const half8*)(xr + c);  // pixel 0 for a padding tap (not used)
+                const T8 xv = *(const T8*)(xr + c);  // pixel 0 for a padding tap (not used)
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
                     const float xf = in ? (float)xv[j] : p.pad_value;  // the pad value stays fp32
@@ -1341,22 +1376,27 @@ __device__ __forceinline__ void conv_narrow_body(const sox_igemm_args& p) {
 #pragma unroll
     for (int e = 0; e < OC; e++) {
         float v = acc[e];
-        if (p.flags & SOX_F_RESIDUAL) v += (float)((const half_t*)p.add)[o + e];
-        ((half_t*)p.y)[o + e] = (half_t)act_fast(v, act);
+        if (p.flags & SOX_F_RESIDUAL) v += (float)((const T*)p.add)[o + e];
+        ((T*)p.y)[o + e] = (T)act_fast(v, act);
     }
 }
 
-#define SOX_CONV_NARROW(OC) \
-    extern "C" __global__ void __launch_bounds__(256) sox_conv_narrow_f16_o##OC(sox_igemm_args p) { conv_narrow_body<OC>(p); }
+#define SOX_CONV_NARROW(OC)                                                                                   \
+    extern "C" __global__ void __launch_bounds__(256) sox_conv_narrow_f16_o##OC(sox_igemm_args p) { conv_narrow_body<half_t, OC>(p); } \
+    extern "C" __global__ void __launch_bounds__(256) sox_conv_narrow_bf16_o##OC(sox_igemm_args p) { conv_narrow_body<bf16_t, OC>(p); }
 SOX_CONV_NARROW(1) SOX_CONV_NARROW(2) SOX_CONV_NARROW(3) SOX_CONV_NARROW(4)
 SOX_CONV_NARROW(5) SOX_CONV_NARROW(6) SOX_CONV_NARROW(7)
 
 extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_333_f16(sox_igemm_args p) { conv_direct_333_body<half_t, 8, false>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_333_bf16(sox_igemm_args p) { conv_direct_333_body<bf16_t, 8, false>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_333_f32(sox_igemm_args p) { conv_direct_333_body<float, 4, false>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_f16(sox_igemm_args p) { conv_direct_body<half_t, 8, false>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_bf16(sox_igemm_args p) { conv_direct_body<bf16_t, 8, false>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_f32(sox_igemm_args p) { conv_direct_body<float, 4, false>(p); }
 // with the fused 2x2/2 max pool (SOX_F_POOL)
 extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_333_pool_f16(sox_igemm_args p) { conv_direct_333_body<half_t, 8, true>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_333_pool_bf16(sox_igemm_args p) { conv_direct_333_body<bf16_t, 8, true>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_333_pool_f32(sox_igemm_args p) { conv_direct_333_body<float, 4, true>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_pool_f16(sox_igemm_args p) { conv_direct_body<half_t, 8, true>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_pool_bf16(sox_igemm_args p) { conv_direct_body<bf16_t, 8, true>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_conv_direct_pool_f32(sox_igemm_args p) { conv_direct_body<float, 4, true>(p); }

@@ -16,6 +16,18 @@ typedef half_t half4 __attribute__((ext_vector_type(4)));
 typedef half_t half2v __attribute__((ext_vector_type(2)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef float float16v __attribute__((ext_vector_type(16)));
+// bfloat16 storage (the bf16 graph mode): conversions from fp32 round to nearest even
+// (v_cvt_pk_bf16_f32), to fp32 are exact
+typedef __bf16 bf16_t;
+typedef bf16_t bf16x8 __attribute__((ext_vector_type(8)));
+typedef bf16_t bf16x4 __attribute__((ext_vector_type(4)));
+typedef bf16_t bf16x2 __attribute__((ext_vector_type(2)));
+
+// N-element vector of a 16-bit storage type
+template <typename T, int N> struct VecN {
+    typedef T type __attribute__((ext_vector_type(N)));
+};
+template <typename T, int N> using vec_t = typename VecN<T, N>::type;
 
 #define SOX_DEV static __device__ __forceinline__
 
@@ -84,6 +96,12 @@ SOX_DEV float gelu_fast(float x) {
 }
 
 SOX_DEV float act_fast(float v, int act) { return act == SOX_ACT_GELU ? gelu_fast(v) : sox_act(v, act); }
+
+// 32x32x16 matrix-core step for either 16-bit storage type, fp32 accumulation
+SOX_DEV float16v mfma32x32x16(half8 a, half8 b, float16v c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
+SOX_DEV float16v mfma32x32x16(bf16x8 a, bf16x8 b, float16v c) { return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0); }
+SOX_DEV float4v mfma16x16x32(half8 a, half8 b, float4v c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+SOX_DEV float4v mfma16x16x32(bf16x8 a, bf16x8 b, float4v c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
 
 SOX_DEV float sox_ew(float a, float b, int op) {
     switch (op) {

@@ -60,7 +60,9 @@ __device__ __forceinline__ void bilinear_body(const sox_bilinear_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_bilinear_f16_v(sox_bilinear_args p) { bilinear_body<half_t, 8>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_bilinear_bf16_v(sox_bilinear_args p) { bilinear_body<bf16_t, 8>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_bilinear_f16_s(sox_bilinear_args p) { bilinear_body<half_t, 1>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_bilinear_bf16_s(sox_bilinear_args p) { bilinear_body<bf16_t, 1>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_bilinear_f32_v(sox_bilinear_args p) { bilinear_body<float, 4>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_bilinear_f32_s(sox_bilinear_args p) { bilinear_body<float, 1>(p); }
 
@@ -99,7 +101,9 @@ __device__ __forceinline__ void pad_body(const sox_pad_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_pad_f16_v(sox_pad_args p) { pad_body<half_t, 8>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_pad_bf16_v(sox_pad_args p) { pad_body<bf16_t, 8>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_pad_f16_s(sox_pad_args p) { pad_body<half_t, 1>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_pad_bf16_s(sox_pad_args p) { pad_body<bf16_t, 1>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_pad_f32_v(sox_pad_args p) { pad_body<float, 4>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_pad_f32_s(sox_pad_args p) { pad_body<float, 1>(p); }
 
@@ -125,6 +129,7 @@ __device__ __forceinline__ void gather_body(const sox_gather_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_gather_f16(sox_gather_args p) { gather_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_gather_bf16(sox_gather_args p) { gather_body<bf16_t>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_gather_f32(sox_gather_args p) { gather_body<float>(p); }
 
 // ------------------------------------------------------------------------------------------
@@ -157,6 +162,7 @@ __device__ __forceinline__ void transpose2d_body(const sox_transpose2d_args& p) 
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_transpose2d_f16(sox_transpose2d_args p) { transpose2d_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_transpose2d_bf16(sox_transpose2d_args p) { transpose2d_body<bf16_t>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_transpose2d_f32(sox_transpose2d_args p) { transpose2d_body<float>(p); }
 
 // ------------------------------------------------------------------------------------------
@@ -193,6 +199,7 @@ __device__ __forceinline__ void unary2_body(const sox_unary2_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_unary2_f16(sox_unary2_args p) { unary2_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_unary2_bf16(sox_unary2_args p) { unary2_body<bf16_t>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_unary2_f32(sox_unary2_args p) { unary2_body<float>(p); }
 
 // ------------------------------------------------------------------------------------------
@@ -226,6 +233,7 @@ __device__ __forceinline__ void d2s_body(const sox_d2s_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_d2s_f16(sox_d2s_args p) { d2s_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_d2s_bf16(sox_d2s_args p) { d2s_body<bf16_t>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_d2s_f32(sox_d2s_args p) { d2s_body<float>(p); }
 
 // DCR order with whole 16-byte channel vectors: the CV consecutive output channels of a work item
@@ -257,6 +265,7 @@ __device__ __forceinline__ void d2s_dcr_body(const sox_d2s_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_d2s_dcr_f16(sox_d2s_args p) { d2s_dcr_body<half_t, 8>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_d2s_dcr_bf16(sox_d2s_args p) { d2s_dcr_body<bf16_t, 8>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_d2s_dcr_f32(sox_d2s_args p) { d2s_dcr_body<float, 4>(p); }
 
 // ------------------------------------------------------------------------------------------
@@ -297,7 +306,9 @@ __device__ __forceinline__ void avgpool_body(const sox_avgpool_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_avgpool_f16_v(sox_avgpool_args p) { avgpool_body<half_t, 8>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_avgpool_bf16_v(sox_avgpool_args p) { avgpool_body<bf16_t, 8>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_avgpool_f16_s(sox_avgpool_args p) { avgpool_body<half_t, 1>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_avgpool_bf16_s(sox_avgpool_args p) { avgpool_body<bf16_t, 1>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_avgpool_f32_v(sox_avgpool_args p) { avgpool_body<float, 4>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_avgpool_f32_s(sox_avgpool_args p) { avgpool_body<float, 1>(p); }
 
@@ -332,6 +343,7 @@ __device__ __forceinline__ void gap_mean_body(const sox_gap_mean_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_gap_mean_f16(sox_gap_mean_args p) { gap_mean_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_gap_mean_bf16(sox_gap_mean_args p) { gap_mean_body<bf16_t>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_gap_mean_f32(sox_gap_mean_args p) { gap_mean_body<float>(p); }
 
 // ------------------------------------------------------------------------------------------
@@ -390,6 +402,7 @@ __device__ __forceinline__ void matmul_body(const sox_matmul_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_matmul_f16(sox_matmul_args p) { matmul_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_matmul_bf16(sox_matmul_args p) { matmul_body<bf16_t>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_matmul_f32(sox_matmul_args p) { matmul_body<float>(p); }
 
 // ------------------------------------------------------------------------------------------
@@ -417,6 +430,7 @@ __device__ __forceinline__ void safediv_body(const sox_safediv_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_safediv_f16(sox_safediv_args p) { safediv_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_safediv_bf16(sox_safediv_args p) { safediv_body<bf16_t>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_safediv_f32(sox_safediv_args p) { safediv_body<float>(p); }
 
 // ------------------------------------------------------------------------------------------
@@ -456,7 +470,9 @@ __device__ __forceinline__ void shift_body(const sox_shift_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_shift_f16_v(sox_shift_args p) { shift_body<half_t, 8>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_shift_bf16_v(sox_shift_args p) { shift_body<bf16_t, 8>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_shift_f16_s(sox_shift_args p) { shift_body<half_t, 1>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_shift_bf16_s(sox_shift_args p) { shift_body<bf16_t, 1>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_shift_f32_v(sox_shift_args p) { shift_body<float, 4>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_shift_f32_s(sox_shift_args p) { shift_body<float, 1>(p); }
 
@@ -548,7 +564,9 @@ __device__ __forceinline__ void uphead_body(const sox_uphead_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_uphead_f16_v(sox_uphead_args p) { uphead_body<half_t, 8>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_uphead_bf16_v(sox_uphead_args p) { uphead_body<bf16_t, 8>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_uphead_f16_s(sox_uphead_args p) { uphead_body<half_t, 4>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_uphead_bf16_s(sox_uphead_args p) { uphead_body<bf16_t, 4>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_uphead_f32_v(sox_uphead_args p) { uphead_body<float, 4>(p); }
 
 // ------------------------------------------------------------------------------------------
@@ -587,6 +605,7 @@ __device__ __forceinline__ void img2nhwc_body(const sox_img2nhwc_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_img2nhwc_f16(sox_img2nhwc_args p) { img2nhwc_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_img2nhwc_bf16(sox_img2nhwc_args p) { img2nhwc_body<bf16_t>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_img2nhwc_f32(sox_img2nhwc_args p) { img2nhwc_body<float>(p); }
 
 template <typename T>
@@ -627,5 +646,6 @@ __device__ __forceinline__ void nhwc2img_body(const sox_nhwc2img_args& p) {
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_nhwc2img_f16(sox_nhwc2img_args p) { nhwc2img_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_nhwc2img_bf16(sox_nhwc2img_args p) { nhwc2img_body<bf16_t>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_nhwc2img_f32(sox_nhwc2img_args p) { nhwc2img_body<float>(p); }
 

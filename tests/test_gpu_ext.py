@@ -60,7 +60,7 @@ class MyHardSigmoid:
         count = int(np.prod(g.shape(outs[0])))
         # kernarg = the two binds, then {count, alpha, beta} and the struct's tail padding
         kp = struct.pack("<Iff4x", count, hs.alpha, hs.beta)
-        return g.dispatch(node, "my_hsig_f16" if g.f16 else "my_hsig_f32", [g.bind(ins[0]), g.bind(outs[0])], kp,
+        return g.dispatch(node, "my_hsig_" + g.storage, [g.bind(ins[0]), g.bind(outs[0])], kp,
                           grid=((count + 255) // 256, 1, 1), module=self.module)
 
 
@@ -73,7 +73,7 @@ def run_session(graph, x, replay=False):
         return s.run().copy()
 
 
-@pytest.mark.parametrize("half", [False, True], ids=["f32", "f16"])
+@pytest.mark.parametrize("half", [False, True, "bf16"], ids=["f32", "f16", "bf16"])
 def test_extension_matches_builtin(hip, half):
     op = MyHardSigmoid(hip)
     x = np.sin(np.arange(8 * 12 * 16, dtype=np.float32) * 0.37).reshape(1, 8, 12, 16).transpose(0, 2, 3, 1).copy()
@@ -82,14 +82,14 @@ def test_extension_matches_builtin(hip, half):
     ext_g = hip.graph(ext_plan, half)
     names = [d[0] for d in ext_g.dispatches]
     print(f"[gpu] extension f16={half} dispatches={names}", flush=True)
-    assert op.emits == 1 and ("my_hsig_f16" if half else "my_hsig_f32") in names
+    assert op.emits == 1 and ("my_hsig_" + {False: "f32", True: "f16", "bf16": "bf16"}[half]) in names
     assert "unary" not in names and "unary" in [d[0] for d in plain_g.dispatches]
     want = run_session(plain_g, x)
     got = run_session(ext_g, x)
     assert np.array_equal(got, want)  # same fp32 formula on the same stored operands
     assert np.array_equal(run_session(ext_g, x, replay=True), want)
     ref = run_plan(plain_plan, [x], f16_storage=half)
-    assert max_rel(got, ref) < (2e-3 if half else 1e-4)
+    assert max_rel(got, ref) < {False: 1e-4, True: 2e-3, "bf16": 1.6e-2}[half]
     # the unit runner relocates the extension dispatch's binds into its own arena window
     r = HipUnitRunner(hip, streams=2)
     r.add(plain_g)

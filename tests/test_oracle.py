@@ -204,3 +204,13 @@ def test_bn_calibration_normalises_preactivations():
     want = run_plan(plan, ins)
     emu = run_plan(plan, ins, f16_storage=True)
     assert max_rel(emu, want) < 2e-2
+
+
+def test_bf16_storage_rounding_matches_torch():
+    """The oracle's bf16 storage emulation (round to nearest even, the v_cvt_pk_bf16_f32 rounding)
+    equals torch's float32 -> bfloat16 cast, ties and subnormals included."""
+    import torch
+    from oracle.interp import _bf16
+    x = np.random.default_rng(0).standard_normal(200000).astype(np.float32) * 100
+    x[:6] = [1.00390625, 1.01171875, -1.00390625, -2.5e-39, 3.0e38, 0.0]  # exact ties, subnormal, large
+    assert np.array_equal(_bf16(x), torch.from_numpy(x).to(torch.bfloat16).float().numpy())
