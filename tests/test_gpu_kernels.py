@@ -518,3 +518,40 @@ def test_conv_narrow_pad_value_is_fp32(hip):
         outs.append(got)
     assert not np.array_equal(outs[0], outs[1])
     assert np.array_equal(outs[0][:, 1:-1, 1:-1], outs[1][:, 1:-1, 1:-1])  # interior pixels see no padding
+
+
+@pytest.mark.parametrize("storage", ["f16", "bf16"])
+def test_gemm_gelu_epilogue_within_one_ulp(hip, storage):
+    """The 16-bit Gemm epilogue's GELU (one exp2 per element) over every fp16 value in [-8, 8] (every
+    bf16 value for bf16): A = x e_0, W row 0 = 1, so each output is GELU(x) of one exact fp32
+    accumulator. Against the float64 erf-GELU (scipy's erfc) it is within one ulp of the 16-bit
+    output at the exact value, or 1e-6 absolute where that is larger (outputs of |x| > 5.5 and
+    fp16's subnormal range: the A&S 7.1.26 form of the reference is itself ~3e-7 off there)."""
+    from scipy.special import erfc
+    from oracle.interp import _bf16
+    pos = np.arange(0, np.float16(8.0).view(np.uint16), dtype=np.uint16).view(np.float16)
+    x = np.unique(np.concatenate([pos, -pos]).astype(np.float32))
+    if storage == "bf16":
+        x = np.unique(_bf16(np.linspace(-8, 8, 200001, dtype=np.float32)))
+    m = (len(x) + 63) // 64 * 64
+    a = np.zeros((m, 64), np.float32)
+    a[: len(x), 0] = x
+    w = np.zeros((64, 64), np.float32)
+    w[0, :] = 1.0
+    pb = PlanBuilder()
+    av = pb.input((m, 64), None, "a")
+    y = pb.gemm(av, w, None, act="gelu", name="gemm")
+    g = hip.graph(pb.build(y), storage)
+    assert [d[0] for d in g.dispatches] == ["gemm"]
+    with HipInferenceSession(g) as s:
+        s.set_input(a)
+        got = s.run().copy()[: len(x)]
+    assert np.all(got == got[:, :1])
+    got = got[:, 0].astype(np.float64)
+    xd = x.astype(np.float64)
+    ref = xd * 0.5 * erfc(-xd / np.sqrt(2.0))
+    mag = np.abs(ref)
+    exp = np.floor(np.log2(np.maximum(mag, 1e-300)))
+    ulp = np.ldexp(1.0, (exp - (10 if storage == "f16" else 7)).astype(np.int32))
+    bad = np.abs(got - ref) > np.maximum(ulp, 1e-6)
+    assert not bad.any(), (x[bad][:8], got[bad][:8], ref[bad][:8])
