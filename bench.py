@@ -386,24 +386,67 @@ def bench_ops(steps: int):
     return out
 
 
-def cpu_detector_ms():
-    """The oracle running the whole detector plan (reference CPU kernels restated), ms per image."""
+def cpu_info():
+    """The host the CPU baseline ran on: model, logical CPUs used, physical cores, oracle ISA tier."""
+    import oracle as O
+    model, cores = "unknown", set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            phys = core = None
+            for line in f:
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "model name" and model == "unknown":
+                    model = v
+                elif k == "physical id":
+                    phys = v
+                elif k == "core id":
+                    core = v
+                elif not k and phys is not None:
+                    cores.add((phys, core))
+                    phys = core = None
+            if phys is not None:
+                cores.add((phys, core))
+    except OSError:
+        pass
+    tier = "avx512" if O.tier_available(O.TIER_AVX512) else "avx2" if O.tier_available(O.TIER_AVX2) else "scalar"
+    return dict(model=model, logical_cpus_used=cpu_threads(), physical_cores=len(cores) or None, isa_tier=tier)
+
+
+def _median_ms(fn, runs):
+    fn()  # warm-up (page-in, thread pool)
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return round(statistics.median(ts) * 1e3, 3)
+
+
+def cpu_configs():
+    """The oracle (the reference's CPU kernels restated) on the other benchmark configurations, all host
+    threads, median ms: config 1 at full size, configs 3 and 4 per image at full size, config 5 on a
+    batch of 8 of its 32 images (ms per image)."""
     import oracle as O
     from oracle.interp import run_plan
     from simdonnx_amd import graphs
     O.set_threads(cpu_threads())
+    out = {}
+    plan, ins = graphs.conv3x3_bias_relu()
+    out["conv3x3_bias_relu_fp32_ms"] = _median_ms(lambda: run_plan(plan, ins), 20)
+    plan, ins = graphs.mobilenetv3_small()
+    out["mobilenetv3_ms_per_image"] = _median_ms(lambda: run_plan(plan, ins), 3)
     plan, ins = graphs.dbnet()
-    run_plan(plan, ins)
-    ts = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        run_plan(plan, ins)
-        ts.append(time.perf_counter() - t0)
-    return round(statistics.median(ts) * 1e3, 2)
+    out["detector_ms_per_image"] = _median_ms(lambda: run_plan(plan, ins), 3)
+    plan, ins = graphs.svtr(n=8)
+    out["recognizer_ms_per_image"] = round(_median_ms(lambda: run_plan(plan, ins), 1) / 8, 3)
+    out["recognizer_sample"] = "batch 8 of the 32 images of config 5 (same per-image work)"
+    return out
 
 
 def cpu_baseline(budget_s: float = 12.0):
-    """The oracle Gemm + GELU on the full workload (M = 8192), all host threads, median of runs."""
+    """The oracle Gemm + GELU on the full workload (M = 8192), all host threads, median of runs; and
+    on one thread over the first 1024 rows (the reference bench's micro mode, Program.cs:12)."""
     import oracle as O
     from simdonnx_amd import graphs
     plan, ins = graphs.matmul_bias_gelu()
@@ -423,10 +466,19 @@ def cpu_baseline(budget_s: float = 12.0):
         if time.perf_counter() - t_start > 3 * budget_s:
             break
     med = statistics.median(times)
-    tier = "avx512" if O.tier_available(O.TIER_AVX512) else "avx2" if O.tier_available(O.TIER_AVX2) else "scalar"
+    info = cpu_info()
+    O.set_threads(1)
+    rows = 1024
+    ms1 = _median_ms(lambda: O.gemm(a[:rows], w, b, act="gelu"), 3)
+    O.set_threads(threads)
+    flops1 = 2 * rows * a.shape[1] * w.shape[1]
     return dict(value=graphs.matmul_flops() / med / 1e12, unit="TFLOP/s", cores=threads, kind="port",
                 sample=f"full workload M=8192 K=768 N=3072 + GELU, {len(times)} runs, median {med*1e3:.1f} ms, "
-                       f"{tier} tier (C++ restatement of Nhwc.Gemm512 / Epilogue512)")
+                       f"{info['isa_tier']} tier (C++ restatement of Nhwc.Gemm512 / Epilogue512)",
+                one_thread={"value": round(flops1 / (ms1 * 1e-3) / 1e12, 4), "unit": "TFLOP/s", "cores": 1,
+                            "sample": f"first {rows} rows (M={rows}, K=768, N=3072) + GELU, median of 3, "
+                                      f"{ms1:.1f} ms"},
+                cpu=info)
 
 
 def main():
@@ -518,9 +570,9 @@ def main():
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
         try:
-            out["cpu_baseline"]["detector_ms_per_image"] = cpu_detector_ms()
+            out["cpu_baseline"]["configs"] = cpu_configs()
         except Exception as e:
-            out["cpu_baseline"]["detector_ms_per_image"] = repr(e)
+            out["cpu_baseline"]["configs"] = {"error": repr(e)}
     print(json.dumps(out), flush=True)
 
 

@@ -1,11 +1,12 @@
-// The LDS-DMA persistent ring (instantiated by gemm.hip for dense Gemm and conv_ring.hip for Conv2d /
-// ConvTranspose): fp16 Gemm with fused bias + activation on CDNA4 matrix cores (the conv_cm.comp Gemm
-// route, Backends/Vulkan/VkGraph.cs:760-773, rebuilt for gfx950):
+// The LDS-DMA persistent ring (instantiated by gemm.hip / gemm_bf16.hip for dense Gemm and
+// conv_ring.hip / conv_ring_bf16.hip for Conv2d / ConvTranspose): 16-bit Gemm with fused bias +
+// activation on CDNA4 matrix cores (the conv_cm.comp Gemm route, Backends/Vulkan/VkGraph.cs:760-773,
+// rebuilt for gfx950):
 //   Y[M,N] = act(A[M,K] . W[N,K]^T + bias[N] (+ R[M,N])),  A dense rows (lda), W packed [N][kpad]
-//   k-fastest, R an optional same-shape residual, fp16 storage, fp32 accumulation, fp16 output.
+//   k-fastest, R an optional same-shape residual, fp16 or bf16 storage (T), fp32 accumulation.
 //
 // Structure (NW waves, BM x BN output tile, BK-deep K slices):
-//  * v_mfma_f32_32x32x16_f16 (the gfx950 instruction that sustains the dense fp16 rate with one wave
+//  * v_mfma_f32_32x32x16_f16 / _bf16 (the gfx950 instruction that sustains the dense rate with one wave
 //    per SIMD; the 16x16x32 form needs two waves per SIMD and still tops out lower). W is the row
 //    operand and A the column operand, so lane l holds Y^T[n = 8(q/4) + 4(l/32) + q%4][m = l%32]:
 //    4 runs of 4 consecutive output channels of one row, i.e. float4 bias/activation and 8-byte stores
@@ -192,7 +193,9 @@ SOX_DEV void store_tile_lds(T* __restrict__ Y, int ldy, int M, int N, int m0, in
             const int idx = decltype(tt)::value * 64 + lane, r = idx / CH, c = idx % CH;
             const T8 v = *(const T8*)(stg + r * CH * 16 + ((c ^ (r % CH)) << 4));
             const int m = m0 + i * 32 + r, n = n0 + j0 * 32 + c * 8;
-            if (m < M && n < N) *(T8*)(Y + (long)m * ldy + n) = v;
+            // streaming (nontemporal) stores: the output is not read again by this kernel, so its lines
+            // do not displace the A rows and W columns the other workgroups of the XCD re-read from L2
+            if (m < M && n < N) __builtin_nontemporal_store(v, (T8*)(Y + (long)m * ldy + n));
         });
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the next group overwrites the stage
         __builtin_amdgcn_wave_barrier();
@@ -244,7 +247,9 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
     constexpr int EPI_BYTES = EPI_LDS ? NW * EPI_WAVE : 0;
     __shared__ __attribute__((aligned(1024))) unsigned char smem[STAGE_BYTES * STAGES + EPI_BYTES];
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // the wave number in a scalar register: the LDS addresses derived from it (the DMA destinations in
+    // M0) are computed by the scalar unit
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l32 = lane & 31, hl = lane >> 5;
     const int M = p.m, N = p.n, K = p.k;
     const int tiles_n = p.tiles_n, tiles_m = (M + BM - 1) / BM, ntiles = tiles_m * tiles_n;
