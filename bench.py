@@ -26,6 +26,7 @@ import argparse
 import json
 import os
 import statistics
+import struct
 import sys
 import time
 
@@ -83,6 +84,85 @@ def bench_gemm(steps: int, warmup: int, storage="f16"):
     g.release()
     return dict(flops=flops, ms_total=ms, per_launch_ms=per_launch_ms, wall_s=wall, dispatches=names,
                 kernel_ms=[p[2] for p in prof])
+
+
+def bench_mfma_peak(iters: int = 4000, reps: int = 20):
+    """The matrix-core rate this GPU sustains on random fp16 operands with no memory traffic: the probe
+    kernel of the Gemm code object (sox_probe_mfma_f16), launched through the thin C ABI with two
+    waves per SIMD, timed with HIP events (median of `reps` launches after warm-up)."""
+    import ctypes
+    from simdonnx_amd import build as B
+    from simdonnx_amd import native as N
+    from simdonnx_amd.backend import HipBackend
+    hip = HipBackend.default()
+    T = N.thin()
+    with open(os.path.join(B.BUILD, "gemm.hsaco"), "rb") as f:
+        mod = hip.load_module(f.read())
+    fn = N.c_void_p()
+    N.check(T.sox_module_function(ctypes.byref(fn), mod, b"sox_probe_mfma_f16"), "probe kernel")
+    cus = hip.device.compute_units
+    threads = 512  # 8 waves per workgroup, one workgroup per CU: 2 waves per SIMD
+    out = N.c_void_p()
+    N.check(T.sox_malloc(ctypes.byref(out), cus * threads * 4), "probe output")
+    stream = N.c_void_p()
+    N.check(T.sox_stream_create(ctypes.byref(stream)), "stream")
+    ev = [N.c_void_p(), N.c_void_p()]
+    for e in ev:
+        N.check(T.sox_event_create(ctypes.byref(e)), "event")
+    grid = (N.c_uint32 * 3)(cus, 1, 1)
+    block = (N.c_uint32 * 3)(threads, 1, 1)
+
+    def launch(n):
+        args = struct.pack("<QiI", out.value, n, 12345)
+        buf = ctypes.create_string_buffer(args, len(args))
+        N.check(T.sox_launch(fn, grid, block, 0, stream, buf, len(args)), "probe launch")
+
+    for _ in range(200):  # warm-up: the clock settles under sustained matrix load
+        launch(iters)
+    times = []
+    for _ in range(reps):
+        N.check(T.sox_event_record(ev[0], stream), "event")
+        launch(iters)
+        N.check(T.sox_event_record(ev[1], stream), "event")
+        N.check(T.sox_event_sync(ev[1]), "event")
+        ms = N.c_float()
+        N.check(T.sox_event_elapsed_ms(ctypes.byref(ms), ev[0], ev[1]), "event")
+        times.append(ms.value)
+    for e in ev:
+        T.sox_event_destroy(e)
+    T.sox_stream_destroy(stream)
+    T.sox_free(out)
+    ms = statistics.median(times)
+    flops = cus * (threads // 64) * iters * 4 * 32 * 32 * 16 * 2
+    tf = flops / (ms * 1e-3) / 1e12
+    return dict(workload=f"{cus} CUs x 8 waves x {iters} x 4 v_mfma_f32_32x32x16_f16, random operands, no memory",
+                ms=round(ms, 4), tflop_s=round(tf, 1), frac_of_peak=round(tf / PEAK_FP16_TFLOPS, 4))
+
+
+def bench_conv_large(steps: int, storage="f16"):
+    """A large implicit-GEMM conv on the LDS-DMA ring: Conv3x3 s1 p1 + bias + ReLU, NHWC, 8x128x128,
+    256 -> 256 channels (154.6 GFLOP), 16-bit storage, against the dense MFMA peak."""
+    from simdonnx_amd import synth
+    from simdonnx_amd.backend import HipBackend, HipInferenceSession
+    from simdonnx_amd.plan import NHWC, PlanBuilder
+    n, h, w, c = 8, 128, 128, 256
+    pb = PlanBuilder()
+    x = pb.input((n, c, h, w), NHWC, "x")
+    y = pb.conv(x, synth.he_normal(64, 1, (c, c, 3, 3)), synth.uniform(64, 2, (c,), -0.1, 0.1), pad=1, act="relu",
+                name="conv")
+    hip = HipBackend.default()
+    g = hip.graph(pb.build(y), storage)
+    kern = [d[0] for d in g.dispatches]
+    with HipInferenceSession(g) as s:
+        s.set_input(synth.normal(64, 3, (n, h, w, c), 1.0))
+        s.run()
+        s.time(100)
+        ms = s.time(steps) / steps
+    g.release()
+    flops = 2 * n * h * w * c * c * 9
+    tf = flops / (ms * 1e-3) / 1e12
+    return dict(workload=f"conv3x3 s1 p1 + bias + ReLU, NHWC {n}x{h}x{w}, {c}->{c}, {storage} storage",
+                kernels=kern, us=round(ms * 1e3, 2), tflop_s=round(tf, 1), frac_of_peak=round(tf / PEAK_FP16_TFLOPS, 4))
 
 
 def bench_conv(steps: int):
@@ -489,7 +569,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-replay", action="store_true",
                     help="launch network dispatches one by one instead of replaying a HIP graph (profiler runs)")
-    ap.add_argument("--only", choices=["gemm", "gemm_bf16", "conv", "detector", "detector_fp32", "recognizer",
+    ap.add_argument("--only", choices=["gemm", "gemm_bf16", "mfma_peak", "conv_large", "conv", "detector", "detector_fp32", "recognizer",
                                        "recognizer_bf16", "mobilenetv3", "copy", "ops",
                                        "recognizer_ctc", "image", "runner"],
                     help="run one workload only (profiling runs); prints its own JSON line")
@@ -501,6 +581,7 @@ def main():
     if args.only:
         fn = {"gemm": lambda: bench_gemm(args.steps, args.warmup), "conv": lambda: bench_conv(args.steps),
               "gemm_bf16": lambda: bench_gemm(args.steps, args.warmup, "bf16"),
+              "mfma_peak": lambda: bench_mfma_peak(), "conv_large": lambda: bench_conv_large(args.steps),
               "copy": lambda: bench_copy(args.steps),
               "ops": lambda: {"ops": bench_ops(args.steps)},
               "recognizer_ctc": lambda: bench_recognizer_ctc(args.steps, not args.no_replay),
@@ -547,6 +628,16 @@ def main():
             log(f"{key}: {out[key]['ms_per_image']} ms/image")
         except Exception as e:  # reported, never hidden
             out[key] = {"error": repr(e)}
+    try:
+        out["mfma_peak_probe"] = bench_mfma_peak()
+        log(f"mfma probe: {out['mfma_peak_probe']['tflop_s']} TFLOP/s")
+    except Exception as e:
+        out["mfma_peak_probe"] = {"error": repr(e)}
+    try:
+        out["conv_large_f16"] = bench_conv_large(50)
+        log(f"large conv: {out['conv_large_f16']['tflop_s']} TFLOP/s")
+    except Exception as e:
+        out["conv_large_f16"] = {"error": repr(e)}
     try:
         out["conv3x3_bias_relu_fp32"] = bench_conv(200)
     except Exception as e:

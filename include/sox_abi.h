@@ -427,6 +427,15 @@ typedef struct sox_mlp_args {
     int32_t flags;      /* bit0 b2, bit1 residual, act2 << 4 */
 } sox_mlp_args;
 
+/* Matrix-core rate probe (sox_probe_mfma_f16 in the Gemm code object; a measurement kernel, no
+ * counterpart in the reference): each of the grid's waves runs `iters` rounds of four independent
+ * 32x32x16 fp16 MFMA chains on hashed register operands and writes one float per thread to out. */
+typedef struct sox_mfma_probe_args {
+    float* out;
+    int32_t iters;
+    uint32_t seed;
+} sox_mfma_probe_args;
+
 #ifdef __cplusplus
 }
 #endif

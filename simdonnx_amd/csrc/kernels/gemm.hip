@@ -23,3 +23,32 @@ SOX_GEMM_LN(sox_gemm_ln_f16_256x128_w8k64s2, half_t, 256, 128, 64, 64, 64, 2, 8,
 SOX_GEMM_LN(sox_gemm_ln_f16_128x128_k64s2, half_t, 128, 128, 64, 64, 64, 2, 4, 2, 4, false)
 SOX_GEMM_LN(sox_gemm_ln_f16_128x64_k64s2, half_t, 128, 64, 64, 64, 32, 2, 4, 3, 4, false)
 SOX_GEMM_LN(sox_gemm_ln_f16_64x64_k64s4, half_t, 64, 64, 64, 32, 32, 4, 4, 2, 4, true)
+
+// Matrix-core rate probe (bench.py --only mfma_peak): every wave runs `iters` rounds of four
+// independent v_mfma_f32_32x32x16_f16 chains on register operands, with operand bits from a per-lane
+// hash (random data: the power the matrix pipe draws, and so its sustained clock, depends on operand
+// toggling), and writes its accumulator sum so nothing is dead. No memory traffic in the loop.
+extern "C" __global__ void __launch_bounds__(512) sox_probe_mfma_f16(sox_mfma_probe_args p) {
+    const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
+    half8 a, b;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        uint32_t h = (gid * 8 + e) * 0x9E3779B1u ^ p.seed;
+        h ^= h >> 15;
+        h *= 0x2C1B3C6Du;
+        h ^= h >> 12;
+        a[e] = (half_t)((float)(h & 0xffff) * (1.0f / 32768.0f) - 1.0f);
+        b[e] = (half_t)((float)(h >> 16) * (1.0f / 32768.0f) - 1.0f);
+    }
+    float16v c0 = {}, c1 = {}, c2 = {}, c3 = {};
+    for (int i = 0; i < p.iters; i++) {
+        c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(b, a, c1, 0, 0, 0);
+        c2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, a, c2, 0, 0, 0);
+        c3 = __builtin_amdgcn_mfma_f32_32x32x16_f16(b, b, c3, 0, 0, 0);
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; e++) s += c0[e] + c1[e] + c2[e] + c3[e];
+    p.out[gid] = s;
+}

@@ -586,3 +586,8 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
     extern "C" __global__ void __launch_bounds__(64 * NW, OCC) NAME(sox_igemm_args p) {           \
         gemm_body<T, BM, BN, BK, WM, WN, ST, NW, GM, true>(p);                                    \
     }
+// conv mode with the epilogue staged through LDS (large convs: whole 128-byte row segments per store)
+#define SOX_CONV_E(NAME, T, BM, BN, BK, WM, WN, ST, NW, OCC, GM)                                    \
+    extern "C" __global__ void __launch_bounds__(64 * NW, OCC) NAME(sox_igemm_args p) {           \
+        gemm_body<T, BM, BN, BK, WM, WN, ST, NW, GM, true, true>(p);                              \
+    }

@@ -555,3 +555,24 @@ def test_gemm_gelu_epilogue_within_one_ulp(hip, storage):
     ulp = np.ldexp(1.0, (exp - (10 if storage == "f16" else 7)).astype(np.int32))
     bad = np.abs(got - ref) > np.maximum(ulp, 1e-6)
     assert not bad.any(), (x[bad][:8], got[bad][:8], ref[bad][:8])
+
+
+@pytest.mark.parametrize("kernel", ["", "sox_conv_f16_256x128_w8k64s2"], ids=["default", "w8-256x128"])
+@pytest.mark.parametrize("storage", ["f16", "bf16"])
+def test_conv_large_channels(hip, storage, kernel, monkeypatch):
+    """The large implicit-GEMM conv the bench times (3x3 s1 p1 + bias + ReLU, 256 -> 256 channels on
+    the LDS-DMA ring), at batch 1 and 48x40 so the oracle stays quick; also forced onto the 8-wave
+    tiling the bench's 8x128x128 size selects."""
+    if kernel:
+        monkeypatch.setenv("SIMDONNX_HIP_CONV", kernel)
+    from oracle.interp import _bf16
+    cv = f16 if storage == "f16" else _bf16
+    x = cv(synth.normal(64, 3, (1, 48, 40, 256), 1.0))
+    wt = cv(synth.he_normal(64, 1, (256, 256, 3, 3)))
+    b = synth.uniform(64, 2, (256,), -0.1, 0.1)
+    plan, ins = conv_plan(x, wt, b, None, (1, 1), (1, 1, 1, 1), "relu", 0, 0.0)
+    g = hip.graph(plan, storage)
+    assert [d[0] for d in g.dispatches] == ["conv"]
+    got = run(hip, plan, ins, storage)
+    want = O.conv(x, wt, b, stride=(1, 1), pads=(1, 1, 1, 1), act="relu")
+    assert max_rel(got, want) < (TOL[True] if storage == "f16" else 4e-3)
