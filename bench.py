@@ -49,13 +49,17 @@ def cpu_threads() -> int:
         return os.cpu_count() or 1
 
 
-def traffic_from_profiles(workload: str):
-    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 PMC summary."""
+def traffic_from_profiles(workload: str, kernel: str):
+    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 PMC summary; None when
+    the summary was taken on another kernel (a tiling that the backend no longer selects)."""
     path = os.path.join(ROOT, "profiles", f"traffic_{workload}.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
         d = json.load(f)
+    if d.get("kernel") != kernel:
+        log(f"traffic summary is for {d.get('kernel')}, the bench runs {kernel}: traffic not reported")
+        return None
     return d.get("bytes_per_launch")
 
 
@@ -69,6 +73,7 @@ def bench_gemm(steps: int, warmup: int, storage="f16"):
     flops = graphs.matmul_flops()
     g = hip.graph(plan, storage)
     names = [d[0] for d in g.dispatches]
+    kernels = g.kernels
     with HipInferenceSession(g) as s:
         s.set_input(ins[0])
         s.run()  # stage the input into the arena once: the timed region reads it resident in HBM
@@ -83,7 +88,7 @@ def bench_gemm(steps: int, warmup: int, storage="f16"):
         prof = s.profile(5)
     g.release()
     return dict(flops=flops, ms_total=ms, per_launch_ms=per_launch_ms, wall_s=wall, dispatches=names,
-                kernel_ms=[p[2] for p in prof])
+                kernels=kernels, kernel_ms=[p[2] for p in prof])
 
 
 def bench_mfma_peak(iters: int = 4000, reps: int = 20):
@@ -611,7 +616,8 @@ def main():
                    "global_batch": 16, "seq_len": 512, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / PEAK_FP16_TFLOPS, 4),
-                     "traffic": traffic_from_profiles("matmul_bias_gelu")},
+                     "kernel": r["kernels"][0],
+                     "traffic": traffic_from_profiles("matmul_bias_gelu", r["kernels"][0])},
     }
     try:
         rb = bench_gemm(max(args.steps // 4, 1), min(args.warmup, 500), "bf16")

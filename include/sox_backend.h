@@ -172,6 +172,9 @@ void sox_graph_release(sox_graph* graph);
 int sox_graph_dispatch_count(sox_graph* graph);
 int sox_graph_dispatch_info(sox_graph* graph, int32_t index, char* name, size_t name_cap, uint32_t grid[3],
                             int32_t* node);
+/* The code object function dispatch `index` launches (its tiling, e.g. sox_gemm_f16_256x192_w8k64s2),
+ * next to the op label of sox_graph_dispatch_info: what a per-kernel profiler trace names it. */
+int sox_graph_dispatch_kernel(sox_graph* graph, int32_t index, char* kernel, size_t kernel_cap);
 uint64_t sox_graph_arena_bytes(sox_graph* graph);
 uint64_t sox_graph_const_bytes(sox_graph* graph);
 /* Last build error text (NotSupportedException message analogue). */

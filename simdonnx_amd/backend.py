@@ -220,6 +220,17 @@ class HipGraphModel:
         return out
 
     @property
+    def kernels(self):
+        """The code object function of each dispatch (its tiling), in dispatch order."""
+        out = []
+        lib = N.backend()
+        for i in range(lib.sox_graph_dispatch_count(self.h)):
+            name = ctypes.create_string_buffer(128)
+            N.check(lib.sox_graph_dispatch_kernel(self.h, i, name, 128), "dispatch_kernel")
+            out.append(name.value.decode())
+        return out
+
+    @property
     def arena_bytes(self) -> int:
         return int(N.backend().sox_graph_arena_bytes(self.h))
 

@@ -105,6 +105,16 @@ def write_resources(objs):
         f.write("\n".join(table) + "\n")
 
 
+def link_backend(cxx=None):
+    """Links libsoxbackend.so from the compiled host code (backend.o) and the code objects that
+    resources.S embeds (the .hsaco files under _build as they are now)."""
+    cxx = cxx or os.path.join(ROCM, "llvm", "bin", "clang++")
+    be = os.path.join(LIB, "libsoxbackend.so")
+    _run([cxx, "-fPIC", f"-I{BUILD}", "-shared", "-o", be, os.path.join(BUILD, "backend.o"),
+          os.path.join(BUILD, "resources.S"), f"-L{LIB}", "-lsoxhip", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{ROCM}/lib"])
+    return be
+
+
 def build_libs(verbose=False):
     os.makedirs(LIB, exist_ok=True)
     cxx = os.path.join(ROCM, "llvm", "bin", "clang++")
@@ -122,8 +132,10 @@ def build_libs(verbose=False):
     _run([cxx, *common, "-shared", "-o", thin, os.path.join(HDIR, "sox_hip.cpp"), scratch_o, f"-L{ROCM}/lib",
           "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib"])
     be = os.path.join(LIB, "libsoxbackend.so")
-    _run([cxx, *common, f"-I{BUILD}", "-shared", "-o", be, os.path.join(HDIR, "backend.cpp"),
-          os.path.join(BUILD, "resources.S"), f"-L{LIB}", "-lsoxhip", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{ROCM}/lib"])
+    # the host code and the embedded code objects link separately: a kernel change re-links the
+    # library without recompiling backend.cpp (link_backend)
+    _run([cxx, *common, f"-I{BUILD}", "-c", "-o", os.path.join(BUILD, "backend.o"), os.path.join(HDIR, "backend.cpp")])
+    link_backend(cxx)
     if verbose:
         print("built", thin, be, flush=True)
     return thin, be

@@ -206,6 +206,7 @@ BACKEND_API = {
     "sox_graph_create": (c_int32, [c_void_p, c_void_p, c_int32, ctypes.POINTER(c_void_p)]),
     "sox_graph_release": (None, [c_void_p]),
     "sox_graph_dispatch_count": (c_int32, [c_void_p]),
+    "sox_graph_dispatch_kernel": (c_int32, [c_void_p, c_int32, ctypes.c_char_p, c_size_t]),
     "sox_graph_dispatch_info": (c_int32, [c_void_p, c_int32, ctypes.c_char_p, c_size_t, ctypes.POINTER(c_uint32),
                                           ctypes.POINTER(c_int32)]),
     "sox_graph_arena_bytes": (c_uint64, [c_void_p]),

@@ -33,6 +33,17 @@ def test_matmul_bias_gelu_fp16(hip):
     assert max_rel(got, want) <= 2e-2
 
 
+def test_dispatch_kernels_name_the_tiling(hip):
+    """Each dispatch reports the code object function it launches beside its op label: the headline
+    Gemm's one dispatch is labelled gemm and runs a fp16 ring tiling (bf16 on a bf16 graph)."""
+    plan, _ = graphs.matmul_bias_gelu()
+    for storage, prefix in (("f16", "sox_gemm_f16_"), ("bf16", "sox_gemm_bf16_")):
+        g = hip.graph(plan, storage)
+        assert [d[0] for d in g.dispatches] == ["gemm"]
+        assert len(g.kernels) == 1 and g.kernels[0].startswith(prefix), g.kernels
+        g.release()
+
+
 def test_matmul_bias_gelu_fp32(hip):
     plan, ins = graphs.matmul_bias_gelu(batch=2)
     got = run_gpu(hip, plan, ins, False)
