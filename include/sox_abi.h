@@ -88,6 +88,27 @@ typedef struct sox_dw_args {
 } sox_dw_args;
 
 /*
+ * Depthwise k x k over LDS tiles (k = 3 or 5, stride 1 or 2, 16-bit storage, zero or reflect pad):
+ * a workgroup computes an output tile of 8 x 8 pixels of 64 channels
+ * from the tile's input halo staged once in LDS. Grid (tiles_x * tiles_y, ceil(c / 64), n).
+ * gap = 1: the workgroup also writes the channel sums of its stored (rounded) outputs,
+ * part[b][tile][c], the GAP partials of an SE gate that reads this conv's output.
+ */
+typedef struct sox_dwt_args {
+    const void* x;
+    const void* w;
+    const float* bias;
+    const void* add;
+    void* y;
+    float* part;
+    int32_t n, c, ih, iw, oh, ow;
+    int32_t kh, kw, sh, sw, pt, pl;
+    int32_t flags;
+    int32_t tiles_x, tiles_y;
+    int32_t gap;
+} sox_dwt_args;
+
+/*
  * ConvTranspose with stride == kernel, no pad, group 1 (convt.comp; Kernels/Nhwc.Det.cs:51-131).
  *   w is [tap][ic][oc] (ConstKind.ConvTW). out[(y*kh+dy), (x*kw+dx), o] = act(b[o] + sum_c x[y,x,c] w[tap][c][o]).
  */

@@ -201,6 +201,158 @@ extern "C" __global__ void __launch_bounds__(256) sox_dw_f16_v5(sox_dw_args p) {
 extern "C" __global__ void __launch_bounds__(256) sox_dw_bf16_v5(sox_dw_args p) { dw_body_k<bf16_t, 8, 5>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_dw_f32_v3(sox_dw_args p) { dw_body_k<float, 4, 3>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_dw_f32_v5(sox_dw_args p) { dw_body_k<float, 4, 5>(p); }
+// Depthwise K x K, stride S, over LDS tiles (16-bit storage). A workgroup owns an output tile of
+// 8 x 8 pixels of 64 channels (8 vectors of 8): it stages the tile's input halo
+// ((8 - 1) S + K rows x (TW - 1) S + K columns, 16-byte channel vectors, constant-0 or reflected
+// padding, channels past c as zeros) and the 64 channels' K x K weights in LDS in one round trip,
+// then each thread computes one channel vector of NP = 2 horizontally adjacent pixels, tap row
+// by tap row, keeping the row's input vectors in registers: every input byte is read from memory
+// once per tile instead of once per tap (K^2 times), and the weights once per workgroup.
+// Accumulation per pixel is bias, then the taps in row-major order (one fma each), as dw_body.
+// Halo rows have an odd pitch (in 128-byte pixels) so the two rows a 16-lane LDS pass reads hit
+// different banks.
+// GAP (p.gap): the channel sums of the tile's stored outputs (after rounding to T), over the
+// thread's pixels and then the tile's 32 pixel lanes in a fixed order, to part[b][tile][c].
+template <int K, int S> struct DwtShape {
+    static constexpr int TH = 8, TW = 8, NP = TW / 4;                   // tile; pixels per thread
+    static constexpr int HH = (TH - 1) * S + K, HW = (TW - 1) * S + K;  // halo
+    static constexpr int HWP = HW | 1;                                   // LDS row pitch in pixels (odd)
+    static constexpr int LDS = HH * HWP * 128 + K * K * 128;             // halo + weights
+};
+
+template <typename T, int K, int S, bool GAP>
+__device__ __forceinline__ void dwt_body(const sox_dwt_args& p, unsigned char* lds) {
+    typedef DwtShape<K, S> D;
+    constexpr int TH = D::TH, TW = D::TW, NP = D::NP, HH = D::HH, HW = D::HW, HWP = D::HWP;
+    constexpr int XR = (NP - 1) * S + K;  // input vectors of one tap row
+    typedef vec_t<T, 8> T8;
+    unsigned char* wl = lds + HH * HWP * 128;
+    const int t = threadIdx.x, cv = t & 7, pl = t >> 3;
+    const int tile = blockIdx.x, b = blockIdx.z;
+    const int c0 = blockIdx.y * 64 + cv * 8;  // this thread's channel vector
+    const bool cok = c0 < p.c;                // p.c % 8 == 0
+    const int ty0 = (tile / p.tiles_x) * TH, tx0 = (tile % p.tiles_x) * TW;
+    const int iy0 = ty0 * S - p.pt, ix0 = tx0 * S - p.pl;
+    const bool reflect = (p.flags & SOX_F_REFLECT) != 0;
+    const T* __restrict__ x = (const T*)p.x + (long)b * p.ih * p.iw * p.c;
+    // halo + weight loads, all issued before the first LDS write
+    constexpr int HL = (HH * HW + 31) / 32;
+    T8 hv[HL];
+#pragma unroll
+    for (int i = 0; i < HL; i++) {
+        const int h = pl + 32 * i;
+        const int hr = h / HW, hc = h - hr * HW;
+        const int iy = sox_src_index(iy0 + hr, p.ih, reflect), ix = sox_src_index(ix0 + hc, p.iw, reflect);
+        const bool ok = h < HH * HW && cok && iy >= 0 && ix >= 0;
+        hv[i] = *(const T8*)(x + (ok ? ((long)iy * p.iw + ix) * p.c + c0 : 0));
+        if (!ok) hv[i] = (T8)(T)0.0f;
+    }
+    T8 wv[(K * K + 31) / 32];
+#pragma unroll
+    for (int i = 0; i < (K * K + 31) / 32; i++) {
+        const int tap = min(pl + 32 * i, K * K - 1);
+        wv[i] = cok ? *(const T8*)((const T*)p.w + (long)tap * p.c + c0) : (T8)(T)0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < HL; i++) {
+        const int h = pl + 32 * i;
+        if (h < HH * HW) {
+            const int hr = h / HW, hc = h - hr * HW;
+            *(T8*)(lds + ((hr * HWP + hc) * 8 + cv) * 16) = hv[i];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < (K * K + 31) / 32; i++)
+        if (pl + 32 * i < K * K) *(T8*)(wl + ((pl + 32 * i) * 8 + cv) * 16) = wv[i];
+    __syncthreads();
+
+    // thread pixel lanes: row = pl % 8, column group = pl / 8 (NP adjacent pixels)
+    const int orow = pl & 7, ocol = (pl >> 3) * NP;
+    float acc[NP][8];
+    const bool hb = (p.flags & SOX_F_BIAS) && cok;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const float bv = hb ? p.bias[c0 + e] : 0.0f;
+#pragma unroll
+        for (int q = 0; q < NP; q++) acc[q][e] = bv;
+    }
+#pragma unroll 1
+    for (int ky = 0; ky < K; ky++) {
+        const unsigned char* row = lds + (((orow * S + ky) * HWP + ocol * S) * 8 + cv) * 16;
+        T8 xr[XR], wr[K];
+#pragma unroll
+        for (int j = 0; j < XR; j++) xr[j] = *(const T8*)(row + j * 128);
+#pragma unroll
+        for (int kx = 0; kx < K; kx++) wr[kx] = *(const T8*)(wl + ((ky * K + kx) * 8 + cv) * 16);
+#pragma unroll
+        for (int kx = 0; kx < K; kx++)
+#pragma unroll
+            for (int q = 0; q < NP; q++)
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    acc[q][e] = __builtin_fmaf(to_f(xr[q * S + kx][e]), to_f(wr[kx][e]), acc[q][e]);
+    }
+    const int act = (p.flags & SOX_F_ACT_MASK) >> SOX_F_ACT_SHIFT;
+    float gs[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) gs[e] = 0.0f;
+    const int oy = ty0 + orow;
+#pragma unroll
+    for (int q = 0; q < NP; q++) {
+        const int ox = tx0 + ocol + q;
+        if (!cok || oy >= p.oh || ox >= p.ow) continue;
+        const long o = (((long)b * p.oh + oy) * p.ow + ox) * p.c + c0;
+        T8 rv = (T8)(T)0.0f;
+        if (p.flags & SOX_F_RESIDUAL) rv = *(const T8*)((const T*)p.add + o);
+        T8 out;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            float v = acc[q][e];
+            if (p.flags & SOX_F_RESIDUAL) v = v + to_f(rv[e]);
+            out[e] = (T)sox_act(v, act);
+            if constexpr (GAP) gs[e] += to_f(out[e]);
+        }
+        *(T8*)((T*)p.y + o) = out;
+    }
+    if constexpr (GAP) {
+        // 32 pixel lanes per channel vector fold in a fixed binary tree through LDS (the halo is done)
+        __syncthreads();
+        float* red = (float*)lds;  // [pl][64 channels]
+#pragma unroll
+        for (int e = 0; e < 8; e++) red[pl * 64 + cv * 8 + e] = gs[e];
+        for (int st = 16; st > 0; st >>= 1) {
+            __syncthreads();
+            if (pl < st) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) red[pl * 64 + cv * 8 + e] += red[(pl + st) * 64 + cv * 8 + e];
+            }
+        }
+        __syncthreads();
+        if (pl == 0 && cok) {
+            float* dst = p.part + ((long)b * p.tiles_x * p.tiles_y + tile) * p.c + c0;
+#pragma unroll
+            for (int e = 0; e < 8; e++) dst[e] = red[cv * 8 + e];
+        }
+    }
+}
+
+#define SOX_DWT(TY, T, K, S)                                                                                   \
+    extern "C" __global__ void __launch_bounds__(256) sox_dwt_##TY##_k##K##s##S(sox_dwt_args p) {          \
+        __shared__ __attribute__((aligned(16))) unsigned char lds[DwtShape<K, S>::LDS];                     \
+        if (p.gap)                                                                                             \
+            dwt_body<T, K, S, true>(p, lds);                                                                   \
+        else                                                                                                   \
+            dwt_body<T, K, S, false>(p, lds);                                                                  \
+    }
+SOX_DWT(f16, half_t, 3, 1)
+SOX_DWT(f16, half_t, 3, 2)
+SOX_DWT(f16, half_t, 5, 1)
+SOX_DWT(f16, half_t, 5, 2)
+SOX_DWT(bf16, bf16_t, 3, 1)
+SOX_DWT(bf16, bf16_t, 3, 2)
+SOX_DWT(bf16, bf16_t, 5, 1)
+SOX_DWT(bf16, bf16_t, 5, 2)
+
 extern "C" __global__ void __launch_bounds__(256) sox_dw_f16_v(sox_dw_args p) { dw_body<half_t, 8>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_dw_bf16_v(sox_dw_args p) { dw_body<bf16_t, 8>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_dw_f16_s(sox_dw_args p) { dw_body<half_t, 1>(p); }

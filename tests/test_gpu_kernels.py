@@ -118,6 +118,76 @@ def test_depthwise_matches_oracle(hip, i, half):
     assert max_rel(got, want) < TOL[half]
 
 
+DW_TILE_CASES = [  # (c, k, s, h, w, pad_mode, act, residual)
+    (64, 3, 1, 16, 16, 0, "relu", False), (72, 3, 2, 240, 240, 0, "relu", False), (88, 3, 1, 37, 53, 1, "none", True),
+    (96, 5, 2, 120, 120, 0, "hardswish", False), (240, 5, 1, 60, 60, 0, "hardswish", False),
+    (16, 3, 2, 33, 17, 1, "relu", False), (576, 5, 1, 30, 30, 0, "hardswish", True), (120, 5, 2, 9, 23, 1, "swish", False)]
+
+
+@pytest.mark.parametrize("storage", ["f16", "bf16"])
+@pytest.mark.parametrize("case", DW_TILE_CASES, ids=[f"c{c[0]}k{c[1]}s{c[2]}_{c[3]}x{c[4]}" for c in DW_TILE_CASES])
+def test_depthwise_tiles_match_per_pixel_kernel(hip, case, storage, monkeypatch):
+    """The LDS-tile depthwise kernels (sox_dwt_*: channel tails, reflect padding, residual, ragged
+    tiles) give the per-pixel kernel's bits (same fma order per output) and meet the oracle."""
+    c, k, s, h, w, mode, act, res = case
+    from oracle.interp import _bf16
+    rnd = f16 if storage == "f16" else _bf16
+    x = rnd(synth.uniform(41, 1, (1, h, w, c), -1, 1))
+    wt = rnd(synth.uniform(41, 2, (c, 1, k, k), -0.5, 0.5))
+    b = synth.uniform(41, 3, (c,), -0.1, 0.1)
+    oh, ow = (h + 2 * (k // 2) - k) // s + 1, (w + 2 * (k // 2) - k) // s + 1
+    add = rnd(synth.uniform(41, 4, (1, oh, ow, c), -1, 1)) if res else None
+    plan, ins = conv_plan(x, wt, b, add, (s, s), (k // 2,) * 4, act, mode, 0.0, group=c)
+    g = hip.graph(plan, storage)
+    assert g.kernels == [f"sox_dwt_{storage}_k{k}s{s}"], g.kernels
+    g.release()
+    tiled = run(hip, plan, ins, storage)
+    monkeypatch.setenv("SIMDONNX_HIP_DW_DIRECT", "1")
+    g = hip.graph(plan, storage)
+    assert g.kernels[0].startswith(f"sox_dw_{storage}_v"), g.kernels
+    g.release()
+    direct = run(hip, plan, ins, storage)
+    assert np.array_equal(tiled, direct)
+    want = O.conv(x, wt, b, add, stride=(s, s), pads=(k // 2,) * 4, group=c, act=act, pad_mode=mode)
+    assert max_rel(tiled, want) < (2e-3 if storage == "f16" else 4e-3)
+
+
+@pytest.mark.parametrize("storage", ["f16", "bf16"])
+@pytest.mark.parametrize("case", [(240, 5, 1, 60, 60), (96, 5, 2, 120, 120), (576, 5, 1, 30, 30), (72, 3, 1, 44, 36)])
+def test_se_gap_partials_from_depthwise(hip, case, storage, monkeypatch):
+    """Depthwise conv -> SE gate -> x * gate -> 1x1 projection (the MobileNetV3 block tail): the
+    depthwise tiles write the gate's GAP partials (no gap_part dispatch), agreeing with the separate
+    GAP pass (SIMDONNX_HIP_NO_DW_GAP) to fp32 summation order and with the oracle on the plan."""
+    from oracle.interp import run_plan
+    c, k, s, h, w = case
+    r = max(8, (c // 4 + 4) // 8 * 8)
+    pb = PlanBuilder()
+    xv = pb.input((1, c, h, w), NHWC, "x")
+    d = pb.conv(xv, synth.uniform(42, 1, (c, 1, k, k), -0.5, 0.5), synth.uniform(42, 2, (c,), -0.1, 0.1),
+                stride=(s, s), pad=(k // 2,) * 4, group=c, act="hardswish", name="dw")
+    gate = pb.channel_gate(d, synth.uniform(42, 3, (r, c, 1, 1), -0.3, 0.3), synth.uniform(42, 4, (r,), -0.1, 0.1),
+                           synth.uniform(42, 5, (c, r, 1, 1), -0.3, 0.3), synth.uniform(42, 6, (c,), -0.1, 0.1),
+                           act1="relu", hard=True, alpha=1.0 / 6.0, beta=0.5, name="se")
+    m = pb.mul(d, gate, name="se_scale")
+    y = pb.conv(m, synth.uniform(42, 7, (48, c, 1, 1), -0.2, 0.2), synth.uniform(42, 8, (48,), -0.1, 0.1),
+                name="project")
+    plan = pb.build(y)
+    x = synth.uniform(42, 9, (1, h, w, c), -1, 1)
+    g = hip.graph(plan, storage)
+    names = [t[0] for t in g.dispatches]
+    assert "gap_part" not in names and names[0] == "depthwise", names
+    g.release()
+    fused = run(hip, plan, [x], storage)
+    monkeypatch.setenv("SIMDONNX_HIP_NO_DW_GAP", "1")
+    g = hip.graph(plan, storage)
+    assert "gap_part" in [t[0] for t in g.dispatches]
+    g.release()
+    sep = run(hip, plan, [x], storage)
+    assert max_rel(fused, sep) < (2e-3 if storage == "f16" else 1e-2)
+    want = run_plan(plan, [x], f16_storage=True if storage == "f16" else "bf16")  # the storage contract
+    assert max_rel(fused, want) < 2e-2
+
+
 @pytest.mark.parametrize("half,path", [(False, "direct"), (True, "gemm"), (True, "direct")],
                          ids=["f32", "f16-gemm", "f16-direct"])
 @pytest.mark.parametrize("i", range(int(G["ct_n"][0])))
