@@ -144,6 +144,62 @@ def bench_mfma_peak(iters: int = 4000, reps: int = 20):
                 ms=round(ms, 4), tflop_s=round(tf, 1), frac_of_peak=round(tf / PEAK_FP16_TFLOPS, 4))
 
 
+def bench_lds_peak(iters: int = 2000, reps: int = 10):
+    """Per-CU throughput of the two LDS paths the Gemm ring lives on (probe.hip, one 16-wave workgroup
+    per CU): ds_read_b128 with 16 KiB in flight per wave, and global_load_lds_dwordx4 from L2-resident
+    data. HIP events, median of `reps` launches after warm-up; bytes per cycle at the device's
+    reported peak clock (a lower bound on bytes per actual cycle)."""
+    import ctypes
+    from simdonnx_amd import build as B
+    from simdonnx_amd import native as N
+    from simdonnx_amd.backend import HipBackend
+    hip = HipBackend.default()
+    T = N.thin()
+    with open(os.path.join(B.BUILD, "probe.hsaco"), "rb") as f:
+        mod = hip.load_module(f.read())
+    cus, threads = hip.device.compute_units, 1024
+    clock_ghz = hip.device.clock_khz / 1e6
+    out, src = N.c_void_p(), N.c_void_p()
+    N.check(T.sox_malloc(ctypes.byref(out), cus * threads * 4), "probe output")
+    N.check(T.sox_malloc(ctypes.byref(src), 64 * 65536), "probe source")
+    stream = N.c_void_p()
+    N.check(T.sox_stream_create(ctypes.byref(stream)), "stream")
+    ev = [N.c_void_p(), N.c_void_p()]
+    for e in ev:
+        N.check(T.sox_event_create(ctypes.byref(e)), "event")
+    grid = (N.c_uint32 * 3)(cus, 1, 1)
+    block = (N.c_uint32 * 3)(threads, 1, 1)
+    res = {}
+    for name, per_round in (("sox_probe_lds_read", 16 * 16 * 1024), ("sox_probe_lds_dma", 16 * 8 * 1024)):
+        fn = N.c_void_p()
+        N.check(T.sox_module_function(ctypes.byref(fn), mod, name.encode()), "probe kernel")
+        args = struct.pack("<QQii", out.value, src.value, iters, 0)
+        buf = ctypes.create_string_buffer(args, len(args))
+        for _ in range(20):
+            N.check(T.sox_launch(fn, grid, block, 0, stream, buf, len(args)), "probe launch")
+        times = []
+        for _ in range(reps):
+            N.check(T.sox_event_record(ev[0], stream), "event")
+            N.check(T.sox_launch(fn, grid, block, 0, stream, buf, len(args)), "probe launch")
+            N.check(T.sox_event_record(ev[1], stream), "event")
+            N.check(T.sox_event_sync(ev[1]), "event")
+            ms = N.c_float()
+            N.check(T.sox_event_elapsed_ms(ctypes.byref(ms), ev[0], ev[1]), "event")
+            times.append(ms.value)
+        ms = statistics.median(times)
+        per_cu = per_round * iters / (ms * 1e-3)  # bytes / s per CU
+        res[name.replace("sox_probe_", "")] = dict(us=round(ms * 1e3, 1), tb_s=round(per_cu * cus / 1e12, 2),
+                                                    gb_s_per_cu=round(per_cu / 1e9, 1),
+                                                    bytes_per_clk_at_peak_clock=round(per_cu / (clock_ghz * 1e9), 1))
+    for e in ev:
+        T.sox_event_destroy(e)
+    T.sox_stream_destroy(stream)
+    T.sox_free(out)
+    T.sox_free(src)
+    return dict(workload=f"{cus} CUs x 16 waves: ds_read_b128 (16 KiB in flight per wave) and "
+                         f"global_load_lds_dwordx4 from L2, {iters} rounds", peak_clock_ghz=clock_ghz, **res)
+
+
 def bench_conv_large(steps: int, storage="f16"):
     """A large implicit-GEMM conv on the LDS-DMA ring: Conv3x3 s1 p1 + bias + ReLU, NHWC, 8x128x128,
     256 -> 256 channels (154.6 GFLOP), 16-bit storage, against the dense MFMA peak."""
@@ -574,7 +630,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-replay", action="store_true",
                     help="launch network dispatches one by one instead of replaying a HIP graph (profiler runs)")
-    ap.add_argument("--only", choices=["gemm", "gemm_bf16", "mfma_peak", "conv_large", "conv", "detector", "detector_fp32", "recognizer",
+    ap.add_argument("--only", choices=["gemm", "gemm_bf16", "mfma_peak", "lds_peak", "conv_large", "conv", "detector", "detector_fp32", "recognizer",
                                        "recognizer_bf16", "mobilenetv3", "copy", "ops",
                                        "recognizer_ctc", "image", "runner"],
                     help="run one workload only (profiling runs); prints its own JSON line")
@@ -586,7 +642,8 @@ def main():
     if args.only:
         fn = {"gemm": lambda: bench_gemm(args.steps, args.warmup), "conv": lambda: bench_conv(args.steps),
               "gemm_bf16": lambda: bench_gemm(args.steps, args.warmup, "bf16"),
-              "mfma_peak": lambda: bench_mfma_peak(), "conv_large": lambda: bench_conv_large(args.steps),
+              "mfma_peak": lambda: bench_mfma_peak(), "lds_peak": lambda: bench_lds_peak(),
+              "conv_large": lambda: bench_conv_large(args.steps),
               "copy": lambda: bench_copy(args.steps),
               "ops": lambda: {"ops": bench_ops(args.steps)},
               "recognizer_ctc": lambda: bench_recognizer_ctc(args.steps, not args.no_replay),
@@ -639,6 +696,10 @@ def main():
         log(f"mfma probe: {out['mfma_peak_probe']['tflop_s']} TFLOP/s")
     except Exception as e:
         out["mfma_peak_probe"] = {"error": repr(e)}
+    try:
+        out["lds_peak_probe"] = bench_lds_peak()
+    except Exception as e:
+        out["lds_peak_probe"] = {"error": repr(e)}
     try:
         out["conv_large_f16"] = bench_conv_large(50)
         log(f"large conv: {out['conv_large_f16']['tflop_s']} TFLOP/s")

@@ -457,6 +457,18 @@ typedef struct sox_mfma_probe_args {
     uint32_t seed;
 } sox_mfma_probe_args;
 
+/* LDS and LDS-DMA throughput probes (sox_probe_lds_read / sox_probe_lds_dma in probe.hip; measurement
+ * kernels, no counterpart in the reference). 1024 threads per workgroup (16 waves), one workgroup per
+ * CU. read: every wave keeps 16 ds_read_b128 of 1 KiB in flight per round; dma: every wave issues 8
+ * global_load_lds_dwordx4 of 1 KiB per round from a 64 KiB slice of src (L2-resident after the first
+ * round) into LDS. `iters` rounds; out gets one float per thread. */
+typedef struct sox_lds_probe_args {
+    float* out;
+    const void* src; /* >= 64 x 64 KiB (dma) */
+    int32_t iters;
+    int32_t pad_;
+} sox_lds_probe_args;
+
 #ifdef __cplusplus
 }
 #endif
