@@ -88,7 +88,7 @@ typedef struct sox_dw_args {
 } sox_dw_args;
 
 /*
- * Depthwise k x k over LDS tiles (k = 3 or 5, stride 1 or 2, 16-bit storage, zero or reflect pad):
+ * Depthwise k x k over LDS tiles (k = 3 or 5, stride 1 or 2, c % 8 == 0, zero or reflect pad):
  * a workgroup computes an output tile of 8 x 8 pixels of 64 channels
  * from the tile's input halo staged once in LDS. Grid (tiles_x * tiles_y, ceil(c / 64), n).
  * gap = 1: the workgroup also writes the channel sums of its stored (rounded) outputs,

@@ -201,32 +201,33 @@ extern "C" __global__ void __launch_bounds__(256) sox_dw_f16_v5(sox_dw_args p) {
 extern "C" __global__ void __launch_bounds__(256) sox_dw_bf16_v5(sox_dw_args p) { dw_body_k<bf16_t, 8, 5>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_dw_f32_v3(sox_dw_args p) { dw_body_k<float, 4, 3>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_dw_f32_v5(sox_dw_args p) { dw_body_k<float, 4, 5>(p); }
-// Depthwise K x K, stride S, over LDS tiles (16-bit storage). A workgroup owns an output tile of
+// Depthwise K x K, stride S, over LDS tiles (any storage type). A workgroup owns an output tile of
 // 8 x 8 pixels of 64 channels (8 vectors of 8): it stages the tile's input halo
-// ((8 - 1) S + K rows x (TW - 1) S + K columns, 16-byte channel vectors, constant-0 or reflected
+// ((8 - 1) S + K rows x (TW - 1) S + K columns, 8-channel vectors, constant-0 or reflected
 // padding, channels past c as zeros) and the 64 channels' K x K weights in LDS in one round trip,
 // then each thread computes one channel vector of NP = 2 horizontally adjacent pixels, tap row
 // by tap row, keeping the row's input vectors in registers: every input byte is read from memory
 // once per tile instead of once per tap (K^2 times), and the weights once per workgroup.
 // Accumulation per pixel is bias, then the taps in row-major order (one fma each), as dw_body.
-// Halo rows have an odd pitch (in 128-byte pixels) so the two rows a 16-lane LDS pass reads hit
-// different banks.
+// Halo rows have a pitch of an odd number of 128-byte units so the two rows a 16-lane LDS pass reads
+// hit different banks.
 // GAP (p.gap): the channel sums of the tile's stored outputs (after rounding to T), over the
 // thread's pixels and then the tile's 32 pixel lanes in a fixed order, to part[b][tile][c].
-template <int K, int S> struct DwtShape {
+template <typename T, int K, int S> struct DwtShape {
     static constexpr int TH = 8, TW = 8, NP = TW / 4;                   // tile; pixels per thread
     static constexpr int HH = (TH - 1) * S + K, HW = (TW - 1) * S + K;  // halo
-    static constexpr int HWP = HW | 1;                                   // LDS row pitch in pixels (odd)
-    static constexpr int LDS = HH * HWP * 128 + K * K * 128;             // halo + weights
+    static constexpr int VB = 8 * sizeof(T), PB = 8 * VB;              // bytes of a channel vector, a pixel
+    static constexpr int RP = ((HW * PB / 128) | 1) * 128;              // halo row pitch: an odd number of 128 B
+    static constexpr int LDS = HH * RP + K * K * PB;                     // halo + weights
 };
 
 template <typename T, int K, int S, bool GAP>
 __device__ __forceinline__ void dwt_body(const sox_dwt_args& p, unsigned char* lds) {
-    typedef DwtShape<K, S> D;
-    constexpr int TH = D::TH, TW = D::TW, NP = D::NP, HH = D::HH, HW = D::HW, HWP = D::HWP;
+    typedef DwtShape<T, K, S> D;
+    constexpr int TH = D::TH, TW = D::TW, NP = D::NP, HH = D::HH, HW = D::HW, VB = D::VB, PB = D::PB, RP = D::RP;
     constexpr int XR = (NP - 1) * S + K;  // input vectors of one tap row
     typedef vec_t<T, 8> T8;
-    unsigned char* wl = lds + HH * HWP * 128;
+    unsigned char* wl = lds + HH * RP;
     const int t = threadIdx.x, cv = t & 7, pl = t >> 3;
     const int tile = blockIdx.x, b = blockIdx.z;
     const int c0 = blockIdx.y * 64 + cv * 8;  // this thread's channel vector
@@ -258,12 +259,12 @@ __device__ __forceinline__ void dwt_body(const sox_dwt_args& p, unsigned char* l
         const int h = pl + 32 * i;
         if (h < HH * HW) {
             const int hr = h / HW, hc = h - hr * HW;
-            *(T8*)(lds + ((hr * HWP + hc) * 8 + cv) * 16) = hv[i];
+            *(T8*)(lds + hr * RP + hc * PB + cv * VB) = hv[i];
         }
     }
 #pragma unroll
     for (int i = 0; i < (K * K + 31) / 32; i++)
-        if (pl + 32 * i < K * K) *(T8*)(wl + ((pl + 32 * i) * 8 + cv) * 16) = wv[i];
+        if (pl + 32 * i < K * K) *(T8*)(wl + (pl + 32 * i) * PB + cv * VB) = wv[i];
     __syncthreads();
 
     // thread pixel lanes: row = pl % 8, column group = pl / 8 (NP adjacent pixels)
@@ -278,12 +279,12 @@ __device__ __forceinline__ void dwt_body(const sox_dwt_args& p, unsigned char* l
     }
 #pragma unroll 1
     for (int ky = 0; ky < K; ky++) {
-        const unsigned char* row = lds + (((orow * S + ky) * HWP + ocol * S) * 8 + cv) * 16;
+        const unsigned char* row = lds + (orow * S + ky) * RP + ocol * S * PB + cv * VB;
         T8 xr[XR], wr[K];
 #pragma unroll
-        for (int j = 0; j < XR; j++) xr[j] = *(const T8*)(row + j * 128);
+        for (int j = 0; j < XR; j++) xr[j] = *(const T8*)(row + j * PB);
 #pragma unroll
-        for (int kx = 0; kx < K; kx++) wr[kx] = *(const T8*)(wl + ((ky * K + kx) * 8 + cv) * 16);
+        for (int kx = 0; kx < K; kx++) wr[kx] = *(const T8*)(wl + (ky * K + kx) * PB + cv * VB);
 #pragma unroll
         for (int kx = 0; kx < K; kx++)
 #pragma unroll
@@ -338,7 +339,7 @@ __device__ __forceinline__ void dwt_body(const sox_dwt_args& p, unsigned char* l
 
 #define SOX_DWT(TY, T, K, S)                                                                                   \
     extern "C" __global__ void __launch_bounds__(256) sox_dwt_##TY##_k##K##s##S(sox_dwt_args p) {          \
-        __shared__ __attribute__((aligned(16))) unsigned char lds[DwtShape<K, S>::LDS];                     \
+        __shared__ __attribute__((aligned(16))) unsigned char lds[DwtShape<T, K, S>::LDS];                  \
         if (p.gap)                                                                                             \
             dwt_body<T, K, S, true>(p, lds);                                                                   \
         else                                                                                                   \
@@ -352,6 +353,10 @@ SOX_DWT(bf16, bf16_t, 3, 1)
 SOX_DWT(bf16, bf16_t, 3, 2)
 SOX_DWT(bf16, bf16_t, 5, 1)
 SOX_DWT(bf16, bf16_t, 5, 2)
+SOX_DWT(f32, float, 3, 1)
+SOX_DWT(f32, float, 3, 2)
+SOX_DWT(f32, float, 5, 1)
+SOX_DWT(f32, float, 5, 2)
 
 extern "C" __global__ void __launch_bounds__(256) sox_dw_f16_v(sox_dw_args p) { dw_body<half_t, 8>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_dw_bf16_v(sox_dw_args p) { dw_body<bf16_t, 8>(p); }
