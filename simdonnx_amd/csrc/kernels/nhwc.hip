@@ -53,9 +53,14 @@ template <typename T> SOX_DEV void keep_in_vgprs(T& v) {
         u2v u = __builtin_bit_cast(u2v, v);
         asm volatile("" : "+v"(u));
         v = __builtin_bit_cast(T, u);
-    } else {
-        static_assert(sizeof(T) == 16, "2, 4, 8 or 16-byte elements");
+    } else if constexpr (sizeof(T) == 16) {
         u4v u = __builtin_bit_cast(u4v, v);
+        asm volatile("" : "+v"(u));
+        v = __builtin_bit_cast(T, u);
+    } else {
+        static_assert(sizeof(T) == 32, "2, 4, 8, 16 or 32-byte elements");
+        typedef unsigned u8v __attribute__((ext_vector_type(8)));
+        u8v u = __builtin_bit_cast(u8v, v);
         asm volatile("" : "+v"(u));
         v = __builtin_bit_cast(T, u);
     }
@@ -235,8 +240,29 @@ __device__ __forceinline__ void dwt_body(const sox_dwt_args& p, unsigned char* l
     const int ty0 = (tile / p.tiles_x) * TH, tx0 = (tile % p.tiles_x) * TW;
     const int iy0 = ty0 * S - p.pt, ix0 = tx0 * S - p.pl;
     const bool reflect = (p.flags & SOX_F_REFLECT) != 0;
+    // every load that does not depend on the halo goes out first and stays in registers (else the
+    // compiler issues each next to its use, one more memory round trip each)
+    T8 wv[(K * K + 31) / 32];
+#pragma unroll
+    for (int i = 0; i < (K * K + 31) / 32; i++) {
+        const int tap = min(pl + 32 * i, K * K - 1);
+        wv[i] = cok ? *(const T8*)((const T*)p.w + (long)tap * p.c + c0) : (T8)(T)0.0f;
+    }
+    const bool hb = (p.flags & SOX_F_BIAS) && cok;
+    float bv[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) bv[e] = hb ? p.bias[c0 + e] : 0.0f;
+    const int orow = pl & 7, ocol = (pl >> 3) * NP;  // thread pixel lanes: row, first of NP columns
+    const int oy = ty0 + orow;
+    T8 rv[NP];
+#pragma unroll
+    for (int q = 0; q < NP; q++) {
+        const int ox = min(tx0 + ocol + q, p.ow - 1);
+        const long o = (((long)b * p.oh + min(oy, p.oh - 1)) * p.ow + ox) * p.c + c0;
+        rv[q] = (p.flags & SOX_F_RESIDUAL) && cok ? *(const T8*)((const T*)p.add + o) : (T8)(T)0.0f;
+    }
+    // the halo loads, issued with those before the first wait
     const T* __restrict__ x = (const T*)p.x + (long)b * p.ih * p.iw * p.c;
-    // halo + weight loads, all issued before the first LDS write
     constexpr int HL = (HH * HW + 31) / 32;
     T8 hv[HL];
 #pragma unroll
@@ -248,12 +274,12 @@ __device__ __forceinline__ void dwt_body(const sox_dwt_args& p, unsigned char* l
         hv[i] = *(const T8*)(x + (ok ? ((long)iy * p.iw + ix) * p.c + c0 : 0));
         if (!ok) hv[i] = (T8)(T)0.0f;
     }
-    T8 wv[(K * K + 31) / 32];
 #pragma unroll
-    for (int i = 0; i < (K * K + 31) / 32; i++) {
-        const int tap = min(pl + 32 * i, K * K - 1);
-        wv[i] = cok ? *(const T8*)((const T*)p.w + (long)tap * p.c + c0) : (T8)(T)0.0f;
-    }
+    for (int i = 0; i < (K * K + 31) / 32; i++) keep_in_vgprs(wv[i]);
+#pragma unroll
+    for (int e = 0; e < 8; e++) keep_in_vgprs(bv[e]);
+#pragma unroll
+    for (int q = 0; q < NP; q++) keep_in_vgprs(rv[q]);
 #pragma unroll
     for (int i = 0; i < HL; i++) {
         const int h = pl + 32 * i;
@@ -267,16 +293,11 @@ __device__ __forceinline__ void dwt_body(const sox_dwt_args& p, unsigned char* l
         if (pl + 32 * i < K * K) *(T8*)(wl + (pl + 32 * i) * PB + cv * VB) = wv[i];
     __syncthreads();
 
-    // thread pixel lanes: row = pl % 8, column group = pl / 8 (NP adjacent pixels)
-    const int orow = pl & 7, ocol = (pl >> 3) * NP;
     float acc[NP][8];
-    const bool hb = (p.flags & SOX_F_BIAS) && cok;
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const float bv = hb ? p.bias[c0 + e] : 0.0f;
+    for (int e = 0; e < 8; e++)
 #pragma unroll
-        for (int q = 0; q < NP; q++) acc[q][e] = bv;
-    }
+        for (int q = 0; q < NP; q++) acc[q][e] = bv[e];
 #pragma unroll 1
     for (int ky = 0; ky < K; ky++) {
         const unsigned char* row = lds + (orow * S + ky) * RP + ocol * S * PB + cv * VB;
@@ -297,19 +318,16 @@ __device__ __forceinline__ void dwt_body(const sox_dwt_args& p, unsigned char* l
     float gs[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) gs[e] = 0.0f;
-    const int oy = ty0 + orow;
 #pragma unroll
     for (int q = 0; q < NP; q++) {
         const int ox = tx0 + ocol + q;
         if (!cok || oy >= p.oh || ox >= p.ow) continue;
         const long o = (((long)b * p.oh + oy) * p.ow + ox) * p.c + c0;
-        T8 rv = (T8)(T)0.0f;
-        if (p.flags & SOX_F_RESIDUAL) rv = *(const T8*)((const T*)p.add + o);
         T8 out;
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             float v = acc[q][e];
-            if (p.flags & SOX_F_RESIDUAL) v = v + to_f(rv[e]);
+            if (p.flags & SOX_F_RESIDUAL) v = v + to_f(rv[q][e]);
             out[e] = (T)sox_act(v, act);
             if constexpr (GAP) gs[e] += to_f(out[e]);
         }
@@ -357,6 +375,7 @@ SOX_DWT(f32, float, 3, 1)
 SOX_DWT(f32, float, 3, 2)
 SOX_DWT(f32, float, 5, 1)
 SOX_DWT(f32, float, 5, 2)
+
 
 extern "C" __global__ void __launch_bounds__(256) sox_dw_f16_v(sox_dw_args p) { dw_body<half_t, 8>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_dw_bf16_v(sox_dw_args p) { dw_body<bf16_t, 8>(p); }
