@@ -670,8 +670,6 @@ extern "C" __global__ void __launch_bounds__(256) sox_se_fc1(sox_se_args p) {
             const int j = min(wave * 4 + rq + 16 * u, p.r - 1);
             wv[u] = *(const float4v*)(p.w1 + (long)j * p.c + c0 + min(4 * sub, cn - 4));
         }
-#pragma unroll
-        for (int u = 0; u < SE_FC1_U; u++) keep_in_vgprs(wv[u]);
     }
     {
         const int ch = t % SE_CG, ph = t / SE_CG;
@@ -680,6 +678,11 @@ extern "C" __global__ void __launch_bounds__(256) sox_se_fc1(sox_se_args p) {
             strided_foreach<16>(p.part + (long)b * p.chunks * p.c + c0 + ch, (long)ph * p.c, (long)p.chunks * p.c,
                                 4L * p.c, [&](long, float v) { acc += v; });
         red[t] = acc;
+    }
+    // the W1 loads stay ahead of the barrier (issued with the first partials, one wait for both)
+    if (pre) {
+#pragma unroll
+        for (int u = 0; u < SE_FC1_U; u++) keep_in_vgprs(wv[u]);
     }
     __syncthreads();
     if (t < SE_CG) mean[t] = ((red[t] + red[t + 64]) + (red[t + 128] + red[t + 192])) * (1.0f / p.hw);
@@ -738,24 +741,46 @@ __device__ __forceinline__ void se_fc2_body(const sox_se_args& p) {
     const bool pre = p.r <= 256 && (!fold || p.wn <= 256);
     const T* __restrict__ ws = (const T*)p.wsrc;
     float w2v[4];
-    T wsv[4];
+    // the consumer's weights as zero-extended 32-bit words: 16-bit values would be packed in pairs,
+    // which waits for their loads right away
+    typedef std::conditional_t<sizeof(T) == 2, unsigned short, unsigned> WU;
+    unsigned wsv[4];
     if (pre) {
 #pragma unroll
         for (int u = 0; u < 4; u++) w2v[u] = p.w2[(long)chc * p.r + min(lane + 64 * u, p.r - 1)];
         if (fold) {
 #pragma unroll
-            for (int u = 0; u < 4; u++) wsv[u] = ws[(long)min(lane + 64 * u, p.wn - 1) * p.wk + chc];
+            for (int u = 0; u < 4; u++) wsv[u] = ((const WU*)ws)[(long)min(lane + 64 * u, p.wn - 1) * p.wk + chc];
+        }
+    }
+    const float* part = p.hid + (long)b * p.groups * p.r;
+    if (pre && p.groups <= 16 && p.r <= (int)blockDim.x) {
+        // one hidden unit per thread, its <= 16 group partials in one batch with the weights: no loop,
+        // so nothing makes the compiler wait for the weight loads before it (a loop preheader would)
+        const int k = min(t, p.r - 1);
+        float pv[16];
+#pragma unroll
+        for (int gi = 0; gi < 16; gi++) pv[gi] = part[(long)min(gi, p.groups - 1) * p.r + k];
+        float s = (p.flags & 1) ? p.b1[k] : 0.0f;
+#pragma unroll
+        for (int gi = 0; gi < 16; gi++)
+            if (gi < p.groups) s += pv[gi];
+        if (t < p.r) h[k] = (p.flags & 4) ? fmaxf(s, 0.0f) : s;
+    } else {
+        for (int k = t; k < p.r; k += blockDim.x) {
+            float s = (p.flags & 1) ? p.b1[k] : 0.0f;
+            strided_foreach<16>(part + k, 0, (long)p.groups * p.r, p.r, [&](long, float v) { s += v; });
+            h[k] = (p.flags & 4) ? fmaxf(s, 0.0f) : s;
+        }
+    }
+    // the weight loads stay ahead of the barrier (issued with the first partials, one wait for all)
+    if (pre) {
+        if (fold) {
 #pragma unroll
             for (int u = 0; u < 4; u++) keep_in_vgprs(wsv[u]);
         }
 #pragma unroll
         for (int u = 0; u < 4; u++) keep_in_vgprs(w2v[u]);
-    }
-    const float* part = p.hid + (long)b * p.groups * p.r;
-    for (int k = t; k < p.r; k += blockDim.x) {
-        float s = (p.flags & 1) ? p.b1[k] : 0.0f;
-        strided_foreach<16>(part + k, 0, (long)p.groups * p.r, p.r, [&](long, float v) { s += v; });
-        h[k] = (p.flags & 4) ? fmaxf(s, 0.0f) : s;
     }
     __syncthreads();
     if (ch >= p.c) return;
@@ -777,7 +802,7 @@ __device__ __forceinline__ void se_fc2_body(const sox_se_args& p) {
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 const int n = lane + 64 * u;
-                if (n < p.wn) wd[(long)n * p.wk + ch] = (T)(to_f(wsv[u]) * gate);
+                if (n < p.wn) wd[(long)n * p.wk + ch] = (T)(to_f(__builtin_bit_cast(T, (WU)wsv[u])) * gate);
             }
         } else {
             strided_foreach<4>(ws + ch, (long)lane * p.wk, (long)p.wn * p.wk, 64L * p.wk,
