@@ -457,6 +457,26 @@ typedef struct sox_mfma_probe_args {
     uint32_t seed;
 } sox_mfma_probe_args;
 
+/*
+ * LayerNorm -> qkv Gemm -> attention of a transformer block in one dispatch (qkv_attn.hip), one 576-thread
+ * workgroup per (image, head): images of t <= 96 tokens of dim = heads * 32 channels, ViT-style packed qkv
+ * (the SVTR mixer). For head h of image b:
+ *   q, k, v = LN(x) . Wqkv[cols of h] + bqkv  with the LayerNorm folded: wqkv gamma-scaled, bqkv = b + beta W,
+ *             cqkv = the column sums of wqkv as rounded (the sox_gemm_ln_* epilogue), rounded to the storage type;
+ *   o[b][:, h] = softmax(q k^T * scale) v  (the sox_attn_*_mfma kernel), rounded.
+ * wqkv is GemmNK-packed [3 dim][kpad]; the head's qkv columns never leave LDS.
+ */
+typedef struct sox_qkvattn_args {
+    const void* x;      /* [n][t][dim] */
+    const void* wqkv;
+    const float* bqkv;  /* [3 dim] (flags bit1) */
+    const float* cqkv;  /* [3 dim] */
+    void* o;            /* [n][t][heads][32] */
+    int32_t n, t, kpad;
+    float eps, scale;
+    int32_t flags;
+} sox_qkvattn_args;
+
 /* LDS and LDS-DMA throughput probes (sox_probe_lds_read / sox_probe_lds_dma in probe.hip; measurement
  * kernels, no counterpart in the reference). 1024 threads per workgroup (16 waves), one workgroup per
  * CU. read: every wave keeps 16 ds_read_b128 of 1 KiB in flight per round; dma: every wave issues 8

@@ -168,3 +168,57 @@ def test_fused_mlp_not_taken_when_hidden_is_read_twice(hip):
         s.set_input(xin)
         got = s.run().copy()
     assert max_rel(got, run_plan(plan, [xin], f16_storage=True)) < 2e-2
+
+
+def _attention_block_plan(n, t, dim=192, heads=6, seed=93):
+    """x [n, t, dim] -> LayerNorm -> qkv Gemm -> attention -> proj Gemm -> + x: the first half of an SVTR
+    mixer block, as graphs.svtr builds it."""
+    from simdonnx_amd import synth
+    from simdonnx_amd.plan import PlanBuilder
+    pb = PlanBuilder()
+    x = pb.input((n, t, dim), None, "x")
+    hn = pb.layer_norm(x, 1.0 + synth.uniform(seed, 1, (dim,), -0.1, 0.1), synth.uniform(seed, 2, (dim,), -0.1, 0.1),
+                       1e-6, name="ln")
+    qkv = pb.gemm(hn, synth.normal(seed, 3, (dim, 3 * dim), 0.05), synth.uniform(seed, 4, (3 * dim,), -0.1, 0.1),
+                  name="qkv")
+    d = dim // heads
+    att = pb.attention(qkv, heads, d, d ** -0.5, name="attn")
+    proj = pb.gemm(att, synth.normal(seed, 5, (dim, dim), 0.05), synth.uniform(seed, 6, (dim,), -0.1, 0.1), name="proj")
+    plan = pb.build(pb.add(x, proj, name="res"))
+    return plan, synth.normal(seed, 7, (n, t, dim), 1.0)
+
+
+@pytest.mark.parametrize("n,t,storage", [(32, 80, "f16"), (3, 96, "f16"), (4, 17, "f16"), (7, 80, "bf16"),
+                                         (5, 33, "bf16")])
+def test_qkv_attention_matches_unfused_and_oracle(hip, n, t, storage, monkeypatch):
+    """LayerNorm -> qkv Gemm -> attention runs as one dispatch per (image, head) (qkv_attn.hip) whose
+    output, through the proj Gemm and residual Add, equals the unfused path's (SIMDONNX_HIP_NO_ATTN_FUSE)
+    bit for bit, and the oracle within the 16-bit contract. t = 96 is the largest fused token count; 17
+    and 33 leave ragged query blocks, key steps and row blocks."""
+    plan, xin = _attention_block_plan(n, t)
+    g = hip.graph(plan, storage)
+    assert [d[0] for d in g.dispatches] == ["qkv_attn", "gemm"]
+    assert g.kernels[0] == f"sox_qkvattn_{storage}_d192"
+    with HipInferenceSession(g) as s:
+        s.set_input(xin)
+        fused = s.run().copy()
+    monkeypatch.setenv("SIMDONNX_HIP_NO_ATTN_FUSE", "1")
+    g2 = hip.graph(plan, storage)
+    assert [d[0] for d in g2.dispatches] == ["gemm_ln", "attn", "gemm"]
+    with HipInferenceSession(g2) as s:
+        s.set_input(xin)
+        unfused = s.run().copy()
+    assert fused.dtype == unfused.dtype and fused.tobytes() == unfused.tobytes()
+    want = run_plan(plan, [xin], f16_storage="bf16" if storage == "bf16" else True)
+    assert max_rel(fused, want) < 2e-2
+
+
+def test_qkv_attention_not_fused_past_96_tokens(hip):
+    """t = 97 does not fit the fused kernel's LDS rows: the three dispatches run and match the oracle."""
+    plan, xin = _attention_block_plan(2, 97)
+    g = hip.graph(plan, True)
+    assert [d[0] for d in g.dispatches] == ["gemm_ln", "attn", "gemm"]
+    with HipInferenceSession(g) as s:
+        s.set_input(xin)
+        got = s.run().copy()
+    assert max_rel(got, run_plan(plan, [xin], f16_storage=True)) < 2e-2
