@@ -433,7 +433,10 @@ typedef struct sox_nhwc2img_args {
 } sox_nhwc2img_args;
 
 /* Fused transformer MLP (mlp.hip): y = act2(GELU(rstd (x . W1 - mean c1) + b1) . W2 + b2 + res), the
- * LayerNorm folded into W1 / b1 / c1 at graph creation. One 512-thread workgroup per 32 rows. */
+ * LayerNorm folded into W1 / b1 / c1 at graph creation. sox_mlp_*: one 512-thread workgroup per 32 rows.
+ * Split form for grids that would leave CUs idle: sox_mlpq_* runs one 512-thread workgroup per (32 rows,
+ * part of the hidden width), each writing its part's fc2 sums to `part`; sox_mlp_sum_* (256 threads, 4
+ * outputs each) then adds b2, the parts in order and the residual. */
 typedef struct sox_mlp_args {
     const void* x;      /* fp16 [m][k1] */
     const void* w1;     /* fp16 gamma-scaled [k1][h] in 32x32x16 fragment order (32 columns x 16 k per KiB) */
@@ -446,6 +449,8 @@ typedef struct sox_mlp_args {
     int32_t m, k1, h, n2, ldw1, ldw2;
     float eps;
     int32_t flags;      /* bit0 b2, bit1 residual, act2 << 4 */
+    float* part;        /* sox_mlpq_* / sox_mlp_sum_*: fp32 [parts][m][n2], fc2 over each part of the hidden width */
+    int32_t parts, pad_;
 } sox_mlp_args;
 
 /* Matrix-core rate probe (sox_probe_mfma_f16 in the Gemm code object; a measurement kernel, no

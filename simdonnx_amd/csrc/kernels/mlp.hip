@@ -137,6 +137,159 @@ __device__ __forceinline__ void mlp_body(const sox_mlp_args& p) {
     }
 }
 
+// ------------------------------------------------------------------------------------------------
+// Split form: workgroup (row block of 32, part q of Q) takes hidden blocks q HB/Q .. (q + 1) HB/Q - 1
+// and fc2's k-steps over those hidden columns, so a grid of M/32 x Q workgroups shares the weights'
+// traffic (each workgroup streams 1/Q of W1 and W2 through its CU) and fills the GPU where M/32 alone
+// would not. fc2's part sums leave as fp32 (part[q][m][n2]); sox_mlp_sum_* adds them, b2 and the residual.
+//  phase 0: the part's W1 fragments (one hidden block per wave), its c1 / b1, the wave's W2 fragments and
+//           the 32 x rows (into LDS, so the hidden waves read their A fragments once per CU) all issued
+//           before the first wait.
+//  phase 1: as sox_mlp_*: the LayerNorm from the row sums, one 32 x 32 hidden block per wave, GELU,
+//           rounding to the storage type, into LDS.
+//  phase 2: wave w < N2 / 32: output block w over the part's hidden k-steps (two accumulator chains).
+template <typename T, int KS1, int HB, int KS2, int Q>  // storage type, K1 / 16, H / 32, H / 16, parts
+__device__ __forceinline__ void mlp_part_body(const sox_mlp_args& p) {
+    typedef vec_t<T, 8> T8;
+    typedef vec_t<T, 4> T4;
+    typedef vec_t<T, 2> T2;
+    constexpr int HBQ = HB / Q, KQ = KS2 / Q, K1 = KS1 * 16;
+    static_assert(HB % Q == 0 && HBQ <= 8 && KQ % 2 == 0, "a part is at most one hidden block per wave");
+    constexpr int HROW = HBQ * 32 * 2 + 16;   // LDS bytes per hidden row (16 bytes of padding)
+    constexpr int XP = K1 + 8;                // x row pitch in LDS, in elements
+    constexpr int XC = 32 * K1 / 8;           // 16-byte chunks of the 32 x rows
+    constexpr int XI = (XC + 511) / 512;
+    __shared__ __attribute__((aligned(16))) unsigned char hs[32 * HROW];
+    __shared__ __attribute__((aligned(16))) T xs[32 * XP];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, l32 = lane & 31, hl = lane >> 5;
+    const int q = blockIdx.x % Q, m0 = (blockIdx.x / Q) * 32;
+    const T* __restrict__ X = (const T*)p.x;
+    const T* __restrict__ W1 = (const T*)p.w1;
+    const T* __restrict__ W2 = (const T*)p.w2;
+    const bool hid_wave = wave < HBQ, out_wave = wave * 32 < p.n2;
+    const int jb = q * HBQ + wave;  // the wave's hidden block
+
+    // ---- phase 0: every load of the workgroup in flight before the first wait ----
+    T8 b[KS1], w2f[KQ];
+    float4v c4[4], b4[4];
+    if (hid_wave) {
+#pragma unroll
+        for (int s = 0; s < KS1; s++) b[s] = *(const T8*)(W1 + (((long)jb * KS1 + s) * 64 + lane) * 8);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int n = jb * 32 + 8 * i + 4 * hl;
+            c4[i] = *(const float4v*)(p.c1 + n);
+            b4[i] = *(const float4v*)(p.b1 + n);
+        }
+    }
+    if (out_wave) {
+#pragma unroll
+        for (int s = 0; s < KQ; s++) w2f[s] = *(const T8*)(W2 + (((long)wave * KS2 + q * KQ + s) * 64 + lane) * 8);
+    }
+    {
+        T8 xv[XI];
+#pragma unroll
+        for (int u = 0; u < XI; u++) {
+            const int i = t + 512 * u, r = i / (K1 / 8), c = i - r * (K1 / 8);
+            if (i < XC) xv[u] = *(const T8*)(X + (long)min(m0 + r, p.m - 1) * p.k1 + 8 * c);
+        }
+#pragma unroll
+        for (int u = 0; u < XI; u++) {
+            const int i = t + 512 * u, r = i / (K1 / 8), c = i - r * (K1 / 8);
+            if (i < XC) *(T8*)(xs + r * XP + 8 * c) = xv[u];
+        }
+    }
+    __syncthreads();
+
+    // ---- phase 1: hidden = GELU(rstd (x . W1 - mean c1) + b1), the part's columns ----
+    if (hid_wave) {
+        const T* ar = xs + l32 * XP + 8 * hl;
+        float s1 = 0.0f, s2 = 0.0f;
+        float16v acc = (float16v)0.0f;
+        const T2 one = {(T)1.0f, (T)1.0f};
+#pragma unroll
+        for (int s = 0; s < KS1; s++) {
+            const T8 a = *(const T8*)(ar + 16 * s);
+            acc = mfma32x32x16(b[s], a, acc);
+#pragma unroll
+            for (int h = 0; h < 4; h++) {
+                const T2 v = {a[2 * h], a[2 * h + 1]};
+                if constexpr (std::is_same<T, half_t>::value) {
+                    s1 = __builtin_amdgcn_fdot2(v, one, s1, false);
+                    s2 = __builtin_amdgcn_fdot2(v, v, s2, false);
+                } else {
+                    s1 = __builtin_amdgcn_fdot2_f32_bf16(v, one, s1, false);
+                    s2 = __builtin_amdgcn_fdot2_f32_bf16(v, v, s2, false);
+                }
+            }
+        }
+        s1 += __shfl_xor(s1, 32);
+        s2 += __shfl_xor(s2, 32);
+        const float inv_k = 1.0f / (float)K1;
+        const float mean = s1 * inv_k;
+        const float rstd = __builtin_amdgcn_rsqf(fmaxf(s2 * inv_k - mean * mean, 0.0f) + p.eps);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            T4 hv;
+#pragma unroll
+            for (int e = 0; e < 4; e++) hv[e] = (T)gelu_fast(rstd * (acc[4 * i + e] - mean * c4[i][e]) + b4[i][e]);
+            *(T4*)(hs + l32 * HROW + (wave * 32 + 8 * i + 4 * hl) * 2) = hv;
+        }
+    }
+    __syncthreads();  // every hidden column of the part written
+
+    // ---- phase 2: the part's share of hidden . W2, fp32 ----
+    if (!out_wave) return;
+    float16v acc = (float16v)0.0f, acc_o = (float16v)0.0f;
+    const unsigned char* hr = hs + l32 * HROW + 16 * hl;
+#pragma unroll
+    for (int s = 0; s < KQ; s += 2) {
+        acc = mfma32x32x16(w2f[s], *(const T8*)(hr + 32 * s), acc);
+        acc_o = mfma32x32x16(w2f[s + 1], *(const T8*)(hr + 32 * (s + 1)), acc_o);
+    }
+    const int m = m0 + l32;
+    if (m >= p.m) return;
+    float* dst = p.part + ((long)q * p.m + m) * p.n2 + wave * 32 + 4 * hl;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float4v v;
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[e] = acc[4 * i + e] + acc_o[4 * i + e];
+        *(float4v*)(dst + 8 * i) = v;
+    }
+}
+
+// y = act2(b2 + part[0] + ... + part[parts - 1] + res), four consecutive outputs per thread
+template <typename T>
+__device__ __forceinline__ void mlp_sum_body(const sox_mlp_args& p) {
+    typedef vec_t<T, 4> T4;
+    const long i = ((long)blockIdx.x * blockDim.x + threadIdx.x) * 4, total = (long)p.m * p.n2;
+    if (i >= total) return;
+    const int n = (int)(i % p.n2);
+    float4v v = (p.flags & 1) ? *(const float4v*)(p.b2 + n) : (float4v)0.0f;
+    T4 r = {};
+    if (p.flags & 2) r = *(const T4*)((const T*)p.res + i);
+    float4v pv[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+        if (q < p.parts) pv[q] = *(const float4v*)(p.part + q * total + i);
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+        if (q < p.parts) v += pv[q];
+    const int act = (p.flags >> 4) & 15;
+    T4 out;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        float x = v[e];
+        if (p.flags & 2) x += (float)r[e];
+        out[e] = (T)sox_act(x, act);
+    }
+    *(T4*)((T*)p.y + i) = out;
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_mlp_sum_f16(sox_mlp_args p) { mlp_sum_body<half_t>(p); }
+extern "C" __global__ void __launch_bounds__(256) sox_mlp_sum_bf16(sox_mlp_args p) { mlp_sum_body<bf16_t>(p); }
+
 // name: K1 x H (inner dim x hidden width); N2 <= 256, a multiple of 32
 #define SOX_MLP(K1, H)                                                                                           \
     extern "C" __global__ void __launch_bounds__(512) sox_mlp_f16_k##K1##_h##H(sox_mlp_args p) {                 \
@@ -148,3 +301,15 @@ __device__ __forceinline__ void mlp_body(const sox_mlp_args& p) {
 SOX_MLP(192, 768)
 SOX_MLP(128, 512)
 SOX_MLP(64, 256)
+
+// name: K1 x H, Q parts of the hidden width (a part: at most 8 hidden blocks, an even number of k-steps)
+#define SOX_MLPQ(K1, H, Q)                                                                                       \
+    extern "C" __global__ void __launch_bounds__(512) sox_mlpq_f16_k##K1##_h##H##_q##Q(sox_mlp_args p) {         \
+        mlp_part_body<half_t, K1 / 16, H / 32, H / 16, Q>(p);                                                    \
+    }                                                                                                            \
+    extern "C" __global__ void __launch_bounds__(512) sox_mlpq_bf16_k##K1##_h##H##_q##Q(sox_mlp_args p) {        \
+        mlp_part_body<bf16_t, K1 / 16, H / 32, H / 16, Q>(p);                                                    \
+    }
+SOX_MLPQ(192, 768, 3)
+SOX_MLPQ(128, 512, 4)
+SOX_MLPQ(64, 256, 2)

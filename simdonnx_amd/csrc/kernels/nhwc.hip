@@ -1234,7 +1234,7 @@ extern "C" __global__ void __launch_bounds__(256) sox_pool_f32(sox_pool_args p) 
 // S^T = K Q^T is built with v_mfma_f32_16x16x32_f16 (lane l: K row s = 16j + l%16, Q row t = l%16,
 // 8 consecutive d), so lane l ends up holding the scores of query t = l%16 for keys
 // s = 16j + 4(l/16) + i. The softmax over s is an in-register max/sum plus two cross-lane steps
-// (lanes l, l^16, l^32, l^48). O = P V reuses that register layout directly as the MFMA A operand:
+// (lanes l, l^16, l^32, l^48), its numerators from the hardware exp2 (exp16). O = P V reuses that register layout directly as the MFMA A operand:
 // within each 32-key step the lane's 8 keys are {32c + 4g + i, 32c + 16 + 4g + i} (g = l/16), and
 // the B operand (V) is read at the same key permutation (two 8-byte runs of V^T), which leaves the
 // sum over keys unchanged. Keys past S hold P = 0 and V = 0.
@@ -1303,7 +1303,7 @@ __device__ __forceinline__ void attn_mfma_body(const sox_attn_args& p) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int s = 16 * j + 4 * g + i;
-                const float e = s < p.s ? sox_exp(sc[j][i] - m) : 0.0f;
+                const float e = s < p.s ? exp16(sc[j][i] - m) : 0.0f;
                 sc[j][i] = e;
                 sum += e;
             }

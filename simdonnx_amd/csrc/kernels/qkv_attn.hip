@@ -168,7 +168,7 @@ __device__ __forceinline__ void qkv_attn_body(const sox_qkvattn_args& p) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int s = 16 * j + 4 * g + i;
-            const float e = s < t ? sox_exp(sc[j][i] - m) : 0.0f;
+            const float e = s < t ? exp16(sc[j][i] - m) : 0.0f;
             sc[j][i] = e;
             sum += e;
         }

@@ -49,6 +49,10 @@ SOX_DEV float sox_exp(float x) {
     return y * __int_as_float(ni << 23);
 }
 
+// exp for results stored in 16 bits (softmax numerators of the attention kernels): the hardware exp2
+// on x log2(e), about 1 ulp of fp32 plus the argument's rounding (|x| 2^-24), far below 16-bit rounding
+SOX_DEV float exp16(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+
 SOX_DEV float sox_sigmoid(float x) { return 1.0f / (1.0f + sox_exp(-x)); }
 
 SOX_DEV float sox_erf(float x) {

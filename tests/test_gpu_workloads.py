@@ -104,11 +104,13 @@ def test_detector_replay_is_bitwise_stable(hip):
             assert np.array_equal(s.run(), direct)
 
 
+@pytest.mark.parametrize("split", ["0", "1"], ids=["whole", "split"])
 @pytest.mark.parametrize("rows,dim,hidden,residual", [(2560, 192, 768, True), (333, 128, 512, True), (70, 64, 256, False)])
-def test_fused_mlp_matches_unfused_and_oracle(hip, rows, dim, hidden, residual, monkeypatch):
-    """LayerNorm -> fc1 (+GELU) -> fc2 (+ residual Add) runs as one dispatch (mlp.hip) and agrees with
-    the two LDS-DMA Gemms it replaces (SIMDONNX_HIP_NO_MLP_FUSE) within the fp16 contract and with the
-    oracle on the unfused plan."""
+def test_fused_mlp_matches_unfused_and_oracle(hip, rows, dim, hidden, residual, split, monkeypatch):
+    """LayerNorm -> fc1 (+GELU) -> fc2 (+ residual Add) runs as one dispatch (mlp.hip), or split over the
+    hidden width as parts and their sum (SIMDONNX_HIP_MLP_SPLIT=1), and agrees with the two LDS-DMA
+    Gemms it replaces (SIMDONNX_HIP_NO_MLP_FUSE) within the fp16 contract and with the oracle on the
+    unfused plan."""
     import numpy as np
     from oracle.interp import run_plan
     from simdonnx_amd import synth
@@ -125,8 +127,9 @@ def test_fused_mlp_matches_unfused_and_oracle(hip, rows, dim, hidden, residual, 
     y = pb.add(x, f2, name="res") if residual else f2
     plan = pb.build(y)
     xin = synth.normal(91, 7, (rows, dim), 1.0)
+    monkeypatch.setenv("SIMDONNX_HIP_MLP_SPLIT", split)
     g = hip.graph(plan, True)
-    assert [d[0] for d in g.dispatches] == ["mlp"]
+    assert [d[0] for d in g.dispatches] == (["mlp", "mlp_sum"] if split == "1" else ["mlp"])
     with HipInferenceSession(g) as s:
         s.set_input(xin)
         fused = s.run().copy()
