@@ -144,6 +144,39 @@ def bench_mfma_peak(iters: int = 4000, reps: int = 20):
                 ms=round(ms, 4), tflop_s=round(tf, 1), frac_of_peak=round(tf / PEAK_FP16_TFLOPS, 4))
 
 
+def bench_vendor_gemm(reps: int = 500):
+    """The vendor BLAS (hipBLASLt through torch) on the headline shape, for scale beside the fused kernel:
+    A[8192,768] x W[768,3072] as a plain product, with the bias (linear), and with the bias and a separate
+    GELU (the unfused form of what the fused kernel computes). fp16 and bf16, HIP events over `reps`
+    launches after warm-up on torch's current stream. A reported reference point, never `value`."""
+    import torch
+    M, K, N = 8192, 768, 3072
+    g = torch.Generator(device="cuda").manual_seed(0)
+    res = {"workload": "A[8192,768] x W[768,3072] (+ b[3072]) (-> GELU), torch.matmul / F.linear / F.gelu"}
+    for name, dt in (("f16", torch.float16), ("bf16", torch.bfloat16)):
+        a = torch.randn(M, K, device="cuda", dtype=dt, generator=g)
+        w = (torch.randn(N, K, device="cuda", dtype=dt, generator=g) * 0.02).contiguous()
+        wt = w.t().contiguous()
+        b = torch.rand(N, device="cuda", dtype=dt, generator=g) * 0.2 - 0.1
+        legs = {"matmul": lambda: a @ wt, "linear_bias": lambda: torch.nn.functional.linear(a, w, b),
+                "linear_bias_gelu": lambda: torch.nn.functional.gelu(torch.nn.functional.linear(a, w, b))}
+        r = {}
+        for leg, f in legs.items():
+            for _ in range(100):
+                f()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                f()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) / reps * 1e3
+            r[leg] = {"us": round(us, 2), "tflop_s": round(2 * M * N * K / us / 1e6, 1)}
+        res[name] = r
+    return res
+
+
 def bench_lds_peak(iters: int = 2000, reps: int = 10):
     """Per-CU throughput of the two LDS paths the Gemm ring lives on (probe.hip, one 16-wave workgroup
     per CU): ds_read_b128 with 16 KiB in flight per wave, and global_load_lds_dwordx4 from L2-resident
@@ -630,7 +663,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-replay", action="store_true",
                     help="launch network dispatches one by one instead of replaying a HIP graph (profiler runs)")
-    ap.add_argument("--only", choices=["gemm", "gemm_bf16", "mfma_peak", "lds_peak", "conv_large", "conv", "detector", "detector_fp32", "recognizer",
+    ap.add_argument("--only", choices=["gemm", "gemm_bf16", "mfma_peak", "lds_peak", "vendor_gemm", "conv_large", "conv", "detector", "detector_fp32", "recognizer",
                                        "recognizer_bf16", "mobilenetv3", "copy", "ops",
                                        "recognizer_ctc", "image", "runner"],
                     help="run one workload only (profiling runs); prints its own JSON line")
@@ -643,6 +676,7 @@ def main():
         fn = {"gemm": lambda: bench_gemm(args.steps, args.warmup), "conv": lambda: bench_conv(args.steps),
               "gemm_bf16": lambda: bench_gemm(args.steps, args.warmup, "bf16"),
               "mfma_peak": lambda: bench_mfma_peak(), "lds_peak": lambda: bench_lds_peak(),
+              "vendor_gemm": lambda: bench_vendor_gemm(),
               "conv_large": lambda: bench_conv_large(args.steps),
               "copy": lambda: bench_copy(args.steps),
               "ops": lambda: {"ops": bench_ops(args.steps)},
@@ -700,6 +734,11 @@ def main():
         out["lds_peak_probe"] = bench_lds_peak()
     except Exception as e:
         out["lds_peak_probe"] = {"error": repr(e)}
+    try:
+        out["vendor_gemm"] = bench_vendor_gemm()
+        log(f"vendor gemm (fp16 linear+bias+gelu): {out['vendor_gemm']['f16']['linear_bias_gelu']['tflop_s']} TFLOP/s")
+    except Exception as e:
+        out["vendor_gemm"] = {"error": repr(e)}
     try:
         out["conv_large_f16"] = bench_conv_large(50)
         log(f"large conv: {out['conv_large_f16']['tflop_s']} TFLOP/s")

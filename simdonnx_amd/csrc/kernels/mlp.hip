@@ -141,26 +141,31 @@ __device__ __forceinline__ void mlp_body(const sox_mlp_args& p) {
 // Split form: workgroup (row block of 32, part q of Q) takes hidden blocks q HB/Q .. (q + 1) HB/Q - 1
 // and fc2's k-steps over those hidden columns, so a grid of M/32 x Q workgroups shares the weights'
 // traffic (each workgroup streams 1/Q of W1 and W2 through its CU) and fills the GPU where M/32 alone
-// would not. fc2's part sums leave as fp32 (part[q][m][n2]); sox_mlp_sum_* adds them, b2 and the residual.
-//  phase 0: the part's W1 fragments (one hidden block per wave), its c1 / b1, the wave's W2 fragments and
-//           the 32 x rows (into LDS, so the hidden waves read their A fragments once per CU) all issued
-//           before the first wait.
+// would not.
+//  phase 0: the part's W1 fragments (one hidden block per wave), the wave's W2 fragments, the part's
+//           c1 / b1 and the 32 x rows (both into LDS: each is read by several waves) all issued before
+//           the first wait.
 //  phase 1: as sox_mlp_*: the LayerNorm from the row sums, one 32 x 32 hidden block per wave, GELU,
 //           rounding to the storage type, into LDS.
-//  phase 2: wave w < N2 / 32: output block w over the part's hidden k-steps (two accumulator chains).
+//  phase 2: wave w < N2 / 32: output block w over the part's hidden k-steps (two accumulator chains),
+//           stored as fp32 to part[q][m][n2]; sox_mlp_sum_* adds the parts, b2 and the residual.
+// (The parts meet in a second dispatch: a last-arriver reduction inside this kernel needs agent-scope
+// release / acquire fences, which write back and invalidate the XCD's L2 and cost several times the
+// second dispatch.)
 template <typename T, int KS1, int HB, int KS2, int Q>  // storage type, K1 / 16, H / 32, H / 16, parts
 __device__ __forceinline__ void mlp_part_body(const sox_mlp_args& p) {
     typedef vec_t<T, 8> T8;
     typedef vec_t<T, 4> T4;
     typedef vec_t<T, 2> T2;
-    constexpr int HBQ = HB / Q, KQ = KS2 / Q, K1 = KS1 * 16;
-    static_assert(HB % Q == 0 && HBQ <= 8 && KQ % 2 == 0, "a part is at most one hidden block per wave");
-    constexpr int HROW = HBQ * 32 * 2 + 16;   // LDS bytes per hidden row (16 bytes of padding)
-    constexpr int XP = K1 + 8;                // x row pitch in LDS, in elements
-    constexpr int XC = 32 * K1 / 8;           // 16-byte chunks of the 32 x rows
+    constexpr int HBQ = HB / Q, KQ = KS2 / Q, K1 = KS1 * 16, HQ = HBQ * 32;
+    static_assert(HB % Q == 0 && HBQ <= 8 && KQ % 2 == 0 && Q <= 4, "a part is at most one hidden block per wave");
+    constexpr int HROW = HQ * 2 + 16;   // LDS bytes per hidden row (16 bytes of padding)
+    constexpr int XP = K1 + 8;          // x row pitch in LDS, in elements
+    constexpr int XC = 32 * K1 / 8;     // 16-byte chunks of the 32 x rows
     constexpr int XI = (XC + 511) / 512;
     __shared__ __attribute__((aligned(16))) unsigned char hs[32 * HROW];
     __shared__ __attribute__((aligned(16))) T xs[32 * XP];
+    __shared__ __attribute__((aligned(16))) float cb[2][HQ];  // the part's c1 and b1
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, l32 = lane & 31, hl = lane >> 5;
     const int q = blockIdx.x % Q, m0 = (blockIdx.x / Q) * 32;
     const T* __restrict__ X = (const T*)p.x;
@@ -171,16 +176,9 @@ __device__ __forceinline__ void mlp_part_body(const sox_mlp_args& p) {
 
     // ---- phase 0: every load of the workgroup in flight before the first wait ----
     T8 b[KS1], w2f[KQ];
-    float4v c4[4], b4[4];
     if (hid_wave) {
 #pragma unroll
         for (int s = 0; s < KS1; s++) b[s] = *(const T8*)(W1 + (((long)jb * KS1 + s) * 64 + lane) * 8);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int n = jb * 32 + 8 * i + 4 * hl;
-            c4[i] = *(const float4v*)(p.c1 + n);
-            b4[i] = *(const float4v*)(p.b1 + n);
-        }
     }
     if (out_wave) {
 #pragma unroll
@@ -188,11 +186,16 @@ __device__ __forceinline__ void mlp_part_body(const sox_mlp_args& p) {
     }
     {
         T8 xv[XI];
+        float4v cv;
+        constexpr int CQ = HQ / 4;  // float4s of one of c1, b1 over the part
+        const bool cl = t < 2 * CQ;
+        if (cl) cv = *(const float4v*)((t < CQ ? p.c1 : p.b1) + q * HQ + 4 * (t % CQ));
 #pragma unroll
         for (int u = 0; u < XI; u++) {
             const int i = t + 512 * u, r = i / (K1 / 8), c = i - r * (K1 / 8);
             if (i < XC) xv[u] = *(const T8*)(X + (long)min(m0 + r, p.m - 1) * p.k1 + 8 * c);
         }
+        if (cl) *(float4v*)(&cb[t / CQ][4 * (t % CQ)]) = cv;
 #pragma unroll
         for (int u = 0; u < XI; u++) {
             const int i = t + 512 * u, r = i / (K1 / 8), c = i - r * (K1 / 8);
@@ -230,34 +233,39 @@ __device__ __forceinline__ void mlp_part_body(const sox_mlp_args& p) {
         const float rstd = __builtin_amdgcn_rsqf(fmaxf(s2 * inv_k - mean * mean, 0.0f) + p.eps);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
+            const int n = wave * 32 + 8 * i + 4 * hl;  // the part's hidden column
+            const float4v c4 = *(const float4v*)(&cb[0][n]), b4 = *(const float4v*)(&cb[1][n]);
             T4 hv;
 #pragma unroll
-            for (int e = 0; e < 4; e++) hv[e] = (T)gelu_fast(rstd * (acc[4 * i + e] - mean * c4[i][e]) + b4[i][e]);
-            *(T4*)(hs + l32 * HROW + (wave * 32 + 8 * i + 4 * hl) * 2) = hv;
+            for (int e = 0; e < 4; e++) hv[e] = (T)gelu_fast(rstd * (acc[4 * i + e] - mean * c4[e]) + b4[e]);
+            *(T4*)(hs + l32 * HROW + n * 2) = hv;
         }
     }
     __syncthreads();  // every hidden column of the part written
 
     // ---- phase 2: the part's share of hidden . W2, fp32 ----
-    if (!out_wave) return;
-    float16v acc = (float16v)0.0f, acc_o = (float16v)0.0f;
-    const unsigned char* hr = hs + l32 * HROW + 16 * hl;
+    if (out_wave) {
+        float16v acc = (float16v)0.0f, acc_o = (float16v)0.0f;
+        const unsigned char* hr = hs + l32 * HROW + 16 * hl;
 #pragma unroll
-    for (int s = 0; s < KQ; s += 2) {
-        acc = mfma32x32x16(w2f[s], *(const T8*)(hr + 32 * s), acc);
-        acc_o = mfma32x32x16(w2f[s + 1], *(const T8*)(hr + 32 * (s + 1)), acc_o);
-    }
-    const int m = m0 + l32;
-    if (m >= p.m) return;
-    float* dst = p.part + ((long)q * p.m + m) * p.n2 + wave * 32 + 4 * hl;
+        for (int s = 0; s < KQ; s += 2) {
+            acc = mfma32x32x16(w2f[s], *(const T8*)(hr + 32 * s), acc);
+            acc_o = mfma32x32x16(w2f[s + 1], *(const T8*)(hr + 32 * (s + 1)), acc_o);
+        }
+        const int m = m0 + l32;
+        if (m < p.m) {
+            float* dst = p.part + ((long)q * p.m + m) * p.n2 + wave * 32 + 4 * hl;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        float4v v;
+            for (int i = 0; i < 4; i++) {
+                float4v v;
 #pragma unroll
-        for (int e = 0; e < 4; e++) v[e] = acc[4 * i + e] + acc_o[4 * i + e];
-        *(float4v*)(dst + 8 * i) = v;
+                for (int e = 0; e < 4; e++) v[e] = acc[4 * i + e] + acc_o[4 * i + e];
+                *(float4v*)(dst + 8 * i) = v;
+            }
+        }
     }
 }
+
 
 // y = act2(b2 + part[0] + ... + part[parts - 1] + res), four consecutive outputs per thread
 template <typename T>
@@ -266,13 +274,13 @@ __device__ __forceinline__ void mlp_sum_body(const sox_mlp_args& p) {
     const long i = ((long)blockIdx.x * blockDim.x + threadIdx.x) * 4, total = (long)p.m * p.n2;
     if (i >= total) return;
     const int n = (int)(i % p.n2);
-    float4v v = (p.flags & 1) ? *(const float4v*)(p.b2 + n) : (float4v)0.0f;
-    T4 r = {};
-    if (p.flags & 2) r = *(const T4*)((const T*)p.res + i);
     float4v pv[4];
 #pragma unroll
     for (int q = 0; q < 4; q++)
         if (q < p.parts) pv[q] = *(const float4v*)(p.part + q * total + i);
+    float4v v = (p.flags & 1) ? *(const float4v*)(p.b2 + n) : (float4v)0.0f;
+    T4 r = {};
+    if (p.flags & 2) r = *(const T4*)((const T*)p.res + i);
 #pragma unroll
     for (int q = 0; q < 4; q++)
         if (q < p.parts) v += pv[q];

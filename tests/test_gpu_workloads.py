@@ -133,6 +133,10 @@ def test_fused_mlp_matches_unfused_and_oracle(hip, rows, dim, hidden, residual, 
     with HipInferenceSession(g) as s:
         s.set_input(xin)
         fused = s.run().copy()
+        s.set_replay(True)
+        for _ in range(2):
+            s.set_input(xin)
+            assert s.run().tobytes() == fused.tobytes()
     monkeypatch.setenv("SIMDONNX_HIP_NO_MLP_FUSE", "1")
     g2 = hip.graph(plan, True)
     assert [d[0] for d in g2.dispatches] == ["gemm_ln", "gemm"]
