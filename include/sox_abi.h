@@ -479,7 +479,7 @@ typedef struct sox_qkvattn_args {
     void* o;            /* [n][t][heads][32] */
     int32_t n, t, kpad;
     float eps, scale;
-    int32_t flags;
+    int32_t flags;      /* bit1 bqkv */
 } sox_qkvattn_args;
 
 /* LDS and LDS-DMA throughput probes (sox_probe_lds_read / sox_probe_lds_dma in probe.hip; measurement

@@ -453,7 +453,7 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
         for (int i = 0; i < TI; i++) {  // lanes l and l + 32 hold the two k-halves of a row
             const float s1 = ls1[i] + __shfl_xor(ls1[i], 32), s2 = ls2[i] + __shfl_xor(ls2[i], 32);
             mu[i] = s1 * inv_k;
-            rs[i] = __builtin_amdgcn_rsqf(fmaxf(s2 * inv_k - mu[i] * mu[i], 0.0f) + p.ln_eps);
+            rs[i] = ln_rstd(mu[i], s2, inv_k, p.ln_eps);
         }
         const bool hb = (p.flags & SOX_F_BIAS) != 0;
         static_for<0, TJ>([&](auto jj) {
@@ -468,7 +468,7 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
             wait_vmcnt<0>();  // as for the residual: no loads carried into the K loop
             static_for<0, TI * 16>([&](auto ie) {
                 constexpr int i = decltype(ie)::value / 16, e = decltype(ie)::value % 16;
-                acc[j][i][e] = rs[i] * (acc[j][i][e] - mu[i] * cv[e / 4][e % 4]) + bv[e / 4][e % 4];
+                acc[j][i][e] = ln_out(acc[j][i][e], mu[i], rs[i], cv[e / 4][e % 4], bv[e / 4][e % 4]);
             });
         });
     };

@@ -69,7 +69,7 @@ __device__ __forceinline__ void mlp_body(const sox_mlp_args& p) {
     }
     const float inv_k = 1.0f / (float)p.k1;
     const float mean = s1 * inv_k;
-    const float rstd = __builtin_amdgcn_rsqf(fmaxf(s2 * inv_k - mean * mean, 0.0f) + p.eps);
+    const float rstd = ln_rstd(mean, s2, inv_k, p.eps);
     // the wave's blocks interleaved k-step by k-step: independent accumulator chains
     float16v acc1[PB1];
 #pragma unroll
@@ -91,7 +91,7 @@ __device__ __forceinline__ void mlp_body(const sox_mlp_args& p) {
             T4 hv;
 #pragma unroll
             for (int e = 0; e < 4; e++)
-                hv[e] = (T)gelu_fast(rstd * (acc[4 * q + e] - mean * c4[e]) + b4[e]);
+                hv[e] = (T)gelu_fast(ln_out(acc[4 * q + e], mean, rstd, c4[e], b4[e]));
             *(T4*)(hs + l32 * HROW + n * 2) = hv;
         }
     }
@@ -230,14 +230,14 @@ __device__ __forceinline__ void mlp_part_body(const sox_mlp_args& p) {
         s2 += __shfl_xor(s2, 32);
         const float inv_k = 1.0f / (float)K1;
         const float mean = s1 * inv_k;
-        const float rstd = __builtin_amdgcn_rsqf(fmaxf(s2 * inv_k - mean * mean, 0.0f) + p.eps);
+        const float rstd = ln_rstd(mean, s2, inv_k, p.eps);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int n = wave * 32 + 8 * i + 4 * hl;  // the part's hidden column
             const float4v c4 = *(const float4v*)(&cb[0][n]), b4 = *(const float4v*)(&cb[1][n]);
             T4 hv;
 #pragma unroll
-            for (int e = 0; e < 4; e++) hv[e] = (T)gelu_fast(rstd * (acc[4 * i + e] - mean * c4[e]) + b4[e]);
+            for (int e = 0; e < 4; e++) hv[e] = (T)gelu_fast(ln_out(acc[4 * i + e], mean, rstd, c4[e], b4[e]));
             *(T4*)(hs + l32 * HROW + n * 2) = hv;
         }
     }
@@ -278,21 +278,10 @@ __device__ __forceinline__ void mlp_sum_body(const sox_mlp_args& p) {
 #pragma unroll
     for (int q = 0; q < 4; q++)
         if (q < p.parts) pv[q] = *(const float4v*)(p.part + q * total + i);
-    float4v v = (p.flags & 1) ? *(const float4v*)(p.b2 + n) : (float4v)0.0f;
+    const float4v b4 = (p.flags & 1) ? *(const float4v*)(p.b2 + n) : (float4v)0.0f;
     T4 r = {};
     if (p.flags & 2) r = *(const T4*)((const T*)p.res + i);
-#pragma unroll
-    for (int q = 0; q < 4; q++)
-        if (q < p.parts) v += pv[q];
-    const int act = (p.flags >> 4) & 15;
-    T4 out;
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        float x = v[e];
-        if (p.flags & 2) x += (float)r[e];
-        out[e] = (T)sox_act(x, act);
-    }
-    *(T4*)((T*)p.y + i) = out;
+    *(T4*)((T*)p.y + i) = mlp_out4<T>(pv, p.parts, b4, r, (p.flags & 2) != 0, (p.flags >> 4) & 15);
 }
 
 extern "C" __global__ void __launch_bounds__(256) sox_mlp_sum_f16(sox_mlp_args p) { mlp_sum_body<half_t>(p); }

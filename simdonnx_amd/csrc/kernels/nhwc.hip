@@ -1241,6 +1241,9 @@ extern "C" __global__ void __launch_bounds__(256) sox_pool_f32(sox_pool_args p) 
 // ------------------------------------------------------------------------------------------
 template <typename T, int NJ, int KD>
 __device__ __forceinline__ void attn_mfma_body(const sox_attn_args& p) {
+    // no contraction: the scaled score and its distance to the row max round separately, here and in the
+    // fused qkv-attention kernel alike, so the two give the same bits
+#pragma clang fp contract(off)
     typedef vec_t<T, 8> T8;
     typedef vec_t<T, 4> T4;
     constexpr int S = 16 * NJ, D = 32 * KD, NC = (NJ + 1) / 2, SP = 32 * NC, JD = 2 * KD;

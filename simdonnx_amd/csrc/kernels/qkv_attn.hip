@@ -20,14 +20,11 @@
 
 #include "sox_device.h"
 
-// The four fp32 results as rounded to fp32, before their conversion to 16 bits: the Gemm kernels round
-// their epilogue's last fma to fp32 and then to 16 bits, and without this the compiler may fold that fma
-// and the conversion into one mixed-precision fma that rounds once (v_fma_mixlo_f16), which differs
-// from the twice-rounded value near 16-bit ties.
-__device__ __forceinline__ void fp32_rounded(float4v& v) { asm volatile("" : "+v"(v)); }
-
 template <typename T, int DIM>
 __device__ __forceinline__ void qkv_attn_body(const sox_qkvattn_args& p) {
+    // no contraction (as sox_attn_*_mfma): the softmax's scaled score and its distance to the row max
+    // round separately; the LayerNorm epilogue's fmas are explicit (ln_out)
+#pragma clang fp contract(off)
     typedef vec_t<T, 8> T8;
     typedef vec_t<T, 4> T4;
     typedef vec_t<T, 2> T2;
@@ -55,7 +52,7 @@ __device__ __forceinline__ void qkv_attn_body(const sox_qkvattn_args& p) {
 
     // ---- phase 0: the head's W' rows, column sums and biases, and the x rows, in one batch ----
     {
-        T8 wv[WI], xv[XI];
+        T8 wv[WI];
         float4v cv = (float4v)0.0f;
 #pragma unroll
         for (int u = 0; u < WI; u++) {
@@ -65,10 +62,16 @@ __device__ __forceinline__ void qkv_attn_body(const sox_qkvattn_args& p) {
         const int cj = tid / 24, ck = tid - 24 * cj;  // threads 0..47: 4 columns of the sums (0) or biases (1)
         if (tid < 48 && (cj == 0 || (p.flags & 2)))
             cv = *(const float4v*)((cj == 0 ? p.cqkv : p.bqkv) + qkv_col(4 * ck));
+        T8 xv[XI];
 #pragma unroll
         for (int u = 0; u < XI; u++) {
             const int i = tid + NT * u, r = i / (DIM / 8), c = i - r * (DIM / 8);
             xv[u] = r < t ? *(const T8*)(x + (long)r * DIM + 8 * c) : zero8;
+        }
+#pragma unroll
+        for (int u = 0; u < XI; u++) {
+            const int i = tid + NT * u, r = i / (DIM / 8), c = i - r * (DIM / 8);
+            *(T8*)(xs + r * XP + 8 * c) = xv[u];
         }
 #pragma unroll
         for (int u = 0; u < WI; u++) {
@@ -76,11 +79,6 @@ __device__ __forceinline__ void qkv_attn_body(const sox_qkvattn_args& p) {
             *(T8*)(ws + r * XP + 8 * c) = wv[u];
         }
         if (tid < 48) *(float4v*)(&cb[cj][4 * ck]) = cv;
-#pragma unroll
-        for (int u = 0; u < XI; u++) {
-            const int i = tid + NT * u, r = i / (DIM / 8), c = i - r * (DIM / 8);
-            *(T8*)(xs + r * XP + 8 * c) = xv[u];
-        }
     }
     __syncthreads();
 
@@ -111,7 +109,7 @@ __device__ __forceinline__ void qkv_attn_body(const sox_qkvattn_args& p) {
         s2 += __shfl_xor(s2, 32);
         const float inv_k = 1.0f / (float)DIM;
         const float mu = s1 * inv_k;
-        const float rs = __builtin_amdgcn_rsqf(fmaxf(s2 * inv_k - mu * mu, 0.0f) + p.eps);
+        const float rs = ln_rstd(mu, s2, inv_k, p.eps);
         T* qr = qs + (mb * 32 + l32) * QP + nb * 32 + 4 * hl;
 #pragma unroll
         for (int q = 0; q < 4; q++) {
@@ -119,7 +117,7 @@ __device__ __forceinline__ void qkv_attn_body(const sox_qkvattn_args& p) {
             const float4v bv = *(const float4v*)(&cb[1][nb * 32 + 8 * q + 4 * hl]);
             float4v f;
 #pragma unroll
-            for (int e = 0; e < 4; e++) f[e] = rs * (acc[4 * q + e] - mu * cv[e]) + bv[e];
+            for (int e = 0; e < 4; e++) f[e] = ln_out(acc[4 * q + e], mu, rs, cv[e], bv[e]);
             fp32_rounded(f);
             *(T4*)(qr + 8 * q) = __builtin_convertvector(f, T4);
         }

@@ -104,6 +104,39 @@ SOX_DEV float gelu_fast(float x) {
     return __builtin_fmaf(-a, __builtin_amdgcn_exp2f(l), fmaxf(x, 0.0f));
 }
 
+// Four fp32 results as rounded to fp32, before their conversion to 16 bits: without the empty asm the
+// compiler may fold the last fma or add and the conversion into one mixed-precision op
+// (v_fma_mixlo_f16) that rounds once, where the unfused kernels round to fp32 and then to 16 bits.
+SOX_DEV void fp32_rounded(float4v& v) { asm volatile("" : "+v"(v)); }
+
+// The split transformer MLP's outputs, four columns: act(b2 + part[0] + .. + part[parts - 1] (+ res)),
+// summed in part order in fp32. sox_mlp_sum_* and the fused qkv-attention's row load both finish the
+// MLP with it, so the two give the same bits. pv holds the parts' float4s, b4 the bias (or zeros), r the
+// residual when has_r.
+template <typename T>
+SOX_DEV vec_t<T, 4> mlp_out4(const float4v (&pv)[4], int parts, float4v b4, vec_t<T, 4> r, bool has_r, int act) {
+    float4v v = b4;
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+        if (q < parts) v += pv[q];
+    float4v o;
+#pragma unroll
+    for (int e = 0; e < 4; e++) o[e] = sox_act(has_r ? v[e] + (float)r[e] : v[e], act);
+    fp32_rounded(o);
+    return __builtin_convertvector(o, vec_t<T, 4>);
+}
+
+// A LayerNorm folded into a Gemm (gamma-scaled weights W', c = column sums of W', b' = b + beta W):
+// rstd from the row's sum of squares over K values, then rstd (acc - mean c) + b'. The fmas are spelled
+// out so that every kernel folding a LayerNorm (the ring Gemm, the MLP, the fused qkv-attention) rounds
+// the same way, whatever the compiler would contract in each.
+SOX_DEV float ln_rstd(float mean, float s2, float inv_k, float eps) {
+    return __builtin_amdgcn_rsqf(fmaxf(__builtin_fmaf(s2, inv_k, -(mean * mean)), 0.0f) + eps);
+}
+SOX_DEV float ln_out(float acc, float mean, float rstd, float c, float b) {
+    return __builtin_fmaf(rstd, __builtin_fmaf(-mean, c, acc), b);
+}
+
 SOX_DEV float act_fast(float v, int act) { return act == SOX_ACT_GELU ? gelu_fast(v) : sox_act(v, act); }
 
 // 32x32x16 matrix-core step for either 16-bit storage type, fp32 accumulation
