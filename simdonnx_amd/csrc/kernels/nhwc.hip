@@ -1069,12 +1069,86 @@ extern "C" __global__ void __launch_bounds__(256) sox_ln_f32(sox_ln_args p) { ln
 // Row softmax (Kernels/Ops.Seq.cs:28-72): max, exp(x - max) by the shared exp core, 1/sum.
 // One 256-thread workgroup per row.
 // ------------------------------------------------------------------------------------------
+// 16-bit rows of at most 8192 values read from a stride that is a multiple of 8: the thread's four
+// 16-byte vectors stay in registers (one read of the row, the exps computed once), and the output,
+// staged in LDS as 16-bit values, leaves in 16-byte stores aligned to the output (dense rows of any
+// length start at any element), a scalar head and tail around them.
+template <typename T>
+__device__ __forceinline__ void softmax_regs(const sox_softmax_args& p, T* ob, float* red) {
+    typedef vec_t<T, 8> T8;
+    const long row = blockIdx.x;
+    const int len = p.len, t = threadIdx.x, lane = t & 63, wv = t >> 6, nv = (len + 7) / 8;
+    const T* x = (const T*)p.x + row * p.ldx;
+    T8 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int j = t + 256 * u;
+        if (j < nv) v[u] = *(const T8*)(x + 8 * j);
+    }
+    float f[4][8];
+    float m = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int i = 8 * (t + 256 * u) + e;
+            f[u][e] = i < len ? (float)v[u][e] : -INFINITY;
+            m = fmaxf(m, f[u][e]);
+        }
+    m = wave_max(m);
+    if (lane == 0) red[wv] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float s = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float ev = f[u][e] == -INFINITY ? 0.0f : exp16(f[u][e] - m);
+            f[u][e] = ev;
+            s += ev;
+        }
+    s = wave_sum(s);
+    if (lane == 0) red[wv] = s;
+    __syncthreads();
+    const float inv = 1.0f / ((red[0] + red[1]) + (red[2] + red[3]));
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int j = t + 256 * u;
+        if (j < nv) {
+            T8 o;
+#pragma unroll
+            for (int e = 0; e < 8; e++) o[e] = (T)(f[u][e] * inv);
+            *(T8*)(ob + 8 * j) = o;
+        }
+    }
+    __syncthreads();
+    T* y = (T*)p.y + row * len;
+    const int head = min(len, (int)(((16 - ((uintptr_t)y & 15)) & 15) / sizeof(T)));  // to a 16-byte boundary
+    const int groups = (len - head) / 8, tail0 = head + 8 * groups;
+    if (t < head) y[t] = ob[t];
+    for (int g = t; g < groups; g += 256) {
+        T8 o;
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[e] = ob[head + 8 * g + e];
+        *(T8*)(y + head + 8 * g) = o;
+    }
+    if (tail0 + t < len) y[tail0 + t] = ob[tail0 + t];
+}
+
 template <typename T>
 __device__ __forceinline__ void softmax_body(const sox_softmax_args& p) {
     // the row is read once (16 loads in flight per thread) into LDS as fp32 when it fits (dynamic
     // LDS of len floats, granted by the host), then max, sum and the output come from LDS
-    extern __shared__ float rowbuf[];
+    extern __shared__ __attribute__((aligned(16))) float rowbuf[];
     __shared__ float red[4];
+    if constexpr (sizeof(T) == 2) {
+        if (p.staged && p.ldx % 8 == 0 && p.len <= 8192 && p.len >= 8) {
+            softmax_regs<T>(p, (T*)rowbuf, red);
+            return;
+        }
+    }
     const long row = blockIdx.x;
     const T* x = (const T*)p.x + row * p.ldx;
     T* y = (T*)p.y + row * p.len;

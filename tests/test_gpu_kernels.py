@@ -439,11 +439,12 @@ def test_layernorm_softmax(hip, half):
 
 
 @pytest.mark.parametrize("half", [False, True], ids=["f32", "f16"])
-@pytest.mark.parametrize("rows,len_", [(37, 1), (37, 13), (19, 2048), (19, 2049), (23, 6625), (5, 8192), (5, 8193),
-                                       (3, 20000)])
+@pytest.mark.parametrize("rows,len_", [(37, 1), (37, 13), (3, 8), (19, 2048), (19, 2049), (9, 4000), (23, 6625),
+                                       (5, 8192), (5, 8193), (3, 20000)])
 def test_softmax_lengths(hip, rows, len_, half):
-    """Row softmax on the LDS-staged kernel (rows <= 16384, including the class head's 6625) and the
-    streaming one past it, with a per-row offset spread so the max subtraction matters."""
+    """Row softmax on the LDS-staged kernel (rows <= 16384, including the class head's 6625), the
+    register-held rows (16-bit, stride a multiple of 8, <= 8192: 8, 2048, 4000, 8192) and the streaming
+    one past 16384, with a per-row offset spread so the max subtraction matters."""
     cv = f16 if half else (lambda a: a)
     x = cv(synth.uniform(18, 1, (rows, len_), -4, 4) + synth.uniform(18, 2, (rows, 1), -20, 20))
     pb = PlanBuilder()
