@@ -1599,6 +1599,105 @@ __device__ __forceinline__ void conv_direct_333_body(const sox_igemm_args& p) {
     *(Vec*)((T*)p.y + o) = out;
 }
 
+// 3x3 over 3 channels (the RGB stems), stride S = 1 or 2, 16-bit storage: one workgroup per 16 x 16 output
+// pixels of one image, as a K = 27 matrix product on the matrix cores. The tile's input window
+// ((16 - 1) S + 3 square, the reflection or pad value already applied) is staged in LDS once, every
+// load of it issued before the first use; each wave then gathers the A fragments of 2 x 32 pixels from
+// the window (k = (ky * 3 + kx) * 3 + c, zero past 27: the packed weights are zero there too) and runs
+// two v_mfma_f32_32x32x16 steps per 32-channel block from accumulators holding the bias. The per-pixel
+// kernel (conv_direct_333) spends 27 fp32 FMAs and two broadcast LDS reads per output and term.
+template <typename T, int S>
+__device__ __forceinline__ void conv_stem_body(const sox_igemm_args& p) {
+    typedef vec_t<T, 8> T8;
+    typedef vec_t<T, 4> T4;
+    constexpr int IC = 3, K = 27, TO = 16, TH = (TO - 1) * S + 3, NEL = TH * TH * IC, NI = (NEL + 255) / 256;
+    __shared__ T xt[NEL];  // [TH][TH][IC]
+    const int oc = p.n, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, hl = lane >> 5;
+    const int tiles_x = (p.ow + TO - 1) / TO;
+    const int ty0 = (blockIdx.x / tiles_x) * TO, tx0 = (blockIdx.x % tiles_x) * TO, b = blockIdx.y;
+    const bool reflect = (p.flags & SOX_F_REFLECT) != 0;
+    const T* __restrict__ x = (const T*)p.x + (long)b * p.ih * p.iw * IC;
+    const int iy0 = ty0 * S - p.pt, ix0 = tx0 * S - p.pl;
+    {
+        T xv[NI];
+#pragma unroll
+        for (int u = 0; u < NI; u++) {
+            const int i = tid + 256 * u, r = i / (TH * IC), rem = i - r * (TH * IC), cx = rem / IC, c = rem - cx * IC;
+            const int iy = sox_src_index(iy0 + r, p.ih, reflect), ix = sox_src_index(ix0 + cx, p.iw, reflect);
+            const bool in = i < NEL && iy >= 0 && ix >= 0;
+            const T v = x[in ? ((long)iy * p.iw + ix) * IC + c : 0];  // a valid address either way
+            xv[u] = in ? v : (T)p.pad_value;
+        }
+#pragma unroll
+        for (int u = 0; u < NI; u++)
+            if (tid + 256 * u < NEL) xt[tid + 256 * u] = xv[u];
+    }
+    // the wave's W fragments and bias (oc <= 32: one 32-channel block; rows past oc are zero)
+    const T* __restrict__ W = (const T*)p.w;
+    T8 bw[2];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; s2++)
+        bw[s2] = l32 < oc ? *(const T8*)(W + (long)l32 * p.kpad + 16 * s2 + 8 * hl) : (T8)(T)0.0f;
+    float4v bv[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int n = 8 * q + 4 * hl;
+        bv[q] = ((p.flags & SOX_F_BIAS) && n < oc) ? *(const float4v*)(p.bias + n) : (float4v)0.0f;
+    }
+    __syncthreads();
+    const int act = (p.flags & SOX_F_ACT_MASK) >> SOX_F_ACT_SHIFT;
+#pragma unroll
+    for (int g2 = 0; g2 < 2; g2++) {
+        const int pg = wave * 2 + g2;               // 32 pixels: tile rows 2 pg, 2 pg + 1
+        const int ty = 2 * pg + (l32 >> 4), tx = l32 & 15;
+        const T* base = xt + ((ty * S) * TH + tx * S) * IC;
+        T8 a[2];
+#pragma unroll
+        for (int s2 = 0; s2 < 2; s2++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int k = 16 * s2 + 8 * hl + e, ky = k / 9, r9 = k - 9 * ky;
+                a[s2][e] = k < K ? base[ky * TH * IC + r9] : (T)0.0f;  // (kx, c) = r9 / 3, r9 % 3: contiguous
+            }
+        float16v acc;
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[4 * q + e] = bv[q][e];
+        acc = mfma32x32x16(bw[0], a[0], acc);
+        acc = mfma32x32x16(bw[1], a[1], acc);
+        const int oy = ty0 + ty, ox = tx0 + tx;
+        if (oy >= p.oh || ox >= p.ow) continue;
+        const long m = ((long)b * p.oh + oy) * p.ow + ox;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int n = 8 * q + 4 * hl;
+            if (n >= oc) continue;  // oc % 8 == 0: a group of 4 is whole or absent
+            const long o = m * p.ldy + n;
+            T4 rv = {};
+            if (p.flags & SOX_F_RESIDUAL) rv = *(const T4*)((const T*)p.add + o);
+            T4 h;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                float v = acc[4 * q + e];
+                if (p.flags & SOX_F_RESIDUAL) v += (float)rv[e];
+                h[e] = (T)act_fast(v, act);
+            }
+            *(T4*)((T*)p.y + o) = h;
+        }
+    }
+}
+
+#define SOX_STEM(S)                                                                                             \
+    extern "C" __global__ void __launch_bounds__(256) sox_conv_stem_s##S##_f16(sox_igemm_args p) {              \
+        conv_stem_body<half_t, S>(p);                                                                           \
+    }                                                                                                           \
+    extern "C" __global__ void __launch_bounds__(256) sox_conv_stem_s##S##_bf16(sox_igemm_args p) {             \
+        conv_stem_body<bf16_t, S>(p);                                                                           \
+    }
+SOX_STEM(1)
+SOX_STEM(2)
+
 // Direct conv for few OUTPUT channels (oc < 8: a final 3x3 conv to an image or a probability map),
 // fp16 with ic % 8 == 0: a 32-channel matrix tile would leave most of its columns empty. One work
 // item = one output pixel x all OC channels (one instance per OC, so no FMA is spent on padding);

@@ -152,6 +152,42 @@ def test_depthwise_tiles_match_per_pixel_kernel(hip, case, storage, monkeypatch)
     assert max_rel(tiled, want) < {"f16": 2e-3, "bf16": 4e-3, "f32": 1e-4}[storage]
 
 
+STEM_CASES = [  # (oc, stride, h, w, pad_mode, act, residual)
+    (16, 2, 97, 131, 0, "relu", False), (32, 2, 48, 320, 0, "gelu", False), (16, 1, 37, 23, 1, "hardswish", True),
+    (8, 2, 33, 17, 1, "none", False), (24, 1, 40, 48, 0, "swish", False)]
+
+
+@pytest.mark.parametrize("storage", ["f16", "bf16"])
+@pytest.mark.parametrize("case", STEM_CASES, ids=[f"oc{c[0]}s{c[1]}_{c[2]}x{c[3]}" for c in STEM_CASES])
+def test_rgb_stem_on_matrix_cores(hip, case, storage, monkeypatch):
+    """3x3 convs over 3 channels in 16-bit graphs take the tiled matrix-core stem (sox_conv_stem_*:
+    ragged 16 x 16 tiles, stride 1 / 2, zero and reflect padding, residual, oc below one 32-channel
+    block) and meet the oracle, as the per-pixel fp32-FMA kernel (SIMDONNX_HIP_STEM_DIRECT) does; the two
+    differ only by summation order."""
+    oc, st, h, w, mode, act, res = case
+    from oracle.interp import _bf16
+    rnd = {"f16": f16, "bf16": _bf16}[storage]
+    x = rnd(synth.uniform(44, 1, (1, h, w, 3), -1, 1))
+    wt = rnd(synth.uniform(44, 2, (oc, 3, 3, 3), -0.5, 0.5))
+    b = synth.uniform(44, 3, (oc,), -0.1, 0.1)
+    oh, ow = (h + 2 - 3) // st + 1, (w + 2 - 3) // st + 1
+    add = rnd(synth.uniform(44, 4, (1, oh, ow, oc), -1, 1)) if res else None
+    plan, ins = conv_plan(x, wt, b, add, (st, st), (1, 1, 1, 1), act, mode, 0.0)
+    g = hip.graph(plan, storage)
+    assert g.kernels == [f"sox_conv_stem_s{st}_{storage}"], g.kernels
+    g.release()
+    tiled = run(hip, plan, ins, storage)
+    monkeypatch.setenv("SIMDONNX_HIP_STEM_DIRECT", "1")
+    g = hip.graph(plan, storage)
+    assert g.kernels == [f"sox_conv_direct_333_{storage}"], g.kernels
+    g.release()
+    direct = run(hip, plan, ins, storage)
+    want = O.conv(x, wt, b, add, stride=(st, st), pads=(1, 1, 1, 1), act=act, pad_mode=mode)
+    tol = {"f16": 2e-3, "bf16": 8e-3}[storage]
+    assert max_rel(tiled, want) < tol and max_rel(direct, want) < tol
+    assert max_rel(tiled, direct) < tol
+
+
 @pytest.mark.parametrize("storage", ["f16", "bf16", "f32"])
 @pytest.mark.parametrize("case", [(240, 5, 1, 60, 60), (96, 5, 2, 120, 120), (576, 5, 1, 30, 30), (72, 3, 1, 44, 36)])
 def test_se_gap_partials_from_depthwise(hip, case, storage, monkeypatch):
