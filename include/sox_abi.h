@@ -450,7 +450,16 @@ typedef struct sox_mlp_args {
     float eps;
     int32_t flags;      /* bit0 b2, bit1 residual, act2 << 4 */
     float* part;        /* sox_mlpq_* / sox_mlp_sum_*: fp32 [parts][m][n2], fc2 over each part of the hidden width */
-    int32_t parts, pad_;
+    int32_t parts;
+    /* sox_mlpqp_*: x is first computed as the preceding projection Gemm with its residual Add,
+     * x = po . Wp^T + pb + px ([m][k1] each, Wp GemmNK-packed [k1][k1]); part 0 of every row block
+     * stores it to xout (the MLP's residual, read by sox_mlp_sum_*). */
+    int32_t pflags;     /* bit0 pb */
+    const void* po;
+    const void* pw;
+    const float* pb;
+    const void* px;
+    void* xout;
 } sox_mlp_args;
 
 /* Matrix-core rate probe (sox_probe_mfma_f16 in the Gemm code object; a measurement kernel, no

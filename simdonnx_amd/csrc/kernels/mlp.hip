@@ -145,6 +145,10 @@ __device__ __forceinline__ void mlp_body(const sox_mlp_args& p) {
 //  phase 0: the part's W1 fragments (one hidden block per wave), the wave's W2 fragments, the part's
 //           c1 / b1 and the 32 x rows (both into LDS: each is read by several waves) all issued before
 //           the first wait.
+//  PROJ (sox_mlpqp_*): x itself is the preceding projection Gemm with its residual Add: phase 0 stages
+//           the projection's input rows instead, with each wave's Wp fragments, bias and residual; then
+//           wave w < K1 / 32 computes x's columns 32 w.. on v_mfma_f32_32x32x16 into LDS (part 0 also
+//           stores them: the MLP's residual), and the W2 fragments load after it (registers).
 //  phase 1: as sox_mlp_*: the LayerNorm from the row sums, one 32 x 32 hidden block per wave, GELU,
 //           rounding to the storage type, into LDS.
 //  phase 2: wave w < N2 / 32: output block w over the part's hidden k-steps (two accumulator chains),
@@ -152,7 +156,7 @@ __device__ __forceinline__ void mlp_body(const sox_mlp_args& p) {
 // (The parts meet in a second dispatch: a last-arriver reduction inside this kernel needs agent-scope
 // release / acquire fences, which write back and invalidate the XCD's L2 and cost several times the
 // second dispatch.)
-template <typename T, int KS1, int HB, int KS2, int Q>  // storage type, K1 / 16, H / 32, H / 16, parts
+template <typename T, int KS1, int HB, int KS2, int Q, bool PROJ>  // storage, K1 / 16, H / 32, H / 16, parts
 __device__ __forceinline__ void mlp_part_body(const sox_mlp_args& p) {
     typedef vec_t<T, 8> T8;
     typedef vec_t<T, 4> T4;
@@ -164,11 +168,12 @@ __device__ __forceinline__ void mlp_part_body(const sox_mlp_args& p) {
     constexpr int XC = 32 * K1 / 8;     // 16-byte chunks of the 32 x rows
     constexpr int XI = (XC + 511) / 512;
     __shared__ __attribute__((aligned(16))) unsigned char hs[32 * HROW];
-    __shared__ __attribute__((aligned(16))) T xs[32 * XP];
+    __shared__ __attribute__((aligned(16))) T xs[32 * XP];   // x rows (PROJ: the projection's input rows)
+    __shared__ __attribute__((aligned(16))) T x2s[PROJ ? 32 * XP : 8];  // PROJ: the x rows computed here
     __shared__ __attribute__((aligned(16))) float cb[2][HQ];  // the part's c1 and b1
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, l32 = lane & 31, hl = lane >> 5;
     const int q = blockIdx.x % Q, m0 = (blockIdx.x / Q) * 32;
-    const T* __restrict__ X = (const T*)p.x;
+    const T* __restrict__ X = (const T*)(PROJ ? p.po : p.x);
     const T* __restrict__ W1 = (const T*)p.w1;
     const T* __restrict__ W2 = (const T*)p.w2;
     const bool hid_wave = wave < HBQ, out_wave = wave * 32 < p.n2;
@@ -180,9 +185,31 @@ __device__ __forceinline__ void mlp_part_body(const sox_mlp_args& p) {
 #pragma unroll
         for (int s = 0; s < KS1; s++) b[s] = *(const T8*)(W1 + (((long)jb * KS1 + s) * 64 + lane) * 8);
     }
-    if (out_wave) {
+    auto load_w2 = [&]() __attribute__((always_inline)) {
+        if (out_wave) {
 #pragma unroll
-        for (int s = 0; s < KQ; s++) w2f[s] = *(const T8*)(W2 + (((long)wave * KS2 + q * KQ + s) * 64 + lane) * 8);
+            for (int s = 0; s < KQ; s++) w2f[s] = *(const T8*)(W2 + (((long)wave * KS2 + q * KQ + s) * 64 + lane) * 8);
+        }
+    };
+    if constexpr (!PROJ) load_w2();
+    // PROJ: the projection's weight fragments (its 32 output columns per wave), bias and residual rows
+    const bool proj_wave = PROJ && wave * 32 < K1;
+    T8 pwf[PROJ ? KS1 : 1];
+    float4v pbv[4];
+    T4 pxv[4];
+    if constexpr (PROJ) {
+        if (proj_wave) {
+            const int r = min(m0 + l32, p.m - 1);
+#pragma unroll
+            for (int s = 0; s < KS1; s++)
+                pwf[s] = *(const T8*)((const T*)p.pw + (long)(wave * 32 + l32) * K1 + 16 * s + 8 * hl);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int n = wave * 32 + 8 * i + 4 * hl;
+                pbv[i] = (p.pflags & 1) ? *(const float4v*)(p.pb + n) : (float4v)0.0f;
+                pxv[i] = *(const T4*)((const T*)p.px + (long)r * K1 + n);
+            }
+        }
     }
     {
         T8 xv[XI];
@@ -204,9 +231,38 @@ __device__ __forceinline__ void mlp_part_body(const sox_mlp_args& p) {
     }
     __syncthreads();
 
+    // ---- PROJ: x = po . Wp^T + pb + px, the projection Gemm with its residual Add, for the 32 rows
+    // (accumulators from the bias, k-steps ascending, rounded to fp32 and then to 16 bits) ----
+    if constexpr (PROJ) {
+        if (proj_wave) {
+            float16v acc;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[4 * i + e] = pbv[i][e];
+            const T* ar = xs + l32 * XP + 8 * hl;
+#pragma unroll
+            for (int s = 0; s < KS1; s++) acc = mfma32x32x16(pwf[s], *(const T8*)(ar + 16 * s), acc);
+            const int m = m0 + l32;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int n = wave * 32 + 8 * i + 4 * hl;
+                float4v f;
+#pragma unroll
+                for (int e = 0; e < 4; e++) f[e] = acc[4 * i + e] + (float)pxv[i][e];
+                fp32_rounded(f);
+                const T4 h = __builtin_convertvector(f, T4);
+                *(T4*)(x2s + l32 * XP + n) = h;
+                if (q == 0 && m < p.m) *(T4*)((T*)p.xout + (long)m * K1 + n) = h;
+            }
+        }
+        load_w2();
+        __syncthreads();
+    }
+
     // ---- phase 1: hidden = GELU(rstd (x . W1 - mean c1) + b1), the part's columns ----
     if (hid_wave) {
-        const T* ar = xs + l32 * XP + 8 * hl;
+        const T* ar = (PROJ ? x2s : xs) + l32 * XP + 8 * hl;
         float s1 = 0.0f, s2 = 0.0f;
         float16v acc = (float16v)0.0f;
         const T2 one = {(T)1.0f, (T)1.0f};
@@ -302,10 +358,16 @@ SOX_MLP(64, 256)
 // name: K1 x H, Q parts of the hidden width (a part: at most 8 hidden blocks, an even number of k-steps)
 #define SOX_MLPQ(K1, H, Q)                                                                                       \
     extern "C" __global__ void __launch_bounds__(512) sox_mlpq_f16_k##K1##_h##H##_q##Q(sox_mlp_args p) {         \
-        mlp_part_body<half_t, K1 / 16, H / 32, H / 16, Q>(p);                                                    \
+        mlp_part_body<half_t, K1 / 16, H / 32, H / 16, Q, false>(p);                                             \
     }                                                                                                            \
     extern "C" __global__ void __launch_bounds__(512) sox_mlpq_bf16_k##K1##_h##H##_q##Q(sox_mlp_args p) {        \
-        mlp_part_body<bf16_t, K1 / 16, H / 32, H / 16, Q>(p);                                                    \
+        mlp_part_body<bf16_t, K1 / 16, H / 32, H / 16, Q, false>(p);                                             \
+    }                                                                                                            \
+    extern "C" __global__ void __launch_bounds__(512) sox_mlpqp_f16_k##K1##_h##H##_q##Q(sox_mlp_args p) {        \
+        mlp_part_body<half_t, K1 / 16, H / 32, H / 16, Q, true>(p);                                              \
+    }                                                                                                            \
+    extern "C" __global__ void __launch_bounds__(512) sox_mlpqp_bf16_k##K1##_h##H##_q##Q(sox_mlp_args p) {       \
+        mlp_part_body<bf16_t, K1 / 16, H / 32, H / 16, Q, true>(p);                                              \
     }
 SOX_MLPQ(192, 768, 3)
 SOX_MLPQ(128, 512, 4)

@@ -177,9 +177,10 @@ def test_fused_mlp_not_taken_when_hidden_is_read_twice(hip):
     assert max_rel(got, run_plan(plan, [xin], f16_storage=True)) < 2e-2
 
 
-def _attention_block_plan(n, t, dim=192, heads=6, seed=93):
+def _attention_block_plan(n, t, dim=192, heads=6, seed=93, mlp=False, proj_bias=True, reread=False):
     """x [n, t, dim] -> LayerNorm -> qkv Gemm -> attention -> proj Gemm -> + x: the first half of an SVTR
-    mixer block, as graphs.svtr builds it."""
+    mixer block, as graphs.svtr builds it; with mlp, the second half too (x2 -> LayerNorm -> fc1 + GELU
+    -> fc2 -> + x2), and with reread the block output plus x2 once more (a later reader of x2)."""
     from simdonnx_amd import synth
     from simdonnx_amd.plan import PlanBuilder
     pb = PlanBuilder()
@@ -190,8 +191,21 @@ def _attention_block_plan(n, t, dim=192, heads=6, seed=93):
                   name="qkv")
     d = dim // heads
     att = pb.attention(qkv, heads, d, d ** -0.5, name="attn")
-    proj = pb.gemm(att, synth.normal(seed, 5, (dim, dim), 0.05), synth.uniform(seed, 6, (dim,), -0.1, 0.1), name="proj")
-    plan = pb.build(pb.add(x, proj, name="res"))
+    proj = pb.gemm(att, synth.normal(seed, 5, (dim, dim), 0.05),
+                   synth.uniform(seed, 6, (dim,), -0.1, 0.1) if proj_bias else None, name="proj")
+    y = pb.add(x, proj, name="res")
+    if mlp:
+        x2 = y
+        h2 = pb.layer_norm(x2, 1.0 + synth.uniform(seed, 8, (dim,), -0.1, 0.1),
+                           synth.uniform(seed, 9, (dim,), -0.1, 0.1), 1e-6, name="ln2")
+        f1 = pb.gemm(h2, synth.normal(seed, 10, (dim, 4 * dim), 0.05), synth.uniform(seed, 11, (4 * dim,), -0.1, 0.1),
+                     act="gelu", name="fc1")
+        f2 = pb.gemm(f1, synth.normal(seed, 12, (4 * dim, dim), 0.05), synth.uniform(seed, 13, (dim,), -0.1, 0.1),
+                     name="fc2")
+        y = pb.add(x2, f2, name="res2")
+        if reread:
+            y = pb.add(y, x2, name="again")
+    plan = pb.build(y)
     return plan, synth.normal(seed, 7, (n, t, dim), 1.0)
 
 
@@ -229,3 +243,36 @@ def test_qkv_attention_not_fused_past_96_tokens(hip):
         s.set_input(xin)
         got = s.run().copy()
     assert max_rel(got, run_plan(plan, [xin], f16_storage=True)) < 2e-2
+
+
+@pytest.mark.parametrize("n,t,storage,proj_bias,reread", [(32, 80, "f16", True, False), (3, 96, "f16", False, False),
+                                                          (5, 33, "bf16", True, True), (7, 80, "bf16", True, False)])
+def test_proj_fused_into_mlp_matches_unfused_and_oracle(hip, n, t, storage, proj_bias, reread, monkeypatch):
+    """A whole SVTR mixer block: the proj Gemm and its residual Add run inside the split MLP's part
+    kernel (sox_mlpqp_*), which rebuilds x2 = x + att . Wp + bp per 32 rows and has part 0 store it for
+    the MLP's residual and any later reader, bit for bit as the separate Gemm dispatch
+    (SIMDONNX_HIP_NO_PROJ_FUSE), and within the 16-bit contract of the oracle. 165 rows (5 x 33) leave
+    a ragged last row block; reread adds a later reader of x2."""
+    plan, xin = _attention_block_plan(n, t, seed=94, mlp=True, proj_bias=proj_bias, reread=reread)
+    monkeypatch.setenv("SIMDONNX_HIP_MLP_SPLIT", "1")
+    g = hip.graph(plan, storage)
+    names = [d[0] for d in g.dispatches]
+    assert names[:3] == ["qkv_attn", "mlp", "mlp_sum"], names
+    assert g.kernels[1] == f"sox_mlpqp_{storage}_k192_h768_q3"
+    with HipInferenceSession(g) as s:
+        s.set_input(xin)
+        fused = s.run().copy()
+        s.set_replay(True)
+        for _ in range(2):
+            s.set_input(xin)
+            assert s.run().tobytes() == fused.tobytes()
+    monkeypatch.setenv("SIMDONNX_HIP_NO_PROJ_FUSE", "1")
+    g2 = hip.graph(plan, storage)
+    assert [d[0] for d in g2.dispatches][:4] == ["qkv_attn", "gemm", "mlp", "mlp_sum"]
+    with HipInferenceSession(g2) as s:
+        s.set_input(xin)
+        unfused = s.run().copy()
+    print(f"[gpu] proj fused vs unfused max-rel {max_rel(fused, unfused):.2e}", flush=True)
+    assert fused.tobytes() == unfused.tobytes()
+    want = run_plan(plan, [xin], f16_storage="bf16" if storage == "bf16" else True)
+    assert max_rel(fused, want) < 2e-2
