@@ -68,6 +68,11 @@ typedef struct sox_igemm_args {
     int32_t ct_kh, ct_kw, ct_oc; /* SOX_F_CONVT: the ConvTranspose kernel (stride == kernel) and its channels */
     float ln_eps;                /* sox_gemm_ln_*: the folded LayerNorm's epsilon */
     const float* ln_c;           /* sox_gemm_ln_*: [N] column sums of the gamma-scaled packed weights */
+    /* sox_conv_halo_*_upcat: the input (x unused) is the channel concat of up_n sources of up_c channels
+     * each, source s the nearest upsample by 2^up_shift[s] of up[s] = [n][ih >> shift][iw >> shift][up_c] */
+    const void* up[4];
+    int32_t up_n, up_c;
+    int32_t up_shift[4];
 } sox_igemm_args;
 
 /*

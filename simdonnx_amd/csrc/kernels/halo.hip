@@ -15,9 +15,13 @@
 //    row stride ldy (a concat slice works).
 // Every DMA lane writes a slot (the regions are padded to whole instructions), so every wave issues
 // the same number of loads per block and one static vmcnt covers them.
+// UPC (sox_conv_halo_*_upcat): the input is a channel concat of nearest upsamples by powers of two
+// (the DB FPN's fuse = concat(up8(p5), up4(p4), up2(p3), p2), Backends/Vulkan/VkGraph.cs:486-510 and
+// concat_ax.comp), never stored: each 8-channel chunk's DMA reads its source at (iy >> s, ix >> s).
+// The gathered bytes are the concat's, so the result is the same bits.
 #include "gemm_ring.h"
 
-template <typename T, int KH, int KW, int SH, int SW>
+template <typename T, int KH, int KW, int SH, int SW, bool UPC>
 __device__ __forceinline__ void halo_body(const sox_igemm_args& p) {
     typedef vec_t<T, 8> T8;
     typedef vec_t<T, 4> T4;
@@ -46,13 +50,19 @@ __device__ __forceinline__ void halo_body(const sox_igemm_args& p) {
     // this thread's DMA sources in channel block 0 (nullptr: the slot is padding and reads zeros);
     // block c adds c * CB channels, and a chunk past ic reads zeros too
     const T* hsrc[HALO_IT];
-    int hch[HALO_IT];
+    int hch[HALO_IT], hpy[UPC ? HALO_IT : 1], hpx[UPC ? HALO_IT : 1];
 #pragma unroll
     for (int i = 0; i < HALO_IT; i++) {
         const int q = i * 256 + t, hp = q / PITCH, sub = q - hp * PITCH;
         const int hy = hp / HW, hx = hp - hy * HW, iy = iy0 + hy, ix = ix0 + hx;
         const bool ok = q < HP * PITCH && sub < 4 && (unsigned)iy < (unsigned)p.ih && (unsigned)ix < (unsigned)p.iw;
-        hsrc[i] = ok ? X + ((long)iy * p.iw + ix) * p.ic + sub * 8 : nullptr;
+        if constexpr (UPC) {  // hsrc only flags the pixel in the image; the source is picked per block
+            hsrc[i] = ok ? Z : nullptr;
+            hpy[i] = iy;
+            hpx[i] = ix;
+        } else {
+            hsrc[i] = ok ? X + ((long)iy * p.iw + ix) * p.ic + sub * 8 : nullptr;
+        }
         hch[i] = sub * 8;
     }
     const T* wsrc[W_IT];
@@ -70,7 +80,19 @@ __device__ __forceinline__ void halo_body(const sox_igemm_args& p) {
         const int c0 = cb * CB;
 #pragma unroll
         for (int i = 0; i < HALO_IT; i++) {
-            const T* src = hsrc[i] && c0 + hch[i] < p.ic ? hsrc[i] + c0 : Z;
+            const T* src = Z;
+            if constexpr (UPC) {
+                const int c = c0 + hch[i];
+                if (hsrc[i] && c < p.ic) {
+                    const int s = c / p.up_c, cl = c - s * p.up_c;
+                    const int sh = s == 0 ? p.up_shift[0] : s == 1 ? p.up_shift[1] : s == 2 ? p.up_shift[2] : p.up_shift[3];
+                    const void* up = s == 0 ? p.up[0] : s == 1 ? p.up[1] : s == 2 ? p.up[2] : p.up[3];
+                    const int sw = p.iw >> sh;
+                    src = (const T*)up + (((long)b * (p.ih >> sh) + (hpy[i] >> sh)) * sw + (hpx[i] >> sh)) * p.up_c + cl;
+                }
+            } else {
+                if (hsrc[i] && c0 + hch[i] < p.ic) src = hsrc[i] + c0;
+            }
             __builtin_amdgcn_global_load_lds(src, LDS_PTR(st + i * 256 * 16), 16, 0, 0);
         }
 #pragma unroll
@@ -144,10 +166,12 @@ __device__ __forceinline__ void halo_body(const sox_igemm_args& p) {
     });
 }
 
-#define SOX_HALO(NAME, T, KH, KW, SH, SW, OCC)                                                    \
+#define SOX_HALO(NAME, T, KH, KW, SH, SW, OCC, UPC)                                               \
     extern "C" __global__ void __launch_bounds__(256, OCC) NAME(sox_igemm_args p) {            \
-        halo_body<T, KH, KW, SH, SW>(p);                                                       \
+        halo_body<T, KH, KW, SH, SW, UPC>(p);                                                  \
     }
 
-SOX_HALO(sox_conv_halo_f16_3x3s1, half_t, 3, 3, 1, 1, 2)
-SOX_HALO(sox_conv_halo_bf16_3x3s1, bf16_t, 3, 3, 1, 1, 2)
+SOX_HALO(sox_conv_halo_f16_3x3s1, half_t, 3, 3, 1, 1, 2, false)
+SOX_HALO(sox_conv_halo_bf16_3x3s1, bf16_t, 3, 3, 1, 1, 2, false)
+SOX_HALO(sox_conv_halo_f16_3x3s1_upcat, half_t, 3, 3, 1, 1, 2, true)
+SOX_HALO(sox_conv_halo_bf16_3x3s1_upcat, bf16_t, 3, 3, 1, 1, 2, true)

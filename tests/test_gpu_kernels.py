@@ -301,6 +301,47 @@ def test_se_block_matches_oracle(hip, half):
     assert max_rel(got, want) < TOL[half]
 
 
+# (n, h, w, c, shifts, oc): sources of c channels at (h >> s, w >> s), each upsampled (nearest) by 2^s,
+# concatenated, then a 3x3 conv (+ bias, relu): the DB FPN's fuse conv at its full size and smaller
+UPCAT_CASES = [(1, 240, 240, 24, (3, 2, 1, 0), 24), (1, 64, 64, 24, (3, 2, 1, 0), 24), (2, 48, 40, 16, (0, 1, 2), 40),
+               (1, 36, 20, 32, (2, 2), 8)]
+
+
+@pytest.mark.parametrize("storage", ["f16", "bf16"])
+@pytest.mark.parametrize("case", UPCAT_CASES, ids=lambda c: "x".join(str(v) for v in c))
+def test_conv_gathers_upsample_concat(hip, case, storage, monkeypatch):
+    """A 3x3 conv over a channel concat of nearest upsamples runs as one halo-conv dispatch that reads each
+    channel chunk from its source at (y >> s, x >> s) (sox_conv_halo_*_upcat): no upsample or concat is
+    stored, and the output is the bits of the three-step path (SIMDONNX_HIP_NO_UPCAT) and the oracle's
+    within the 16-bit contract."""
+    from oracle.interp import run_plan
+    n, h, w, c, shifts, oc = case
+    pb = PlanBuilder()
+    srcs, xs = [], []
+    for i, sh in enumerate(shifts):
+        v = pb.input((n, c, h >> sh, w >> sh), NHWC, f"p{i}")
+        srcs.append(pb.resize_nearest(v, 1 << sh, name=f"up{i}") if sh else v)
+        xs.append(synth.uniform(44, i, (n, h >> sh, w >> sh, c), -1, 1))
+    fuse = pb.concat_channels(srcs, name="fuse")
+    y = pb.conv(fuse, synth.uniform(44, 10, (oc, c * len(shifts), 3, 3), -0.1, 0.1),
+                synth.uniform(44, 11, (oc,), -0.1, 0.1), pad=(1, 1, 1, 1), act="relu", name="conv")
+    plan = pb.build(y)
+    g = hip.graph(plan, storage)
+    assert [d[0] for d in g.dispatches] == ["conv_halo"]
+    assert g.kernels == [f"sox_conv_halo_{storage}_3x3s1_upcat"]
+    g.release()
+    got = run(hip, plan, xs, storage)
+    monkeypatch.setenv("SIMDONNX_HIP_NO_UPCAT", "1")
+    g = hip.graph(plan, storage)
+    names = [d[0] for d in g.dispatches]
+    assert "nearest" in names and names[-1] == "conv_halo", names
+    g.release()
+    ref = run(hip, plan, xs, storage)
+    assert got.tobytes() == ref.tobytes()
+    emu = {"f16": True, "bf16": "bf16"}[storage]
+    assert max_rel(got, run_plan(plan, xs, f16_storage=emu)) < 2e-2
+
+
 # (m, k, n): Gemm -> Softmax over rows whose N is not a multiple of 4 (the class head): the Gemm runs
 # on the LDS-DMA ring into rows padded to a multiple of 8, the Softmax reads that stride
 HEAD_CASES = [(300, 128, 1001), (2560, 192, 6625), (77, 64, 13)]
