@@ -73,6 +73,9 @@ typedef struct sox_igemm_args {
     const void* up[4];
     int32_t up_n, up_c;
     int32_t up_shift[4];
+    /* conv-ring kernels with a residual: res_shift > 0 reads it as the nearest upsample by 2^res_shift of
+     * [n][oh >> res_shift][ow >> res_shift][ldy] (the FPN's top-down Add, fused) */
+    int32_t res_shift, pad_;
 } sox_igemm_args;
 
 /*

@@ -64,11 +64,16 @@ struct ConvtOut {
     int ih, iw, kh, kw, oc;
     const float* bias;
 };
+// A conv's residual read as the nearest upsample by 2^shift of a map of (oh >> shift) x (ow >> shift)
+// pixels (shift 0: the residual has the output's rows).
+struct ResUp {
+    int shift, oh, ow;
+};
 
-template <typename T, int ACT, int TJ, int TI>
+template <typename T, int ACT, int TJ, int TI, bool RU = false>  // RU: ru may upsample the residual
 SOX_DEV void store_tile(T* __restrict__ Y, const T* __restrict__ R, int ldy, int M, int N, int m0, int n0,
                         const float16v (&acc)[TJ][TI], int act = 0, bool convt = false, ConvtOut ctv = {},
-                        bool pad_rows = false) {
+                        bool pad_rows = false, ResUp ru = {}) {
     typedef vec_t<T, 4> T4;
     const int lane = threadIdx.x & 63, l32 = lane & 31, hl = lane >> 5;
     // whole 4-element groups: rows of a multiple of 4 elements, or rows padded past the N tail
@@ -119,10 +124,17 @@ SOX_DEV void store_tile(T* __restrict__ Y, const T* __restrict__ R, int ldy, int
         // residual (the next node's Add, fused): the block's four 8-byte groups load together
         T4 rv[4];
         if (R) {
+            long rm = m;  // the residual's row
+            if constexpr (RU) {
+                if (ru.shift > 0) {
+                    const int q = m / ru.ow, x = m - q * ru.ow, y = q % ru.oh, b = q / ru.oh;
+                    rm = ((long)b * (ru.oh >> ru.shift) + (y >> ru.shift)) * (ru.ow >> ru.shift) + (x >> ru.shift);
+                }
+            }
             static_for<0, 4>([&](auto qq) {
                 constexpr int q = decltype(qq)::value;
                 const int n = n0 + j * 32 + 8 * q + 4 * hl;
-                const long o = (m < M && n < N) ? (long)m * ldy + n : 0;
+                const long o = (m < M && n < N) ? (RU ? rm : (long)m) * ldy + n : 0;
                 if (aligned) {
                     rv[q] = *(const T4*)(R + o);
                 } else {
@@ -476,6 +488,7 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
     const ConvtOut cto{p.ih, p.iw, p.ct_kh, p.ct_kw, p.ct_oc, (p.flags & SOX_F_BIAS) ? p.bias : nullptr};
     const bool ctp = CONV && (p.flags & SOX_F_CONVT);
     const bool pad_rows = (p.flags & SOX_F_PAD_ROWS) != 0;
+    const ResUp ru = CONV ? ResUp{p.res_shift, p.oh, p.ow} : ResUp{};
     // whole 16-byte chunks of every stored row (pad_rows: the row pitch covers N rounded up to 8)
     const bool lds_ok = EPI_LDS && !R && !ctp && (p.ldy & 7) == 0 && (pad_rows || (N & 7) == 0);
     auto epilogue = [&](int gs) __attribute__((always_inline)) {
@@ -497,10 +510,10 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
             }
         }
         switch (act) {
-        case SOX_ACT_NONE: store_tile<T, SOX_ACT_NONE>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, ctp, cto, pad_rows); break;
-        case SOX_ACT_RELU: store_tile<T, SOX_ACT_RELU>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, ctp, cto, pad_rows); break;
-        case SOX_ACT_GELU: store_tile<T, SOX_ACT_GELU>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, ctp, cto, pad_rows); break;
-        default: store_tile<T, -1>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, act, ctp, cto, pad_rows); break;
+        case SOX_ACT_NONE: store_tile<T, SOX_ACT_NONE, TJ, TI, CONV>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, ctp, cto, pad_rows, ru); break;
+        case SOX_ACT_RELU: store_tile<T, SOX_ACT_RELU, TJ, TI, CONV>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, ctp, cto, pad_rows, ru); break;
+        case SOX_ACT_GELU: store_tile<T, SOX_ACT_GELU, TJ, TI, CONV>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, 0, ctp, cto, pad_rows, ru); break;
+        default: store_tile<T, -1, TJ, TI, CONV>(Y, R, p.ldy, M, N, bm_cur + wm0, bn_cur + wn0, acc, act, ctp, cto, pad_rows, ru); break;
         }
         if (gs + 1 < total) {
             tile_origin(vid + (gs + 1) / nk * G, bm_cur, bn_cur);

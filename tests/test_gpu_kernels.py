@@ -342,6 +342,49 @@ def test_conv_gathers_upsample_concat(hip, case, storage, monkeypatch):
     assert max_rel(got, run_plan(plan, xs, f16_storage=emu)) < 2e-2
 
 
+# (n, h, w, levels, ic, c): an FPN top-down chain over `levels` pyramid levels (the finest h x w): 1x1
+# laterals of ic channels to c, then out_k = up2(out_{k+1}) + lat_k; the 4-level case is the detector's
+UPADD_CASES = [(1, 240, 240, 4, 16, 96), (2, 40, 24, 3, 32, 64), (1, 36, 52, 2, 8, 16)]
+
+
+@pytest.mark.parametrize("storage", ["f16", "bf16"])
+@pytest.mark.parametrize("case", UPADD_CASES, ids=lambda c: "x".join(str(v) for v in c))
+def test_fpn_topdown_add_in_lateral_conv(hip, case, storage, monkeypatch):
+    """The FPN's nearest-upsample + Add runs inside the lateral 1x1 conv that produces the addend (the
+    conv moves to the Add's place, the coarser level as its residual read at (y >> 1, x >> 1)): no upsample
+    dispatch and no lateral output stored; within the 16-bit contract of the separate passes
+    (SIMDONNX_HIP_NO_UPADD: the fused form rounds once) and of the oracle."""
+    from oracle.interp import run_plan
+    n, h, w, levels, ic, c = case
+    pb = PlanBuilder()
+    feats, xs = [], []
+    for i in range(levels):
+        ch = ic * (i + 1)
+        feats.append(pb.input((n, ch, h >> i, w >> i), NHWC, f"c{i}"))
+        xs.append(synth.uniform(45, i, (n, h >> i, w >> i, ch), -1, 1))
+    lat = [pb.conv(f, synth.uniform(45, 10 + i, (c, ic * (i + 1), 1, 1), -0.3, 0.3), None, name=f"lat{i}")
+           for i, f in enumerate(feats)]
+    out = lat[-1]
+    outs = []
+    for i in range(levels - 2, -1, -1):
+        out = pb.resize_nearest(out, 2, add=lat[i], name=f"up{i}")
+        outs.append(out)
+    plan = pb.build(outs[-1])  # each coarser level is read again as the next level's residual
+    g = hip.graph(plan, storage)
+    names = [d[0] for d in g.dispatches]
+    g.release()
+    assert "nearest" not in names and names == ["conv"] * levels, names
+    got = run(hip, plan, xs, storage)
+    monkeypatch.setenv("SIMDONNX_HIP_NO_UPADD", "1")
+    g = hip.graph(plan, storage)
+    assert [d[0] for d in g.dispatches].count("nearest") == levels - 1
+    g.release()
+    ref = run(hip, plan, xs, storage)
+    assert max_rel(got, ref) < {"f16": 2e-3, "bf16": 1e-2}[storage]
+    emu = {"f16": True, "bf16": "bf16"}[storage]
+    assert max_rel(got, run_plan(plan, xs, f16_storage=emu)) < 2e-2
+
+
 # (m, k, n): Gemm -> Softmax over rows whose N is not a multiple of 4 (the class head): the Gemm runs
 # on the LDS-DMA ring into rows padded to a multiple of 8, the Softmax reads that stride
 HEAD_CASES = [(300, 128, 1001), (2560, 192, 6625), (77, 64, 13)]
