@@ -406,6 +406,35 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
         prep(gs, q);
         fire(gs, q);
     };
+    // Dense A: a slice's DMA instructions go out in KS parts, one per k-step, each after that step's
+    // MFMAs (part 0 right after the slice barrier, parts 1.. during the next slice's first k-steps).
+    // A wave that issues global -> LDS DMA stalls at issue while the CU's ~64 B/cycle path drains; in
+    // parts, the stall falls while its MFMAs (and the other wave's) keep the matrix pipe busy, instead
+    // of every wave stopping at the barrier for the whole slice. Every part of slice g + STAGES - 1 is
+    // out before the vmcnt wait of slice g, so the waits count the same loads as before.
+    constexpr bool SPREAD = !CONV && KS >= 2;
+    constexpr int PER = (LOADS + KS - 1) / KS;  // DMA instructions per part
+    auto fire_part = [&](int gs, auto pp) __attribute__((always_inline)) {
+        constexpr int p0 = decltype(pp)::value * PER;
+        if constexpr (p0 == 0) {
+            if (gs % nk == 0 && gs < total) set_sources(vid + (gs / nk) * G);
+        }
+        const int k0 = (gs % nk) * BK;
+        unsigned char* st = smem + (gs % STAGES) * STAGE_BYTES;
+        static_for<p0, (p0 + PER < LOADS ? p0 + PER : LOADS)>([&](auto xx) {
+            constexpr int x = decltype(xx)::value;
+            if constexpr (x < A_IT) {
+                if (a_lane) __builtin_amdgcn_global_load_lds(a_src[x] + k0, LDS_PTR(st + (wave * A_IT + x) * CH_A), 16, 0, 0);
+            } else if constexpr (x < A_IT + B_IT) {
+                if (b_lane)
+                    __builtin_amdgcn_global_load_lds(b_src[x - A_IT] + k0, LDS_PTR(st + A_BYTES + (wave * B_IT + x - A_IT) * CH_B),
+                                                     16, 0, 0);
+            } else {
+                if (lane < BIAS_LANES)
+                    __builtin_amdgcn_global_load_lds(c_src, LDS_PTR(st + A_BYTES + B_BYTES + wave * BIAS_LANES * 16), 16, 0, 0);
+            }
+        });
+    };
 
     // fragment offsets: k-step s of a lane covers chunk 2s + l/32 of rows (row0 + l%32), stored at slot
     // (2s + l/32) ^ swz(row) = 2s ^ (l/32 ^ swz(row)): the offset of step 0 with bit 5 flipped by s
@@ -540,7 +569,11 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
                 wait_vmcnt<(STAGES - 2) * LOADS>();
                 wait_lgkmcnt0();
                 __builtin_amdgcn_s_barrier();
-                issue(gs + STAGES);  // into stage gs % STAGES; may already be a later tile's slice
+                // into stage gs % STAGES; may already be a later tile's slice
+                if constexpr (SPREAD)
+                    fire_part(gs + STAGES, std::integral_constant<int, 0>{});
+                else
+                    issue(gs + STAGES);
                 read_step(gs + 1, 0, na, nb);
             } else {
                 read_step(gs, s + 1, na, nb);
@@ -549,6 +582,11 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
                 constexpr int j = decltype(ji)::value / TI, i = decltype(ji)::value % TI;
                 acc[j][i] = mfma32x32x16(cb[j], ca[i], acc[j][i]);
             });
+            if constexpr (SPREAD && s + 1 < KS && (s + 1) * PER < LOADS) {
+                // part s + 1 of the slice whose part 0 went out after the last barrier (the prologue
+                // issued slices 0 .. STAGES - 1 whole)
+                if (gs >= 1) fire_part(gs - 1 + STAGES, std::integral_constant<int, s + 1>{});
+            }
             if constexpr (LN) {  // the step's 8 values of each of the lane's rows, by fp32 dot2
                 const T2 one = {(T)1.0f, (T)1.0f};
                 static_for<0, TI * 4>([&](auto ih) {
