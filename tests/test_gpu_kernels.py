@@ -528,6 +528,42 @@ def test_se_then_projection(hip, case, half):
 
 
 @pytest.mark.parametrize("half", [False, True], ids=["f32", "f16"])
+def test_se_fold_with_projection_planned_over_its_input(hip, half):
+    """The gate's input x is an intermediate value, dead after x * s, so the arena packer places the
+    projection's output over x. The folded projection reads x while it writes its output, so that
+    output moves to a buffer of its own and the fold still happens: no broadcast multiply dispatch,
+    and the result matches the unfused oracle."""
+    c, r, h, w, out = 96, 24, 9, 11, 40
+    cv = f16 if half else (lambda a: a)
+    x0 = cv(synth.uniform(12, 1, (1, h, w, c), -1, 1))
+    w1 = synth.normal(12, 2, (r, c, 1, 1), 0.2)
+    w2 = synth.normal(12, 3, (c, r, 1, 1), 0.2)
+    b1, b2 = synth.uniform(12, 4, (r,), -0.1, 0.1), synth.uniform(12, 5, (c,), -0.1, 0.1)
+    wp = cv(synth.normal(12, 6, (out, c, 1, 1), 0.1))
+    bp = synth.uniform(12, 7, (out,), -0.1, 0.1)
+    pb = PlanBuilder()
+    x0v = pb.input((1, c, h, w), NHWC, "x0")
+    xv = pb.unary("Relu", x0v, name="x")
+    gate = pb.channel_gate(xv, w1, b1, w2, b2, act1="relu", hard=True, alpha=1.0 / 6.0, beta=0.5, name="se")
+    hv = pb.mul(xv, gate, name="se_scale")
+    y = pb.conv(hv, wp, bp, stride=1, pad=0, name="project")
+    plan = pb.build(y)
+    vals = {v.name: v for v in plan.values}
+    off = plan.buf_offset
+    assert off[vals["x"].buf] == off[vals["project"].buf], "the packer no longer overlaps them: case untested"
+    g = hip.graph(plan, half)
+    names = [d[0] for d in g.dispatches]
+    assert "ew2" not in names, names
+    with HipInferenceSession(g) as s:
+        s.set_input(x0)
+        got = s.run().copy()
+    x = np.maximum(x0, 0)
+    s_ = O.channel_gate(x, w1.reshape(r, c), b1, w2.reshape(c, r), b2)
+    want = O.conv(cv(x * s_[:, None, None, :]), wp, bp, None)
+    assert max_rel(got, want) < TOL[half]
+
+
+@pytest.mark.parametrize("half", [False, True], ids=["f32", "f16"])
 def test_nearest_add_and_concat(hip, half):
     cv = f16 if half else (lambda a: a)
     x, add = cv(G["near_x"]), cv(G["near_add"])
