@@ -671,12 +671,15 @@ extern "C" __global__ void __launch_bounds__(256) sox_se_fc1(sox_se_args p) {
             wv[u] = *(const float4v*)(p.w1 + (long)j * p.c + c0 + min(4 * sub, cn - 4));
         }
     }
+    // cw channel lanes x nph chunk phases: a group of few channels takes more phases, so a depthwise
+    // conv of many tiles can hand over its per-tile partials (up to 64 per thread)
+    const int cw = cn <= 16 ? 16 : cn <= 32 ? 32 : SE_CG, nph = 256 / cw;
     {
-        const int ch = t % SE_CG, ph = t / SE_CG;
+        const int ch = t % cw, ph = t / cw;
         float acc = 0.0f;
         if (ch < cn)
             strided_foreach<16>(p.part + (long)b * p.chunks * p.c + c0 + ch, (long)ph * p.c, (long)p.chunks * p.c,
-                                4L * p.c, [&](long, float v) { acc += v; });
+                                (long)nph * p.c, [&](long, float v) { acc += v; });
         red[t] = acc;
     }
     // the W1 loads stay ahead of the barrier (issued with the first partials, one wait for both)
@@ -684,8 +687,14 @@ extern "C" __global__ void __launch_bounds__(256) sox_se_fc1(sox_se_args p) {
 #pragma unroll
         for (int u = 0; u < SE_FC1_U; u++) keep_in_vgprs(wv[u]);
     }
+    // the phases fold in a fixed binary tree, adjacent phases first ((0+1) + (2+3) for four)
+    for (int st = 1; st < nph; st *= 2) {
+        __syncthreads();
+        const int ph = t / cw;
+        if (ph % (2 * st) == 0 && ph + st < nph) red[t] += red[t + st * cw];
+    }
     __syncthreads();
-    if (t < SE_CG) mean[t] = ((red[t] + red[t + 64]) + (red[t + 128] + red[t + 192])) * (1.0f / p.hw);
+    if (t < cw) mean[t] = red[t] * (1.0f / p.hw);
     __syncthreads();
     float m4[4];
 #pragma unroll

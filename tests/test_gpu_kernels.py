@@ -189,7 +189,8 @@ def test_rgb_stem_on_matrix_cores(hip, case, storage, monkeypatch):
 
 
 @pytest.mark.parametrize("storage", ["f16", "bf16", "f32"])
-@pytest.mark.parametrize("case", [(240, 5, 1, 60, 60), (96, 5, 2, 120, 120), (576, 5, 1, 30, 30), (72, 3, 1, 44, 36)])
+@pytest.mark.parametrize("case", [(240, 5, 1, 60, 60), (96, 5, 2, 120, 120), (576, 5, 1, 30, 30), (72, 3, 1, 44, 36),
+                                  (16, 3, 2, 480, 480), (24, 3, 1, 100, 92), (16, 3, 1, 100, 92)])
 def test_se_gap_partials_from_depthwise(hip, case, storage, monkeypatch):
     """Depthwise conv -> SE gate -> x * gate -> 1x1 projection (the MobileNetV3 block tail): the
     depthwise tiles write the gate's GAP partials (no gap_part dispatch), agreeing with the separate
