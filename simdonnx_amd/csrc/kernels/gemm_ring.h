@@ -406,14 +406,16 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
         prep(gs, q);
         fire(gs, q);
     };
-    // Dense A: a slice's DMA instructions go out in KS parts, one per k-step, each after that step's
-    // MFMAs (part 0 right after the slice barrier, parts 1.. during the next slice's first k-steps).
-    // A wave that issues global -> LDS DMA stalls at issue while the CU's ~64 B/cycle path drains; in
-    // parts, the stall falls while its MFMAs (and the other wave's) keep the matrix pipe busy, instead
-    // of every wave stopping at the barrier for the whole slice. Every part of slice g + STAGES - 1 is
-    // out before the vmcnt wait of slice g, so the waits count the same loads as before.
+    // Dense A: a slice's DMA instructions go out in two parts: part 0 right after the slice barrier,
+    // part 1 after the next k-step's MFMAs. A wave that issues global -> LDS DMA stalls at issue while
+    // the CU's ~64 B/cycle path drains; in two parts the stall falls while its MFMAs (and the other
+    // wave's) keep the matrix pipe busy, and the loads still go out early enough to land before the
+    // slice's vmcnt wait (one part per k-step over all four k-steps left the last part too little time).
+    // Every part of slice g + STAGES - 1 is out before the vmcnt wait of slice g, so the waits count the
+    // same loads as before.
     constexpr bool SPREAD = !CONV && KS >= 2;
-    constexpr int PER = (LOADS + KS - 1) / KS;  // DMA instructions per part
+    constexpr int NPARTS = 2;
+    constexpr int PER = (LOADS + NPARTS - 1) / NPARTS;  // DMA instructions per part
     auto fire_part = [&](int gs, auto pp) __attribute__((always_inline)) {
         constexpr int p0 = decltype(pp)::value * PER;
         if constexpr (p0 == 0) {
@@ -582,7 +584,7 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
                 constexpr int j = decltype(ji)::value / TI, i = decltype(ji)::value % TI;
                 acc[j][i] = mfma32x32x16(cb[j], ca[i], acc[j][i]);
             });
-            if constexpr (SPREAD && s + 1 < KS && (s + 1) * PER < LOADS) {
+            if constexpr (SPREAD && s + 1 < NPARTS && (s + 1) * PER < LOADS) {
                 // part s + 1 of the slice whose part 0 went out after the last barrier (the prologue
                 // issued slices 0 .. STAGES - 1 whole)
                 if (gs >= 1) fire_part(gs - 1 + STAGES, std::integral_constant<int, s + 1>{});
