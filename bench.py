@@ -300,6 +300,7 @@ def bench_network(key: str, steps: int, replay: bool = True):
     with HipInferenceSession(g) as s:
         s.set_input(ins[0])
         s.set_replay(replay)
+        replayed = s.replaying
         s.run()
         s.time(200)  # ~0.1 s: the clock ramps up under sustained load
         ms = s.time(steps) / steps
@@ -332,6 +333,7 @@ def bench_network(key: str, steps: int, replay: bool = True):
                         bound=bound, frac=round(frac, 4)))
     return dict(workload=desc, ms_per_image=round(ms / images, 4), images_per_s=round(images / (ms * 1e-3), 1),
                 ms_per_batch=round(ms, 4), ms_per_image_with_staging=round(ms_e2e / images, 4), dispatches=ndisp,
+                replay=replayed,
                 gflop=round(tot_fl / 1e9, 3), algorithmic_mb=round(tot_by / 1e6, 1),
                 kernel_sum_ms=round(sum(t for _, _, t in prof), 4), kernels=out[:8])
 

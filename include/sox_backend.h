@@ -132,6 +132,16 @@ int sox_plan_set_io(sox_plan* plan, const int32_t* inputs, int32_t ninputs, int3
 int sox_backend_default(sox_backend** backend);   /* Default: device 0, re-created after a device loss */
 int sox_backend_info(sox_backend* backend, sox_device_info* info);
 int sox_backend_is_lost(sox_backend* backend);
+/* No counterpart in the reference (its analogue is the Vulkan validation layer, VkDevice.cs:176): a
+ * backend that touches no device. Graphs built on it run every graph-creation step (the rewrites,
+ * the arena changes, const packing, kernel choice against the embedded code objects' symbol tables)
+ * and can be inspected (dispatch_*, value_place, const/arena bytes), but sessions, CTC heads, image
+ * sessions, unit runners and extension code objects need a device and return SOX_E_UNSUPPORTED.
+ * info = NULL describes an MI355X (gfx950, 256 CUs, 8 XCDs). For host-only checks (sanitizer builds,
+ * CI without a GPU). */
+int sox_backend_create_offline(const sox_device_info* info, sox_backend** backend);
+/* Frees an offline backend (the device backend of sox_backend_default lives for the process). */
+void sox_backend_destroy(sox_backend* backend);
 /* Loads an extension's code object (an embedded resource of its owner, ShaderResources.Open). */
 int sox_backend_load_module(sox_backend* backend, const void* image, size_t bytes, void** module);
 
@@ -175,6 +185,13 @@ int sox_graph_dispatch_info(sox_graph* graph, int32_t index, char* name, size_t 
 /* The code object function dispatch `index` launches (its tiling, e.g. sox_gemm_f16_256x192_w8k64s2),
  * next to the op label of sox_graph_dispatch_info: what a per-kernel profiler trace names it. */
 int sox_graph_dispatch_kernel(sox_graph* graph, int32_t index, char* kernel, size_t kernel_cap);
+/* The arena and const bindings dispatch `index` is patched with, in kernarg order (VkDispatch.Binds,
+ * VkGraph.cs:24-31): up to cap written, *n = the count. */
+int sox_graph_dispatch_binds(sox_graph* graph, int32_t index, sox_bind* binds, int32_t cap, int32_t* n);
+/* The place of activation `value` in a session's slab after the graph-creation rewrites (BufOffset x
+ * element size, VkGraph.cs:362-368): byte offset and size. A value moved to a buffer of its own moves
+ * with its views, which report the same offset. */
+int sox_graph_value_place(sox_graph* graph, int32_t value, uint64_t* offset, uint64_t* bytes);
 uint64_t sox_graph_arena_bytes(sox_graph* graph);
 uint64_t sox_graph_const_bytes(sox_graph* graph);
 /* Last build error text (NotSupportedException message analogue). */
@@ -183,6 +200,28 @@ const char* sox_last_error(void);
 /* ---- session (VkInferenceSession); not thread-safe: one per thread ---- */
 int sox_session_create(sox_graph* graph, sox_session** session);
 void sox_session_destroy(sox_session* session);
+
+/* ---- shared session buffers (VkBufferPool / VkSessionBuffers, Backends/Vulkan/VkBatch.cs:6-25,
+ * VkSession.cs:10-55) ----
+ * The arena slab, device staging and pinned fp32 input / output staging of the sessions of one owner
+ * that run one at a time (one shape-varying OCR stage): each session then costs only its dispatch
+ * list, and only the largest session's memory is held. The buffers grow (to the need, and by at least
+ * half again) when a session needs more; growing makes every session created on the pool before it
+ * stale. Borrowing sessions enqueue on the pool's one stream, so their runs never overlap on the
+ * device; the host staging is shared, so write a session's input only after the previous session's
+ * Wait. Not thread-safe. */
+typedef struct sox_buffer_pool sox_buffer_pool;
+int sox_buffer_pool_create(sox_backend* backend, sox_buffer_pool** pool);   /* VkBackend.CreateBufferPool (VkBackend.cs:220) */
+/* VkBufferPool.Dispose: the buffers are freed with the last session that borrows them. */
+void sox_buffer_pool_destroy(sox_buffer_pool* pool);
+/* The pool's arena slab size and generation (bumped by each growth). */
+int sox_buffer_pool_info(sox_buffer_pool* pool, uint64_t* arena_bytes, int32_t* generation);
+/* NewSession(model, shape, options, pool) (VkBackend.cs:205-216): a session on the pool's buffers. */
+int sox_session_create_pooled(sox_graph* graph, sox_buffer_pool* pool, sox_session** session);
+/* IsStale (VkSession.cs:178-180): 1 once another session on the same pool grew its buffers. A stale
+ * session cannot run: run / submit / time / profile / read_value / value_ptr / input / output return
+ * SOX_E_INVALID with a message (sox_last_error); destroy it and create it again. */
+int sox_session_is_stale(sox_session* session);
 /* Mapped fp32 staging of graph input `index` / the output, in the plan's physical layout. */
 int sox_session_input(sox_session* session, int32_t index, float** host, int64_t* count);
 int sox_session_output(sox_session* session, float** host, int64_t* count);
@@ -190,8 +229,12 @@ int sox_session_output(sox_session* session, float** host, int64_t* count);
 int sox_session_run(sox_session* session);
 int sox_session_submit(sox_session* session);
 int sox_session_wait(sox_session* session);
-/* Replay the dispatch sequence from a captured HIP graph (1) or launch it node by node (0). */
+/* Replay the dispatch sequence from a captured HIP graph (1) or launch it node by node (0). While a
+ * rocprofiler-sdk tool (rocprofv3) is loaded into the process, replay stays off (one note on stderr):
+ * captured replay under its kernel tracer has crashed the host process. */
 int sox_session_set_replay(sox_session* session, int32_t on);
+/* 1 when the session replays a captured HIP graph, 0 when it launches node by node. */
+int sox_session_is_replaying(sox_session* session);
 /* Device-side timing with HIP events on the session stream: `iters` back-to-back enqueues of the
  * dispatch list (flags bit0: include the staging copies/conversions), total ms. */
 enum { SOX_RUN_STAGING = 1, SOX_RUN_DISPATCHES = 2 };

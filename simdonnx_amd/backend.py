@@ -66,6 +66,27 @@ class HipBackend:
         return cls._default
 
     @classmethod
+    def offline(cls, info: Optional[N.DeviceInfo] = None) -> "HipBackend":
+        """A backend that touches no device (sox_backend_create_offline): graphs lower completely and
+        can be inspected, but cannot run. ``info`` None describes an MI355X."""
+        h = N.c_void_p()
+        N.check(N.backend().sox_backend_create_offline(ctypes.byref(info) if info is not None else None,
+                                                       ctypes.byref(h)), "HipBackend.offline")
+        b = cls(h)
+        b._offline = True
+        return b
+
+    def close(self):
+        """Frees an offline backend (the device backend lives for the process)."""
+        if getattr(self, "_offline", False) and self.h:
+            N.backend().sox_backend_destroy(self.h)
+            self.h = None
+
+    def create_buffer_pool(self) -> "HipBufferPool":
+        """CreateBufferPool (VkBackend.cs:220): buffers shared by sessions that run one at a time."""
+        return HipBufferPool(self)
+
+    @classmethod
     def try_default(cls) -> Optional["HipBackend"]:
         """TryGetDefault (VkBackend.cs:75-86): None when no device can be opened."""
         try:
@@ -88,10 +109,10 @@ class HipBackend:
         """f16: True / "f16" (fp16 storage), "bf16" (bfloat16 storage) or False / "f32"."""
         return HipGraphModel(self, plan, f16)
 
-    def new_session(self, plan: ExecPlan, f16=True) -> "HipInferenceSession":
-        """NewSession(model, shape, opt) (VkBackend.cs:238-243) for an already compiled plan."""
+    def new_session(self, plan: ExecPlan, f16=True, pool: Optional["HipBufferPool"] = None) -> "HipInferenceSession":
+        """NewSession(model, shape, opt[, pool]) (VkBackend.cs:205-243) for an already compiled plan."""
         g = self.graph(plan, f16)
-        s = HipInferenceSession(g)
+        s = HipInferenceSession(g, pool)
         g.release()  # the session holds its own reference
         return s
 
@@ -125,6 +146,47 @@ class HipBackend:
         self._ext_keep += [emit_fn, consts_fn]
         N.check(N.backend().sox_backend_register_ext(self.h, name.encode(), emit_fn, consts_fn, None),
                 "register_ext")
+
+
+class HipBufferPool:
+    """VkBufferPool analogue (Backends/Vulkan/VkBatch.cs:6-25): the arena slab and staging shared by
+    the sessions of one owner that run one at a time; grows to the largest, making earlier sessions
+    stale. Not thread-safe."""
+
+    def __init__(self, backend: HipBackend):
+        self.backend = backend
+        h = N.c_void_p()
+        N.check(N.backend().sox_buffer_pool_create(backend.h, ctypes.byref(h)), "CreateBufferPool")
+        self.h = h
+
+    @property
+    def arena_bytes(self) -> int:
+        n = N.c_uint64()
+        N.check(N.backend().sox_buffer_pool_info(self.h, ctypes.byref(n), None), "pool info")
+        return int(n.value)
+
+    @property
+    def generation(self) -> int:
+        g = N.c_int32()
+        N.check(N.backend().sox_buffer_pool_info(self.h, None, ctypes.byref(g)), "pool info")
+        return int(g.value)
+
+    def close(self):
+        if self.h:
+            N.backend().sox_buffer_pool_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
 
 
 class HipGraphView:
@@ -234,6 +296,20 @@ class HipGraphModel:
     def arena_bytes(self) -> int:
         return int(N.backend().sox_graph_arena_bytes(self.h))
 
+    def value_place(self, value: int):
+        """(byte offset, bytes) of an activation in a session's slab after the graph-creation rewrites."""
+        off, n = N.c_uint64(), N.c_uint64()
+        N.check(N.backend().sox_graph_value_place(self.h, value, ctypes.byref(off), ctypes.byref(n)), "value_place")
+        return int(off.value), int(n.value)
+
+    def binds(self, index: int):
+        """The (slot, offset, size) bindings dispatch `index` is patched with, in kernarg order."""
+        n = N.c_int32()
+        N.check(N.backend().sox_graph_dispatch_binds(self.h, index, None, 0, ctypes.byref(n)), "dispatch_binds")
+        arr = (N.Bind * max(n.value, 1))()
+        N.check(N.backend().sox_graph_dispatch_binds(self.h, index, arr, n.value, ctypes.byref(n)), "dispatch_binds")
+        return [(b.slot, int(b.offset), int(b.size)) for b in arr[: n.value]]
+
     @property
     def const_bytes(self) -> int:
         return int(N.backend().sox_graph_const_bytes(self.h))
@@ -242,10 +318,14 @@ class HipGraphModel:
 class HipInferenceSession:
     """VkInferenceSession analogue: one arena slab, mapped fp32 staging; not thread-safe."""
 
-    def __init__(self, graph: HipGraphModel):
+    def __init__(self, graph: HipGraphModel, pool: Optional[HipBufferPool] = None):
         self.graph = graph
+        self.pool = pool
         h = N.c_void_p()
-        N.check(N.backend().sox_session_create(graph.h, ctypes.byref(h)), "HipInferenceSession")
+        if pool is None:
+            N.check(N.backend().sox_session_create(graph.h, ctypes.byref(h)), "HipInferenceSession")
+        else:
+            N.check(N.backend().sox_session_create_pooled(graph.h, pool.h, ctypes.byref(h)), "HipInferenceSession")
         self.h = h
         self._inputs = []
         lib = N.backend()
@@ -277,18 +357,33 @@ class HipInferenceSession:
         self.close()
 
     @property
+    def is_stale(self) -> bool:
+        """IsStale (VkSession.cs:178-180): a later session on the same buffer pool grew its buffers."""
+        return bool(N.backend().sox_session_is_stale(self.h))
+
+    def _current(self):
+        # the staging windows of a stale pooled session were freed by the growth: refuse, as Run does
+        if self.pool is not None and self.is_stale:
+            p = ctypes.POINTER(N.c_float)()
+            N.check(N.backend().sox_session_input(self.h, 0, ctypes.byref(p), None), "stale session")
+
+    @property
     def input(self) -> np.ndarray:
         """Mapped fp32 staging of input 0, in the plan's physical layout (flat)."""
+        self._current()
         return self._inputs[0]
 
     def get_input(self, i: int) -> np.ndarray:
+        self._current()
         return self._inputs[i]
 
     @property
     def output(self) -> np.ndarray:
+        self._current()
         return self._output
 
     def set_input(self, x: np.ndarray, i: int = 0):
+        self._current()
         self._inputs[i][:] = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
 
     def run(self) -> np.ndarray:
@@ -304,6 +399,11 @@ class HipInferenceSession:
 
     def set_replay(self, on: bool):
         N.check(N.backend().sox_session_set_replay(self.h, int(on)), "replay")
+
+    @property
+    def replaying(self) -> bool:
+        """Whether runs replay a captured HIP graph (off while a rocprofiler-sdk tool is loaded)."""
+        return bool(N.backend().sox_session_is_replaying(self.h))
 
     def time(self, iters: int, staging: bool = False) -> float:
         """Device ms for `iters` back-to-back enqueues, measured with HIP events on the session stream."""

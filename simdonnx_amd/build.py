@@ -141,11 +141,48 @@ def build_libs(verbose=False):
     return thin, be
 
 
+SAN_DIR = os.path.join(BUILD, "sanitize")
+SAN_BACKEND = os.path.join(SAN_DIR, "libsoxbackend.so")
+SAN_FLAGS = ["-fsanitize=address,undefined", "-fno-sanitize-recover=undefined", "-shared-libasan"]
+
+
+def _host_cxx() -> str:
+    cxx = os.path.join(ROCM, "llvm", "bin", "clang++")
+    return cxx if os.path.exists(cxx) else _hipcc()
+
+
+def sanitizer_runtime() -> str:
+    """The shared AddressSanitizer runtime (with UndefinedBehaviorSanitizer) of the host compiler that
+    builds the sanitizer library: a process must preload it to load that library ("" when absent)."""
+    r = subprocess.run([_host_cxx(), "-print-file-name=libclang_rt.asan-x86_64.so"], capture_output=True, text=True)
+    path = r.stdout.strip()
+    return path if r.returncode == 0 and os.path.isabs(path) and os.path.exists(path) else ""
+
+
+def build_sanitized_backend(verbose=False):
+    """The backend library again with its host code built under AddressSanitizer and
+    UndefinedBehaviorSanitizer, into _build/sanitize/ (host code only: it embeds the same code objects
+    and links the same libsoxhip.so). Loaded through SIMDONNX_HIP_BACKEND_LIB with the sanitizer
+    runtime preloaded, it runs the host lowering (graph-creation rewrites, arena moves, const packing,
+    kernel choice) of every workload plan on a backend created without a device
+    (tests/test_host_lowering.py)."""
+    os.makedirs(SAN_DIR, exist_ok=True)
+    _run([_host_cxx(), "-O1", "-g", "-fno-omit-frame-pointer", *SAN_FLAGS, "-fPIC", "-std=c++17", "-Wall",
+          "-Wno-unused-result", f"-I{BUILD}", "-shared", "-o", SAN_BACKEND, os.path.join(HDIR, "backend.cpp"),
+          os.path.join(BUILD, "resources.S"), f"-L{LIB}", "-lsoxhip", "-Wl,-rpath,$ORIGIN/../../lib",
+          f"-Wl,-rpath,{ROCM}/lib"])
+    if verbose:
+        print("built", SAN_BACKEND, flush=True)
+    return SAN_BACKEND
+
+
 def build(verbose=False):
     objs = build_code_objects(verbose)
     write_resources(objs)
     build_ext_examples(verbose)
-    return build_libs(verbose)
+    libs = build_libs(verbose)
+    build_sanitized_backend(verbose)
+    return libs
 
 
 if __name__ == "__main__":

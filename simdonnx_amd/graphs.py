@@ -175,26 +175,28 @@ def mobilenetv3_backbone(pb: PlanBuilder, x: int, seed: int, ids: _Ids, name="mb
     return y, taps
 
 
-def mobilenetv3_small(seed: int = 3, n=1, size=640, scales=None):
+def mobilenetv3_small(seed: int = 3, n=1, size=640, scales=None, input_id=10_000):
     """Config 3: the MobileNetV3-small block stack at 3 x size x size, input ~ N(0,1), He-normal
-    weights with folded BatchNorms (scales: see _bn_scale)."""
+    weights with folded BatchNorms (scales: see _bn_scale; {} = the plain He-normal weights). The input
+    is tensor `input_id` of the seed: the default one is the calibration image, others are held out."""
     pb = PlanBuilder()
     ids = _Ids()
     x = pb.input((n, 3, size, size), NHWC, "image")
     y, _ = mobilenetv3_backbone(pb, x, seed, ids, model="mbv3", scales=scales)
     plan = pb.build(y)
-    xin = synth.normal(seed, 10_000, (n, size, size, 3), 1.0)
+    xin = synth.normal(seed, input_id, (n, size, size, 3), 1.0)
     return plan, [xin]
 
 
-def dbnet(seed: int = 4, n=1, size=960, scales=None, logit=False):
+def dbnet(seed: int = 4, n=1, size=960, scales=None, logit=False, input_id=10_000):
     """Config 4: DBNet-style detector - MobileNetV3-small backbone, 4-level FPN (1x1 laterals to 96,
     nearest x2 + add top-down, 3x3 convs 96->24 per level, upsample + concat to 96 at 1/4 scale), head
     conv3x3 + BN + ReLU, ConvT 2x2 s2 + BN + ReLU, ConvT 2x2 s2 + bias + Sigmoid -> 1 x size x size.
     The BatchNormalization after the first ConvTranspose is not foldable (OnnxRewrites.cs:78-82) and
     lowers to per-channel Mul + Add(+ReLU) (GraphCompiler.cs:1898-1923). He-normal weights with the
-    folded BatchNorms of every other conv (scales: see _bn_scale); logit=True ends at the logit (no
-    sigmoid), for calibration."""
+    folded BatchNorms of every other conv (scales: see _bn_scale; {} = the plain He-normal weights);
+    logit=True ends at the logit (no sigmoid), for calibration. The input is tensor `input_id` of the
+    seed: the default one is the calibration image, others are held out."""
     pb = PlanBuilder()
     ids = _Ids()
     x = pb.input((n, 3, size, size), NHWC, "image")
@@ -235,7 +237,7 @@ def dbnet(seed: int = 4, n=1, size=960, scales=None, logit=False):
     y = convt(h, synth.he_normal(seed, ids(), (q, 1, 2, 2)), _bias(seed, ids, 1), act="none" if logit else "sigmoid",
               name="head.convt2")
     plan = pb.build(y)
-    xin = synth.normal(seed, 10_000, (n, size, size, 3), 1.0)
+    xin = synth.normal(seed, input_id, (n, size, size, 3), 1.0)
     return plan, [xin]
 
 

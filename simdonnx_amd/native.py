@@ -11,7 +11,9 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(HERE, "lib")
 THIN_PATH = os.path.join(LIB_DIR, "libsoxhip.so")
-BACKEND_PATH = os.path.join(LIB_DIR, "libsoxbackend.so")
+# SIMDONNX_HIP_BACKEND_LIB names another build of the same library: the host-sanitizer build
+# (simdonnx_amd.build.build_sanitized_backend) that the device-free lowering checks load
+BACKEND_PATH = os.environ.get("SIMDONNX_HIP_BACKEND_LIB") or os.path.join(LIB_DIR, "libsoxbackend.so")
 
 c_int32, c_int64, c_uint32, c_uint64, c_float, c_void_p, c_size_t = (
     ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_float, ctypes.c_void_p,
@@ -187,6 +189,8 @@ BACKEND_API = {
     "sox_plan_set_arena": (c_int32, [c_void_p, ctypes.POINTER(c_int64), c_int32, c_int64]),
     "sox_plan_set_io": (c_int32, [c_void_p, ctypes.POINTER(c_int32), c_int32, c_int32]),
     "sox_backend_default": (c_int32, [ctypes.POINTER(c_void_p)]),
+    "sox_backend_create_offline": (c_int32, [c_void_p, ctypes.POINTER(c_void_p)]),
+    "sox_backend_destroy": (None, [c_void_p]),
     "sox_backend_info": (c_int32, [c_void_p, ctypes.POINTER(DeviceInfo)]),
     "sox_backend_is_lost": (c_int32, [c_void_p]),
     "sox_backend_load_module": (c_int32, [c_void_p, c_void_p, c_size_t, ctypes.POINTER(c_void_p)]),
@@ -209,11 +213,18 @@ BACKEND_API = {
     "sox_graph_dispatch_kernel": (c_int32, [c_void_p, c_int32, ctypes.c_char_p, c_size_t]),
     "sox_graph_dispatch_info": (c_int32, [c_void_p, c_int32, ctypes.c_char_p, c_size_t, ctypes.POINTER(c_uint32),
                                           ctypes.POINTER(c_int32)]),
+    "sox_graph_dispatch_binds": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, ctypes.POINTER(c_int32)]),
+    "sox_graph_value_place": (c_int32, [c_void_p, c_int32, ctypes.POINTER(c_uint64), ctypes.POINTER(c_uint64)]),
     "sox_graph_arena_bytes": (c_uint64, [c_void_p]),
     "sox_graph_const_bytes": (c_uint64, [c_void_p]),
     "sox_last_error": (ctypes.c_char_p, []),
     "sox_session_create": (c_int32, [c_void_p, ctypes.POINTER(c_void_p)]),
     "sox_session_destroy": (None, [c_void_p]),
+    "sox_buffer_pool_create": (c_int32, [c_void_p, ctypes.POINTER(c_void_p)]),
+    "sox_buffer_pool_destroy": (None, [c_void_p]),
+    "sox_buffer_pool_info": (c_int32, [c_void_p, ctypes.POINTER(c_uint64), ctypes.POINTER(c_int32)]),
+    "sox_session_create_pooled": (c_int32, [c_void_p, c_void_p, ctypes.POINTER(c_void_p)]),
+    "sox_session_is_stale": (c_int32, [c_void_p]),
     "sox_session_input": (c_int32, [c_void_p, c_int32, ctypes.POINTER(ctypes.POINTER(c_float)),
                                     ctypes.POINTER(c_int64)]),
     "sox_session_output": (c_int32, [c_void_p, ctypes.POINTER(ctypes.POINTER(c_float)), ctypes.POINTER(c_int64)]),
@@ -221,6 +232,7 @@ BACKEND_API = {
     "sox_session_submit": (c_int32, [c_void_p]),
     "sox_session_wait": (c_int32, [c_void_p]),
     "sox_session_set_replay": (c_int32, [c_void_p, c_int32]),
+    "sox_session_is_replaying": (c_int32, [c_void_p]),
     "sox_session_time": (c_int32, [c_void_p, c_int32, c_int32, ctypes.POINTER(c_float)]),
     "sox_session_profile": (c_int32, [c_void_p, c_int32, ctypes.POINTER(c_float), c_int32]),
     "sox_session_read_value": (c_int32, [c_void_p, c_int32, ctypes.POINTER(c_float), c_int64]),
