@@ -51,12 +51,62 @@ def test_matmul_bias_gelu_fp32(hip):
     assert max_rel(got, want) <= 1e-4
 
 
-@pytest.mark.parametrize("half", [True, False], ids=["f16", "f32"])
-def test_mobilenetv3_small(hip, half):
+def test_mobilenetv3_small_fp32(hip):
     plan, ins = graphs.mobilenetv3_small()
-    got = run_gpu(hip, plan, ins, half)
+    got = run_gpu(hip, plan, ins, False)
+    assert max_rel(got, run_plan(plan, ins)) <= 1e-4
+
+
+# Whole 16-bit convnets (configs 3 and 4) against the fp32 oracle and against the oracle's emulation of
+# the storage contract (the same roundings at the same points, Backends/Vulkan/VkGraph.cs:33-43). Each
+# emulation bound is about twice the error measured on one MI355X (noted per case; the runs are
+# deterministic). The distance to the emulation is of the same order as the emulation's own distance
+# from fp32: the GPU sums each dot product in another order, a last-bit difference flips some 16-bit
+# roundings, and 60-odd stored layers carry those flips to the output. The single-kernel tests hold
+# each kernel to 2e-3. "calibrated": the committed BatchNorm folds and the calibration image;
+# "held_out": the same weights on another input; "plain": the literal He-normal weights (no
+# BatchNorm folds), whose fp16 contract alone is 4.6e-2 off fp32 on the detector, so only the
+# emulation bound applies there (and bf16's 8-bit mantissa is 5e-2 / 1e-1 off fp32 by itself).
+CONVNET_CASES = {
+    # (network, weights / input, storage): (bound vs the fp32 oracle or None, bound vs the emulation)
+    ("mobilenetv3", "calibrated", "f16"): (2e-2, 1e-2),  # measured 5.2e-3 / 4.7e-3
+    ("mobilenetv3", "held_out", "f16"): (2e-2, 1e-2),  # 4.9e-3 / 5.2e-3
+    ("mobilenetv3", "plain", "f16"): (2e-2, 5e-3),  # 2.9e-3 / 2.1e-3
+    ("dbnet", "calibrated", "f16"): (2e-2, 2.2e-2),  # 1.07e-2 / 1.10e-2
+    ("dbnet", "held_out", "f16"): (2e-2, 2.3e-2),  # 1.73e-2 / 1.13e-2
+    ("dbnet", "plain", "f16"): (None, 8e-2),  # 4.5e-2 / 3.9e-2 (the emulation itself: 4.6e-2 off fp32)
+    ("mobilenetv3", "calibrated", "bf16"): (None, 8.5e-2),  # 4.0e-2 / 4.3e-2 (emulation: 5.2e-2)
+    ("dbnet", "calibrated", "bf16"): (None, 1.6e-1),  # 1.04e-1 / 7.8e-2 (emulation: 1.01e-1)
+}
+
+
+def _convnet(net, variant):
+    fn = {"mobilenetv3": graphs.mobilenetv3_small, "dbnet": graphs.dbnet}[net]
+    kw = {"calibrated": {}, "held_out": {"input_id": 10_001}, "plain": {"scales": {}}}[variant]
+    return fn(**kw)
+
+
+@pytest.mark.parametrize("net,variant,storage", list(CONVNET_CASES), ids=["-".join(k) for k in CONVNET_CASES])
+def test_convnet_16bit_against_fp32_and_contract(hip, net, variant, storage):
+    plan, ins = _convnet(net, variant)
+    got = run_gpu(hip, plan, ins, storage)
     want = run_plan(plan, ins)
-    assert max_rel(got, want) <= (2e-2 if half else 1e-4)
+    emu = run_plan(plan, ins, f16_storage=True if storage == "f16" else "bf16")
+    err, err_emu, contract = max_rel(got, want), max_rel(got, emu), max_rel(emu, want)
+    print(f"[gpu] {net} {variant} {storage}: max-rel {err:.2e} vs fp32, {err_emu:.2e} vs the contract "
+          f"emulation (the emulation itself {contract:.2e} vs fp32)", flush=True)
+    bound_fp32, bound_emu = CONVNET_CASES[(net, variant, storage)]
+    if bound_fp32 is not None:
+        assert err <= bound_fp32
+    assert err_emu <= bound_emu
+
+
+@pytest.mark.parametrize("net", ["mobilenetv3", "dbnet"])
+def test_plain_he_normal_convnet_fp32(hip, net):
+    """The literal config text (He-normal weights, no BatchNorm folds) on the fp32 path."""
+    plan, ins = _convnet(net, "plain")
+    got = run_gpu(hip, plan, ins, False)
+    assert max_rel(got, run_plan(plan, ins)) <= 1e-4
 
 
 def test_dbnet_detector_fp32(hip):
@@ -65,21 +115,6 @@ def test_dbnet_detector_fp32(hip):
     want = run_plan(plan, ins)
     assert got.shape == (1, 960, 960, 1)
     assert max_rel(got, want) <= 1e-4
-
-
-def test_dbnet_detector_fp16(hip):
-    """The fp16 detector (the benchmarked one) within 2e-2 of the fp32 CPU reference, and within 2e-2
-    of the CPU's emulation of the fp16 storage contract (the same roundings at the same points; it
-    pins the kernels to the contract rather than to the tolerance)."""
-    plan, ins = graphs.dbnet()
-    got = run_gpu(hip, plan, ins, True)
-    want = run_plan(plan, ins)
-    emu = run_plan(plan, ins, f16_storage=True)
-    err, err_emu = max_rel(got, want), max_rel(got, emu)
-    print(f"[gpu] detector fp16 max-rel {err:.4f} vs fp32, {err_emu:.4f} vs the fp16-contract emulation", flush=True)
-    assert got.shape == (1, 960, 960, 1)
-    assert err <= 2e-2
-    assert err_emu <= 2e-2
 
 
 def test_svtr_recognizer_fp16(hip):
