@@ -750,7 +750,8 @@ def test_conv_narrow_pad_value_is_fp32(hip):
 
 
 @pytest.mark.parametrize("storage", ["f16", "bf16"])
-def test_gemm_gelu_epilogue_within_one_ulp(hip, storage):
+@pytest.mark.parametrize("route", ["ring", "pp"])
+def test_gemm_gelu_epilogue_within_one_ulp(hip, storage, route, monkeypatch):
     """The 16-bit Gemm epilogue's GELU (one exp2 per element) over every fp16 value in [-8, 8] (every
     bf16 value for bf16): A = x e_0, W row 0 = 1, so each output is GELU(x) of one exact fp32
     accumulator. Against the float64 erf-GELU (scipy's erfc) it is within one ulp of the 16-bit
@@ -762,16 +763,21 @@ def test_gemm_gelu_epilogue_within_one_ulp(hip, storage):
     x = np.unique(np.concatenate([pos, -pos]).astype(np.float32))
     if storage == "bf16":
         x = np.unique(_bf16(np.linspace(-8, 8, 200001, dtype=np.float32)))
-    m = (len(x) + 63) // 64 * 64
-    a = np.zeros((m, 64), np.float32)
+    # the ring (K = 64), or the epilogue-under-MFMA kernel (K = 768, 256 x 128 tiles, >= 256 of them)
+    k, n = (64, 64) if route == "ring" else (768, 512)
+    if route == "pp":
+        monkeypatch.setenv("SIMDONNX_HIP_GEMMPP", "1")
+    m = max((len(x) + 255) // 256 * 256, 64 if route == "ring" else 16384)  # pp: >= 256 tiles (zero rows)
+    a = np.zeros((m, k), np.float32)
     a[: len(x), 0] = x
-    w = np.zeros((64, 64), np.float32)
+    w = np.zeros((k, n), np.float32)
     w[0, :] = 1.0
     pb = PlanBuilder()
-    av = pb.input((m, 64), None, "a")
+    av = pb.input((m, k), None, "a")
     y = pb.gemm(av, w, None, act="gelu", name="gemm")
     g = hip.graph(pb.build(y), storage)
     assert [d[0] for d in g.dispatches] == ["gemm"]
+    assert g.kernels[0].startswith("sox_gemmpp_" if route == "pp" else "sox_gemm_"), g.kernels
     with HipInferenceSession(g) as s:
         s.set_input(a)
         got = s.run().copy()[: len(x)]
@@ -784,6 +790,47 @@ def test_gemm_gelu_epilogue_within_one_ulp(hip, storage):
     ulp = np.ldexp(1.0, (exp - (10 if storage == "f16" else 7)).astype(np.int32))
     bad = np.abs(got - ref) > np.maximum(ulp, 1e-6)
     assert not bad.any(), (x[bad][:8], got[bad][:8], ref[bad][:8])
+
+
+@pytest.mark.parametrize("storage", ["f16", "bf16"])
+@pytest.mark.parametrize("m,n,act,bias", [(4096, 2048, "gelu", True), (8192, 3072, "gelu", True),
+                                          (6144, 1536, "relu", True), (6144, 1536, "none", False)],
+                         ids=["1-tile-per-cu", "config2", "uneven-relu", "uneven-none-nobias"])
+def test_gemm_pp_matches_ring_bitwise(hip, m, n, act, bias, storage, monkeypatch):
+    """Under SIMDONNX_HIP_GEMMPP, whole 256 x 128 tiles with K = 768 take the kernel that runs each
+    tile's epilogue under the next tile's MFMAs (gemm_pp.h). It accumulates the same 32x32x16 steps from
+    the bias in the same k order and applies the same activation as the LDS-DMA ring (the default), so
+    the two agree bit for bit; both within the fp16 (2e-3) / bf16 (8e-3) contract of the oracle on the rounded operands.
+    Shapes: one tile per workgroup (first tile and the trailing epilogue only), config 2 (three per
+    workgroup), and 288 tiles over 256 workgroups (one or two each)."""
+    from oracle.interp import _bf16
+    k = 768
+    rnd = f16 if storage == "f16" else _bf16
+    a = rnd(synth.normal(71, 1, (m, k), 1.0))
+    w = rnd(synth.normal(71, 2, (k, n), 0.05))
+    b = synth.uniform(71, 3, (n,), -0.1, 0.1) if bias else None
+    pb = PlanBuilder()
+    av = pb.input((m, k), None, "a")
+    y = pb.gemm(av, w, b, act=act, name="gemm")
+    plan = pb.build(y)
+    print(f"[gpu] gemm_pp {m}x{n}x{k} {act} bias={bias} {storage}", flush=True)
+    monkeypatch.setenv("SIMDONNX_HIP_GEMMPP", "1")
+    g = hip.graph(plan, storage)
+    assert g.kernels == [f"sox_gemmpp_{storage}_256x128_k768_{act}"], g.kernels
+    with HipInferenceSession(g) as s:
+        s.set_input(a)
+        got = s.run().copy()
+    g.release()
+    monkeypatch.delenv("SIMDONNX_HIP_GEMMPP")
+    g2 = hip.graph(plan, storage)
+    assert g2.kernels[0].startswith(f"sox_gemm_{storage}_"), g2.kernels
+    with HipInferenceSession(g2) as s:
+        s.set_input(a)
+        ring = s.run().copy()
+    g2.release()
+    assert got.tobytes() == ring.tobytes(), f"max diff {np.abs(got - ring).max()}"
+    want = O.gemm(a, w, b, act=act)
+    assert max_rel(got, want) < (2e-3 if storage == "f16" else 8e-3)
 
 
 @pytest.mark.parametrize("kernel", ["", "sox_conv_f16_256x128_w8k64s2"], ids=["default", "w8-256x128"])
