@@ -164,6 +164,24 @@ typedef struct sox_se_args {
     float alpha, beta, offset;
 } sox_se_args;
 
+/*
+ * Depthwise tiles (sox_dwt_args, dw.gap = 1) with the SE gate that reads their output run in the same
+ * launch: depthwise.comp + gap_part.comp + se_gate.comp (VkGraph.cs:595-605, 949-965) as one dispatch.
+ * Each workgroup stores its GAP partials and counts itself in sync[b][g] (a vector atomic increment
+ * that wraps to 0 at its last arrival, with agent-scope release / acquire fences around it). The last
+ * tile of channel group g runs sox_se_fc1's work for that group and counts in sync[b][groups]; the
+ * last group's workgroup runs sox_se_fc2's for every channel of image b (the gates, then the folded
+ * weights or s). No workgroup waits on another. The counters are 0 between launches; their memory
+ * (SOX_SLOT_SYNC) belongs to the session, zeroed when it is made. Taken when SIMDONNX_HIP_SE_IN_DW is
+ * set: the one-workgroup fc2 is slower than the separate passes on MI355X.
+ *   kernels: sox_dwt_{f16,bf16,f32}_k{3,5}s{1,2}_se, grid as sox_dwt_*, 256 threads
+ */
+typedef struct sox_dwt_se_args {
+    sox_dwt_args dw;
+    sox_se_args se;
+    uint32_t* sync; /* [n][groups + 1] */
+} sox_dwt_se_args;
+
 /* out[p, c] = act(x[p, c] op v[img(p), c]): NHWC per-channel broadcast (ew2 / ChannelBroadcast). */
 typedef struct sox_chan_args {
     const void* x;

@@ -147,7 +147,9 @@ int sox_backend_load_module(sox_backend* backend, const void* image, size_t byte
 
 /* ---- extension ops (ExtOp.EmitVulkan analogue) ---- */
 typedef struct sox_bind { int32_t slot; int32_t pad_; uint64_t offset, size; } sox_bind; /* VkBind, VkGraph.cs:12-21 */
-enum { SOX_SLOT_ARENA = 0, SOX_SLOT_CONSTS = 1, SOX_SLOT_DUMMY = 2 };
+/* SOX_SLOT_SYNC: the session's cross-workgroup counters (zeroed once, back at 0 after every launch that
+ * uses them; no counterpart in the reference, whose SE gate is a dispatch of its own) */
+enum { SOX_SLOT_ARENA = 0, SOX_SLOT_CONSTS = 1, SOX_SLOT_DUMMY = 2, SOX_SLOT_SYNC = 3 };
 /* ConstKind (Engine/Extensions.cs:144-159) as an id. */
 enum { SOX_CK_RAW = 0, SOX_CK_F32 = 1, SOX_CK_CONVWT = 2, SOX_CK_GEMMNK = 3, SOX_CK_DWW = 4, SOX_CK_CONVTW = 5,
        SOX_CK_F32T = 7 /* fp32, rank-2 view [a][b...] transposed to [b...][a] */ };
@@ -194,6 +196,8 @@ int sox_graph_dispatch_binds(sox_graph* graph, int32_t index, sox_bind* binds, i
 int sox_graph_value_place(sox_graph* graph, int32_t value, uint64_t* offset, uint64_t* bytes);
 uint64_t sox_graph_arena_bytes(sox_graph* graph);
 uint64_t sox_graph_const_bytes(sox_graph* graph);
+/* Bytes of cross-workgroup counters (SOX_SLOT_SYNC) each session of the graph holds (0: none). */
+uint64_t sox_graph_sync_bytes(sox_graph* graph);
 /* Last build error text (NotSupportedException message analogue). */
 const char* sox_last_error(void);
 

@@ -314,6 +314,12 @@ class HipGraphModel:
     def const_bytes(self) -> int:
         return int(N.backend().sox_graph_const_bytes(self.h))
 
+    @property
+    def sync_bytes(self) -> int:
+        """Bytes of cross-workgroup counters each session holds (the depthwise launches that run their SE
+        gate)."""
+        return int(N.backend().sox_graph_sync_bytes(self.h))
+
 
 class HipInferenceSession:
     """VkInferenceSession analogue: one arena slab, mapped fp32 staging; not thread-safe."""

@@ -66,20 +66,37 @@ template <typename T> SOX_DEV void keep_in_vgprs(T& v) {
     }
 }
 
-template <int U, typename T, typename F>
-SOX_DEV void strided_foreach(const T* __restrict__ x, long start, long n, long step, F&& f) {
+template <int U, typename T, typename L, typename F>
+SOX_DEV void strided_foreach_ld(L&& load, long start, long n, long step, F&& f) {
     if (start >= n) return;
     const long cnt = (n - 1 - start) / step + 1;  // elements start, start + step, ... < n
     for (long j0 = 0; j0 < cnt; j0 += U) {
         T v[U];
 #pragma unroll
-        for (int u = 0; u < U; u++) v[u] = x[start + (j0 + u < cnt ? j0 + u : cnt - 1) * step];
+        for (int u = 0; u < U; u++) v[u] = load(start + (j0 + u < cnt ? j0 + u : cnt - 1) * step);
 #pragma unroll
         for (int u = 0; u < U; u++) keep_in_vgprs(v[u]);
 #pragma unroll
         for (int u = 0; u < U; u++)
             if (j0 + u < cnt) f(start + (j0 + u) * step, v[u]);
     }
+}
+template <int U, typename T, typename F>
+SOX_DEV void strided_foreach(const T* __restrict__ x, long start, long n, long step, F&& f) {
+    strided_foreach_ld<U, T>([&](long i) { return x[i]; }, start, n, step, f);
+}
+
+// Data handed from workgroup to workgroup inside one launch (the fused SE gate) moves through
+// agent-scope atomics: they are performed at the agent's coherence point, so no cache-wide
+// write-back or invalidate (what an agent-scope fence costs on a multi-XCD part) is needed.
+// store_coherent returns the old value, which the caller hands to wait_performed: once the wave has
+// the old values, the stores are performed, before any later memory operation of the wave is issued.
+SOX_DEV float store_coherent(float* p, float v) {
+    return __hip_atomic_exchange(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+SOX_DEV void wait_performed(uint32_t dep) { asm volatile("" ::"v"(dep) : "memory"); }
+SOX_DEV float load_coherent(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Dot of a contiguous fp32 row with a vector, lanes striding the row, 8 loads in flight per lane.
@@ -226,7 +243,7 @@ template <typename T, int K, int S> struct DwtShape {
     static constexpr int LDS = HH * RP + K * K * PB;                     // halo + weights
 };
 
-template <typename T, int K, int S, bool GAP>
+template <typename T, int K, int S, bool GAP, bool COH = false>
 __device__ __forceinline__ void dwt_body(const sox_dwt_args& p, unsigned char* lds) {
     typedef DwtShape<T, K, S> D;
     constexpr int TH = D::TH, TW = D::TW, NP = D::NP, HH = D::HH, HW = D::HW, VB = D::VB, PB = D::PB, RP = D::RP;
@@ -349,8 +366,15 @@ __device__ __forceinline__ void dwt_body(const sox_dwt_args& p, unsigned char* l
         __syncthreads();
         if (pl == 0 && cok) {
             float* dst = p.part + ((long)b * p.tiles_x * p.tiles_y + tile) * p.c + c0;
+            if constexpr (COH) {  // read by the launch's last tile of the group (sox_dwt_*_se)
+                uint32_t dep = 0;
 #pragma unroll
-            for (int e = 0; e < 8; e++) dst[e] = red[cv * 8 + e];
+                for (int e = 0; e < 8; e++) dep |= __float_as_uint(store_coherent(dst + e, red[cv * 8 + e]));
+                wait_performed(dep);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++) dst[e] = red[cv * 8 + e];
+            }
         }
     }
 }
@@ -653,10 +677,12 @@ extern "C" __global__ void __launch_bounds__(256) sox_gap_f32_s(sox_gap_args p) 
 // shuffle reduces each row.
 constexpr int SE_CG = 64;
 constexpr int SE_FC1_U = 16;  // W1 rows prefetched per lane: r <= 16 * SE_FC1_U takes the one-round-trip path
-extern "C" __global__ void __launch_bounds__(256) sox_se_fc1(sox_se_args p) {
-    __shared__ float red[256];
-    __shared__ float mean[SE_CG];
-    const int g = blockIdx.x, b = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+// Channel group g of image b (256 threads; red: 256 floats, mean: SE_CG floats of LDS).
+// COH: the partials come from other workgroups of the same launch, and hid goes to one (coherent
+// loads and stores).
+template <bool COH = false>
+__device__ __forceinline__ void se_fc1_group(const sox_se_args& p, int g, int b, float* red, float* mean) {
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int c0 = g * SE_CG, cn = min(SE_CG, p.c - c0);
     const int sub = lane & 15, rq = lane >> 4;  // channel quad, row within the wave's four
     const bool vec = (p.c & 3) == 0;            // rows and groups start 16-byte aligned, cn % 4 == 0
@@ -678,8 +704,12 @@ extern "C" __global__ void __launch_bounds__(256) sox_se_fc1(sox_se_args p) {
         const int ch = t % cw, ph = t / cw;
         float acc = 0.0f;
         if (ch < cn)
-            strided_foreach<16>(p.part + (long)b * p.chunks * p.c + c0 + ch, (long)ph * p.c, (long)p.chunks * p.c,
-                                (long)nph * p.c, [&](long, float v) { acc += v; });
+            strided_foreach_ld<16, float>(
+                [&](long i) {
+                    const float* q = p.part + (long)b * p.chunks * p.c + c0 + ch + i;
+                    return COH ? load_coherent(q) : *q;
+                },
+                (long)ph * p.c, (long)p.chunks * p.c, (long)nph * p.c, [&](long, float v) { acc += v; });
         red[t] = acc;
     }
     // the W1 loads stay ahead of the barrier (issued with the first partials, one wait for both)
@@ -700,6 +730,13 @@ extern "C" __global__ void __launch_bounds__(256) sox_se_fc1(sox_se_args p) {
 #pragma unroll
     for (int e = 0; e < 4; e++) m4[e] = 4 * sub + e < cn ? mean[4 * sub + e] : 0.0f;  // 0: lane past the group
     float* hid = p.hid + ((long)b * p.groups + g) * p.r;
+    uint32_t dep = 0;
+    auto put = [&](int j, float v) {
+        if constexpr (COH)
+            dep |= __float_as_uint(store_coherent(hid + j, v));
+        else
+            hid[j] = v;
+    };
     if (pre) {
 #pragma unroll
         for (int u = 0; u < SE_FC1_U; u++) {
@@ -708,8 +745,9 @@ extern "C" __global__ void __launch_bounds__(256) sox_se_fc1(sox_se_args p) {
             float s = wv[u][0] * m4[0] + wv[u][1] * m4[1] + wv[u][2] * m4[2] + wv[u][3] * m4[3];
 #pragma unroll
             for (int o = 8; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-            if (sub == 0 && j < p.r) hid[j] = s;
+            if (sub == 0 && j < p.r) put(j, s);
         }
+        if constexpr (COH) wait_performed(dep);
         return;
     }
     // four rows per wave instruction, four instructions' loads in flight (clamped, branch-free)
@@ -733,9 +771,32 @@ extern "C" __global__ void __launch_bounds__(256) sox_se_fc1(sox_se_args p) {
 #pragma unroll
             for (int o = 8; o > 0; o >>= 1) s[u] += __shfl_xor(s[u], o, 64);
             const int j = j0 + 16 * u + rq;
-            if (sub == 0 && j < p.r) hid[j] = s[u];
+            if (sub == 0 && j < p.r) put(j, s[u]);
         }
     }
+    if constexpr (COH) wait_performed(dep);
+}
+
+extern "C" __global__ void __launch_bounds__(256) sox_se_fc1(sox_se_args p) {
+    __shared__ float red[256];
+    __shared__ float mean[SE_CG];
+    se_fc1_group(p, blockIdx.x, blockIdx.y, red, mean);
+}
+
+// A folded weight: w * gate rounded to fp32, then to T. The product is pinned in a register first:
+// the compiler otherwise may or may not fuse the multiply with the conversion into one
+// mixed-precision instruction that rounds once, depending on the surrounding code, and the separate
+// fc2 pass and the fused depthwise launch would differ in the last bit.
+template <typename T> __device__ __forceinline__ T se_scaled(T w, float gate) {
+    float prod = to_f(w) * gate;
+    keep_in_vgprs(prod);
+    return (T)prod;
+}
+
+// The gate of channel ch from its fc2 dot product z (before b2).
+__device__ __forceinline__ float se_gate_value(const sox_se_args& p, int ch, float z) {
+    z += (p.flags & 2) ? p.b2[ch] : 0.0f;
+    return ((p.flags & 8) ? fminf(fmaxf(z * p.alpha + p.beta, 0.0f), 1.0f) : sox_sigmoid(z)) + p.offset;
 }
 
 // fc2: the workgroup rebuilds h from the groups' partials in LDS (fixed summation order), then one
@@ -803,19 +864,18 @@ __device__ __forceinline__ void se_fc2_body(const sox_se_args& p) {
     } else {
         z = wave_sum(row_dot(p.w2 + (long)ch * p.r, p.r, lane, [&](int k) { return h[k]; }));
     }
-    z += (p.flags & 2) ? p.b2[ch] : 0.0f;
-    const float gate = ((p.flags & 8) ? fminf(fmaxf(z * p.alpha + p.beta, 0.0f), 1.0f) : sox_sigmoid(z)) + p.offset;
+    const float gate = se_gate_value(p, ch, z);
     if (fold) {
         T* __restrict__ wd = (T*)p.wdst;
         if (pre) {
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 const int n = lane + 64 * u;
-                if (n < p.wn) wd[(long)n * p.wk + ch] = (T)(to_f(__builtin_bit_cast(T, (WU)wsv[u])) * gate);
+                if (n < p.wn) wd[(long)n * p.wk + ch] = se_scaled(__builtin_bit_cast(T, (WU)wsv[u]), gate);
             }
         } else {
             strided_foreach<4>(ws + ch, (long)lane * p.wk, (long)p.wn * p.wk, 64L * p.wk,
-                               [&](long i, T v) { wd[ch + i] = (T)(to_f(v) * gate); });
+                               [&](long i, T v) { wd[ch + i] = se_scaled(v, gate); });
         }
     } else if (lane == 0) {
         ((T*)p.s)[(long)b * p.c + ch] = (T)gate;
@@ -825,6 +885,101 @@ __device__ __forceinline__ void se_fc2_body(const sox_se_args& p) {
 extern "C" __global__ void __launch_bounds__(256) sox_se_fc2_f16(sox_se_args p) { se_fc2_body<half_t>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_se_fc2_bf16(sox_se_args p) { se_fc2_body<bf16_t>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_se_fc2_f32(sox_se_args p) { se_fc2_body<float>(p); }
+
+// ------------------------------------------------------------------------------------------
+// Depthwise tiles + their SE gate in one launch (sox_dwt_se_args). After its tile, a workgroup counts
+// itself; the last tile of a channel group runs that group's fc1 (se_fc1_group), the last group's
+// workgroup runs fc2 for all of the image's channels. The arithmetic is sox_se_fc1's and sox_se_fc2's,
+// in the same order, so the gates and the folded weights equal the separate passes' bit for bit.
+// ------------------------------------------------------------------------------------------
+// Whether this workgroup is the last of `total` to arrive at `counter` (an agent-scope atomic
+// increment that wraps back to 0 at the last arrival). What the arrivers hand over went out with
+// store_coherent and wait_performed before the call, so it is performed before the count is; the last
+// arriver reads it with load_coherent after.
+__device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t total, uint32_t* flag) {
+    __syncthreads();
+    if (threadIdx.x == 0) *flag = atomicInc(counter, total - 1) == total - 1;
+    __syncthreads();
+    const bool last = *flag != 0;
+    asm volatile("" ::: "memory");
+    return last;
+}
+
+// fc2 of image b in one workgroup: h into LDS, then a wave per channel (NB channels' W2 rows in flight
+// per wave) into gate[] in LDS, then the folded weights (16-byte vectors along the channels) or s.
+// lds: >= 4 (align64(r) + c) bytes; r <= 256; c % 8 == 0.
+template <typename T>
+__device__ __forceinline__ void se_fc2_image(const sox_se_args& p, int b, float* lds) {
+    constexpr int NB = 8;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, nw = blockDim.x >> 6;
+    float* h = lds;
+    float* gate = lds + ((p.r + 63) & ~63);
+    const float* part = p.hid + (long)b * p.groups * p.r;
+    for (int k = t; k < p.r; k += blockDim.x) {
+        float s = (p.flags & 1) ? p.b1[k] : 0.0f;
+        strided_foreach_ld<16, float>([&](long i) { return load_coherent(part + k + i); }, 0, (long)p.groups * p.r,
+                                      p.r, [&](long, float v) { s += v; });
+        h[k] = (p.flags & 4) ? fmaxf(s, 0.0f) : s;
+    }
+    __syncthreads();
+    for (int c0 = wave * NB; c0 < p.c; c0 += nw * NB) {
+        float w2v[NB][4];
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+            const int ch = min(c0 + j, p.c - 1);
+#pragma unroll
+            for (int u = 0; u < 4; u++) w2v[j][u] = p.w2[(long)ch * p.r + min(lane + 64 * u, p.r - 1)];
+        }
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+            float z = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                if (lane + 64 * u < p.r) z = __builtin_fmaf(w2v[j][u], h[lane + 64 * u], z);
+            z = wave_sum(z);
+            if (lane == 0 && c0 + j < p.c) gate[c0 + j] = se_gate_value(p, c0 + j, z);
+        }
+    }
+    __syncthreads();
+    if (p.flags & SOX_SE_FOLD) {
+        typedef vec_t<T, 8> T8;
+        const int cv = p.c / 8;  // wk == c
+        strided_foreach<8>((const T8*)p.wsrc, t, (long)p.wn * cv, blockDim.x, [&](long i, T8 v) {
+            const float* gt = gate + (int)(i % cv) * 8;
+            T8 o;
+#pragma unroll
+            for (int e = 0; e < 8; e++) o[e] = se_scaled(v[e], gt[e]);
+            ((T8*)p.wdst)[i] = o;
+        });
+    } else {
+        for (int ch = t; ch < p.c; ch += blockDim.x) ((T*)p.s)[(long)b * p.c + ch] = (T)gate[ch];
+    }
+}
+
+#define SOX_DWT_SE(TY, T, K, S)                                                                                \
+    extern "C" __global__ void __launch_bounds__(256) sox_dwt_##TY##_k##K##s##S##_se(sox_dwt_se_args p) {  \
+        __shared__ __attribute__((aligned(16))) unsigned char lds[DwtShape<T, K, S>::LDS];                  \
+        __shared__ uint32_t flag;                                                                              \
+        dwt_body<T, K, S, true, true>(p.dw, lds);                                                              \
+        const int g = blockIdx.y, b = blockIdx.z, groups = p.se.groups;                                        \
+        uint32_t* sync = p.sync + (long)b * (groups + 1);                                                      \
+        if (!arrive_last(sync + g, p.dw.tiles_x * p.dw.tiles_y, &flag)) return;                               \
+        se_fc1_group<true>(p.se, g, b, (float*)lds, (float*)lds + 256);                                        \
+        if (!arrive_last(sync + groups, groups, &flag)) return;                                                \
+        se_fc2_image<T>(p.se, b, (float*)lds);                                                                 \
+    }
+SOX_DWT_SE(f16, half_t, 3, 1)
+SOX_DWT_SE(f16, half_t, 3, 2)
+SOX_DWT_SE(f16, half_t, 5, 1)
+SOX_DWT_SE(f16, half_t, 5, 2)
+SOX_DWT_SE(bf16, bf16_t, 3, 1)
+SOX_DWT_SE(bf16, bf16_t, 3, 2)
+SOX_DWT_SE(bf16, bf16_t, 5, 1)
+SOX_DWT_SE(bf16, bf16_t, 5, 2)
+SOX_DWT_SE(f32, float, 3, 1)
+SOX_DWT_SE(f32, float, 3, 2)
+SOX_DWT_SE(f32, float, 5, 1)
+SOX_DWT_SE(f32, float, 5, 2)
 
 // ------------------------------------------------------------------------------------------
 // Per-channel broadcast y[p, c] = act(x[p, c] op v[img, c]) (ChannelBroadcast, Nhwc.Det.cs:317-351).

@@ -29,7 +29,7 @@ OP = dict(Conv=0, MaxPool=1, Elementwise=2, Relu=3, Sigmoid=4, Erf=5, Gelu=6, La
           DepthToSpace=32, SpaceToDepth=33)
 ACT = dict(none=0, relu=1, sigmoid=2, gelu=3, hardswish=4, swish=5)
 CK = dict(raw=0, f32=1, convwt=2, gemmnk=3, dww=4, convtw=5, f32t=7)
-SLOT_ARENA, SLOT_CONSTS, SLOT_DUMMY = 0, 1, 2
+SLOT_ARENA, SLOT_CONSTS, SLOT_DUMMY, SLOT_SYNC = 0, 1, 2, 3
 PIX = dict(Bgr24=0, Rgb24=1, Bgra32=2, Rgba32=3)  # PixelFormat (Imaging/ImageTensor.cs:8-20)
 RUN_STAGING, RUN_DISPATCHES = 1, 2
 
@@ -217,6 +217,7 @@ BACKEND_API = {
     "sox_graph_value_place": (c_int32, [c_void_p, c_int32, ctypes.POINTER(c_uint64), ctypes.POINTER(c_uint64)]),
     "sox_graph_arena_bytes": (c_uint64, [c_void_p]),
     "sox_graph_const_bytes": (c_uint64, [c_void_p]),
+    "sox_graph_sync_bytes": (c_uint64, [c_void_p]),
     "sox_last_error": (ctypes.c_char_p, []),
     "sox_session_create": (c_int32, [c_void_p, ctypes.POINTER(c_void_p)]),
     "sox_session_destroy": (None, [c_void_p]),

@@ -46,13 +46,17 @@ def offline():
 
 
 def _check_binds(g):
-    arena, consts = g.arena_bytes, g.const_bytes
+    arena, consts, sync = g.arena_bytes, g.const_bytes, g.sync_bytes
     for i in range(len(g.dispatches)):
         for slot, off, size in g.binds(i):
             if slot == N.SLOT_ARENA:
                 assert off + size <= arena, (i, g.kernels[i], off, size, arena)
             elif slot == N.SLOT_CONSTS:
                 assert off + size <= consts, (i, g.kernels[i], off, size, consts)
+            elif slot == N.SLOT_SYNC:
+                assert off + size <= sync, (i, g.kernels[i], off, size, sync)
+            else:
+                assert slot == N.SLOT_DUMMY, (i, g.kernels[i], slot)
 
 
 def test_sanitizer_build_is_the_one_loaded_when_asked():
@@ -75,6 +79,27 @@ def test_workload_lowers_without_device(offline, name, storage):
         kernels = g.kernels
         assert kernels and all(k.startswith("sox_") for k in kernels)
         _check_binds(g)
+    finally:
+        g.release()
+
+
+@pytest.mark.parametrize("storage", STORAGES)
+@pytest.mark.parametrize("name", ["mobilenetv3", "dbnet"])
+def test_se_in_depthwise_lowers_without_device(offline, name, storage, monkeypatch):
+    """Under SIMDONNX_HIP_SE_IN_DW every SE gate of the convnets runs in its depthwise conv's launch:
+    nine depthwise_se dispatches, no gap_part / se_gate, each with its own counters in the session's
+    counter block (33 dispatches for MobileNetV3-small, 44 for the fp16 / bf16 detector)."""
+    monkeypatch.setenv("SIMDONNX_HIP_SE_IN_DW", "1")
+    g = offline.graph(_workload(name), storage)
+    try:
+        labels = [d[0] for d in g.dispatches]
+        assert labels.count("depthwise_se") == 9 and "se_gate" not in labels and "gap_part" not in labels, labels
+        if storage != "f32":
+            assert len(labels) == {"mobilenetv3": 33, "dbnet": 44}[name], labels
+        _check_binds(g)
+        syncs = [(off, size) for i in range(len(labels)) for slot, off, size in g.binds(i) if slot == N.SLOT_SYNC]
+        assert len(syncs) == 9 and len({off for off, _ in syncs}) == 9
+        assert sum(size for _, size in syncs) <= g.sync_bytes
     finally:
         g.release()
 
