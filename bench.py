@@ -19,6 +19,9 @@ Also reported on the same line:
   conv3x3       the fp32 Conv3x3 + bias + ReLU 1x64x64x64 kernel (us, TFLOP/s)
   ops           the kernels of the rest of the ExecOp surface (resize, pad, transpose, slice, unary,
                 depth-space, pools, MatMul) at detector / recognizer sizes, GB/s vs the HBM peak
+  hbm_kernels   the convnets' bandwidth-bound kernels (depthwise 5x5 s1 / 3x3 s2, the SE passes, nearest,
+                elementwise) past the L2: GB/s from algorithmic bytes and from the committed
+                rocprofv3 FETCH_SIZE / WRITE_SIZE counts (profiles/traffic_hbm_kernels.json)
 """
 from __future__ import annotations
 
@@ -246,7 +249,7 @@ def bench_conv_large(steps: int, storage="f16"):
                 name="conv")
     hip = HipBackend.default()
     g = hip.graph(pb.build(y), storage)
-    kern = [d[0] for d in g.dispatches]
+    kern = g.kernels  # the code object functions (the ring tiling), not the op labels
     with HipInferenceSession(g) as s:
         s.set_input(synth.normal(64, 3, (n, h, w, c), 1.0))
         s.run()
@@ -562,6 +565,96 @@ def bench_ops(steps: int):
     return out
 
 
+def _hbm_cases():
+    """The convnets' bandwidth-bound kernels at sizes past the L2 (fp16 storage): (label, plan, inputs,
+    {kernel: algorithmic bytes per launch}). Bytes count each tensor read or written once."""
+    from simdonnx_amd import synth
+    from simdonnx_amd.plan import NHWC, PlanBuilder
+    cases = []
+
+    def img(seed, shape):
+        return synth.normal(79, seed, shape, 1.0)
+
+    def f16b(*shape):
+        n = 1
+        for d in shape:
+            n *= d
+        return 2 * n
+
+    pb = PlanBuilder()
+    x = pb.input((4, 240, 80, 80), NHWC, "x")
+    y = pb.conv(x, synth.uniform(79, 1, (240, 1, 5, 5), -0.3, 0.3), synth.uniform(79, 2, (240,), -0.1, 0.1), pad=2,
+                group=240, act="hardswish", name="dw")
+    cases.append(("depthwise 5x5 s1 + hardswish, 4x80x80x240", pb.build(y), [img(1, (4, 80, 80, 240))],
+                  {"sox_dwt_f16_k5s1": 2 * f16b(4, 80, 80, 240) + f16b(25, 240) + 4 * 240}))
+    pb = PlanBuilder()
+    x = pb.input((4, 64, 320, 320), NHWC, "x")
+    y = pb.conv(x, synth.uniform(79, 3, (64, 1, 3, 3), -0.3, 0.3), synth.uniform(79, 4, (64,), -0.1, 0.1), stride=2,
+                pad=1, group=64, act="relu", name="dw")
+    cases.append(("depthwise 3x3 s2 + relu, 4x320x320x64 -> 160x160", pb.build(y), [img(2, (4, 320, 320, 64))],
+                  {"sox_dwt_f16_k3s2": f16b(4, 320, 320, 64) + f16b(4, 160, 160, 64) + f16b(9, 64) + 4 * 64}))
+    # the largest MobileNetV3-small SE block: 20x20x576, r = 144, projection to 96 channels (folded)
+    c, r, wn, tiles = 576, 144, 96, 9
+    pb = PlanBuilder()
+    x = pb.input((1, c, 20, 20), NHWC, "x")
+    d = pb.conv(x, synth.uniform(79, 5, (c, 1, 5, 5), -0.3, 0.3), synth.uniform(79, 6, (c,), -0.1, 0.1), pad=2,
+                group=c, act="hardswish", name="dw")
+    gate = pb.channel_gate(d, synth.uniform(79, 7, (r, c, 1, 1), -0.1, 0.1), synth.uniform(79, 8, (r,), -0.1, 0.1),
+                           synth.uniform(79, 9, (c, r, 1, 1), -0.1, 0.1), synth.uniform(79, 10, (c,), -0.1, 0.1),
+                           act1="relu", hard=True, alpha=1.0 / 6.0, beta=0.5, name="se")
+    y = pb.conv(pb.mul(d, gate, name="scale"), synth.uniform(79, 11, (wn, c, 1, 1), -0.1, 0.1), None, name="proj")
+    groups = (c + 63) // 64
+    cases.append(("SE gate 1x20x20x576, r 144, folded into a 576 -> 96 projection", pb.build(y),
+                  [img(3, (1, 20, 20, c))],
+                  {"sox_se_fc1": 4 * (tiles * c + r * c + groups * r),
+                   "sox_se_fc2_f16": 4 * (groups * r + c * r + r + c) + 2 * f16b(wn, c)}))
+    pb = PlanBuilder()
+    y = pb.resize_nearest(pb.input((4, 96, 160, 160), NHWC, "x"), 2, name="up")
+    cases.append(("nearest x2, 4x160x160x96 -> 320x320", pb.build(y), [img(4, (4, 160, 160, 96))],
+                  {"sox_nearest_f16_v": f16b(4, 160, 160, 96) + f16b(4, 320, 320, 96)}))
+    pb = PlanBuilder()
+    y = pb.add(pb.input((4, 96, 160, 160), NHWC, "a"), pb.input((4, 96, 160, 160), NHWC, "b"), act="relu", name="add")
+    cases.append(("add + relu, 4x160x160x96", pb.build(y), [img(5, (4, 160, 160, 96)), img(6, (4, 160, 160, 96))],
+                  {"sox_ew_f16": 3 * f16b(4, 160, 160, 96)}))
+    return cases
+
+
+def bench_hbm_kernels(steps: int):
+    """Per-launch time of the convnets' bandwidth-bound kernels (HIP events around each dispatch, the
+    minimum over `steps` runs), with achieved GB/s from the algorithmic bytes and, where the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary covers the kernel, from the counted HBM bytes."""
+    from simdonnx_amd.backend import HipBackend, HipInferenceSession
+    hip = HipBackend.default()
+    path = os.path.join(ROOT, "profiles", "traffic_hbm_kernels.json")
+    counted = json.load(open(path))["kernels"] if os.path.exists(path) else {}
+    out = []
+    for label, plan, ins, alg in _hbm_cases():
+        g = hip.graph(plan, True)
+        kernels = g.kernels
+        wgs = [grid[0] * grid[1] * grid[2] for _, grid, _ in g.dispatches]
+        with HipInferenceSession(g) as s:
+            for i, x in enumerate(ins):
+                s.set_input(x, i)
+            s.run()
+            prof = s.profile(steps)
+        g.release()
+        for (name, node, ms), k, nwg in zip(prof, kernels, wgs):
+            if k not in alg:
+                continue
+            rec = dict(op=label, kernel=k, us=round(ms * 1e3, 2), algorithmic_mb=round(alg[k] / 1e6, 3),
+                       gb_s=round(alg[k] / (ms * 1e-3) / 1e9, 1))
+            rec["frac"] = round(rec["gb_s"] / PEAK_HBM_GBS, 4)
+            c = counted.get(k)
+            if c and c.get("workgroups") == nwg:  # counted on this kernel at this launch shape
+                rec["traffic_mb"] = round(c["bytes_per_launch"] / 1e6, 3)
+                rec["traffic_gb_s"] = round(c["bytes_per_launch"] / (ms * 1e-3) / 1e9, 1)
+                rec["traffic_frac"] = round(rec["traffic_gb_s"] / PEAK_HBM_GBS, 4)
+            out.append(rec)
+        if not any(k in alg for k in kernels):
+            raise RuntimeError(f"{label}: none of {sorted(alg)} in the dispatches {kernels}")
+    return out
+
+
 def cpu_info():
     """The host the CPU baseline ran on: model, logical CPUs used, physical cores, oracle ISA tier."""
     import oracle as O
@@ -669,7 +762,7 @@ def main():
     ap.add_argument("--no-replay", action="store_true",
                     help="launch network dispatches one by one instead of replaying a HIP graph (profiler runs)")
     ap.add_argument("--only", choices=["gemm", "gemm_bf16", "mfma_peak", "lds_peak", "vendor_gemm", "conv_large", "conv", "detector", "detector_fp32", "recognizer",
-                                       "recognizer_bf16", "mobilenetv3", "copy", "ops",
+                                       "recognizer_bf16", "mobilenetv3", "copy", "ops", "hbm_kernels",
                                        "recognizer_ctc", "image", "runner"],
                     help="run one workload only (profiling runs); prints its own JSON line")
     args = ap.parse_args()
@@ -685,6 +778,7 @@ def main():
               "conv_large": lambda: bench_conv_large(args.steps),
               "copy": lambda: bench_copy(args.steps),
               "ops": lambda: {"ops": bench_ops(args.steps)},
+              "hbm_kernels": lambda: {"hbm_kernels": bench_hbm_kernels(args.steps)},
               "recognizer_ctc": lambda: bench_recognizer_ctc(args.steps, not args.no_replay),
               "image": lambda: bench_image_session(args.steps),
               "runner": lambda: bench_unit_runner(args.steps)}.get(args.only) or (lambda: bench_network(args.only, args.steps, not args.no_replay))
@@ -781,6 +875,10 @@ def main():
         out["ops"] = bench_ops(200)
     except Exception as e:
         out["ops"] = {"error": repr(e)}
+    try:
+        out["hbm_kernels"] = bench_hbm_kernels(50)
+    except Exception as e:
+        out["hbm_kernels"] = {"error": repr(e)}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
         try:
