@@ -243,6 +243,23 @@ template <typename T, int K, int S> struct DwtShape {
     static constexpr int LDS = HH * RP + K * K * PB;                     // halo + weights
 };
 
+// The workgroup's (tile, channel group, image). Workgroups go to the 8 XCDs in turn, so consecutive
+// ids land on different L2s; numbered XCD-major (when the grid divides by 8), one XCD runs a run of
+// consecutive (tile, group) pairs, group fastest: the groups of a pixel (whose 128-byte slices share
+// lines when c * 2 bytes is no multiple of 128) and neighbouring tiles (whose halos overlap) read the
+// same L2.
+struct DwtCoords {
+    int tile, g, b;
+};
+__device__ __forceinline__ DwtCoords dwt_coords() {
+    const int groups = gridDim.y, tiles = gridDim.x;
+    const int total = tiles * groups * gridDim.z;
+    const int lin = blockIdx.x + tiles * (blockIdx.y + groups * blockIdx.z);
+    const int v = total % 8 == 0 ? (lin % 8) * (total / 8) + lin / 8 : lin;
+    const int rest = v / groups;
+    return DwtCoords{rest % tiles, v % groups, rest / tiles};
+}
+
 template <typename T, int K, int S, bool GAP, bool COH = false>
 __device__ __forceinline__ void dwt_body(const sox_dwt_args& p, unsigned char* lds) {
     typedef DwtShape<T, K, S> D;
@@ -251,8 +268,9 @@ __device__ __forceinline__ void dwt_body(const sox_dwt_args& p, unsigned char* l
     typedef vec_t<T, 8> T8;
     unsigned char* wl = lds + HH * RP;
     const int t = threadIdx.x, cv = t & 7, pl = t >> 3;
-    const int tile = blockIdx.x, b = blockIdx.z;
-    const int c0 = blockIdx.y * 64 + cv * 8;  // this thread's channel vector
+    const DwtCoords wc = dwt_coords();
+    const int tile = wc.tile, b = wc.b;
+    const int c0 = wc.g * 64 + cv * 8;  // this thread's channel vector
     const bool cok = c0 < p.c;                // p.c % 8 == 0
     const int ty0 = (tile / p.tiles_x) * TH, tx0 = (tile % p.tiles_x) * TW;
     const int iy0 = ty0 * S - p.pt, ix0 = tx0 * S - p.pl;
@@ -961,7 +979,8 @@ __device__ __forceinline__ void se_fc2_image(const sox_se_args& p, int b, float*
         __shared__ __attribute__((aligned(16))) unsigned char lds[DwtShape<T, K, S>::LDS];                  \
         __shared__ uint32_t flag;                                                                              \
         dwt_body<T, K, S, true, true>(p.dw, lds);                                                              \
-        const int g = blockIdx.y, b = blockIdx.z, groups = p.se.groups;                                        \
+        const DwtCoords wc = dwt_coords();                                                                     \
+        const int g = wc.g, b = wc.b, groups = p.se.groups;                                                    \
         uint32_t* sync = p.sync + (long)b * (groups + 1);                                                      \
         if (!arrive_last(sync + g, p.dw.tiles_x * p.dw.tiles_y, &flag)) return;                               \
         se_fc1_group<true>(p.se, g, b, (float*)lds, (float*)lds + 256);                                        \
