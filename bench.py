@@ -682,8 +682,10 @@ def cpu_info():
     return dict(model=model, logical_cpus_used=cpu_threads(), physical_cores=len(cores) or None, isa_tier=tier)
 
 
-def _median_ms(fn, runs):
-    fn()  # warm-up (page-in, thread pool)
+def _median_ms(fn, runs=20, warmups=3):
+    """Median wall time of `runs` calls after `warmups` untimed ones (page-in, thread pool, caches)."""
+    for _ in range(warmups):
+        fn()
     ts = []
     for _ in range(runs):
         t0 = time.perf_counter()
@@ -694,28 +696,30 @@ def _median_ms(fn, runs):
 
 def cpu_configs():
     """The oracle (the reference's CPU kernels restated) on the other benchmark configurations, all host
-    threads, median ms: config 1 at full size, configs 3 and 4 per image at full size, config 5 on a
-    batch of 8 of its 32 images (ms per image)."""
+    threads, median ms of 20 runs after 3 warm-ups: config 1 at full size, configs 3 and 4 per image at
+    full size, config 5 on its full batch of 32 images (ms per image)."""
     import oracle as O
     from oracle.interp import run_plan
     from simdonnx_amd import graphs
     O.set_threads(cpu_threads())
-    out = {}
+    out = {"method": "median of 20 runs after 3 warm-ups, all host threads"}
     plan, ins = graphs.conv3x3_bias_relu()
-    out["conv3x3_bias_relu_fp32_ms"] = _median_ms(lambda: run_plan(plan, ins), 20)
+    out["conv3x3_bias_relu_fp32_ms"] = _median_ms(lambda: run_plan(plan, ins))
     plan, ins = graphs.mobilenetv3_small()
-    out["mobilenetv3_ms_per_image"] = _median_ms(lambda: run_plan(plan, ins), 3)
+    out["mobilenetv3_ms_per_image"] = _median_ms(lambda: run_plan(plan, ins))
     plan, ins = graphs.dbnet()
-    out["detector_ms_per_image"] = _median_ms(lambda: run_plan(plan, ins), 3)
-    plan, ins = graphs.svtr(n=8)
-    out["recognizer_ms_per_image"] = round(_median_ms(lambda: run_plan(plan, ins), 1) / 8, 3)
-    out["recognizer_sample"] = "batch 8 of the 32 images of config 5 (same per-image work)"
+    out["detector_ms_per_image"] = _median_ms(lambda: run_plan(plan, ins))
+    plan, ins = graphs.svtr()
+    batch = plan.values[plan.inputs[0]].shape[0]
+    out["recognizer_ms_per_image"] = round(_median_ms(lambda: run_plan(plan, ins)) / batch, 3)
+    out["recognizer_batch"] = batch
     return out
 
 
-def cpu_baseline(budget_s: float = 12.0):
-    """The oracle Gemm + GELU on the full workload (M = 8192), all host threads, median of runs; and
-    on one thread over the first 1024 rows (the reference bench's micro mode, Program.cs:12)."""
+def cpu_baseline():
+    """The oracle Gemm + GELU on the full workload (M = 8192), all host threads; and on one thread over
+    the first 1024 rows (the reference bench's micro mode, Program.cs:12). Each: median of 20 runs
+    after 3 warm-ups."""
     import oracle as O
     from simdonnx_amd import graphs
     plan, ins = graphs.matmul_bias_gelu()
@@ -725,28 +729,19 @@ def cpu_baseline(budget_s: float = 12.0):
     b = plan.values[node.p.bias].data
     threads = cpu_threads()
     O.set_threads(threads)
-    O.gemm(a[:512], w, b, act="gelu")  # warm-up (page-in, thread pool)
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 20):
-        t0 = time.perf_counter()
-        O.gemm(a, w, b, act="gelu")
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > 3 * budget_s:
-            break
-    med = statistics.median(times)
+    med = _median_ms(lambda: O.gemm(a, w, b, act="gelu")) * 1e-3
     info = cpu_info()
     O.set_threads(1)
     rows = 1024
-    ms1 = _median_ms(lambda: O.gemm(a[:rows], w, b, act="gelu"), 3)
+    ms1 = _median_ms(lambda: O.gemm(a[:rows], w, b, act="gelu"))
     O.set_threads(threads)
     flops1 = 2 * rows * a.shape[1] * w.shape[1]
     return dict(value=graphs.matmul_flops() / med / 1e12, unit="TFLOP/s", cores=threads, kind="port",
-                sample=f"full workload M=8192 K=768 N=3072 + GELU, {len(times)} runs, median {med*1e3:.1f} ms, "
-                       f"{info['isa_tier']} tier (C++ restatement of Nhwc.Gemm512 / Epilogue512)",
+                sample=f"full workload M=8192 K=768 N=3072 + GELU, median of 20 runs after 3 warm-ups, "
+                       f"{med*1e3:.1f} ms, {info['isa_tier']} tier (C++ restatement of Nhwc.Gemm512 / Epilogue512)",
                 one_thread={"value": round(flops1 / (ms1 * 1e-3) / 1e12, 4), "unit": "TFLOP/s", "cores": 1,
-                            "sample": f"first {rows} rows (M={rows}, K=768, N=3072) + GELU, median of 3, "
-                                      f"{ms1:.1f} ms"},
+                            "sample": f"first {rows} rows (M={rows}, K=768, N=3072) + GELU, median of 20 runs "
+                                      f"after 3 warm-ups, {ms1:.1f} ms"},
                 cpu=info)
 
 

@@ -23,7 +23,9 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "build", "liboracle.so")
+# SIMDONNX_ORACLE_LIB: another build of the restatement (the mutation guard loads planted-mistake
+# copies through it)
+_LIB_PATH = os.environ.get("SIMDONNX_ORACLE_LIB") or os.path.join(_HERE, "build", "liboracle.so")
 _lib = None
 
 ACT = {"none": 0, "relu": 1, "sigmoid": 2, "gelu": 3, "hardswish": 4, "swish": 5}

@@ -5,7 +5,8 @@
   * tier invariants of the reference: AVX-512 == AVX2 (== scalar) bit for bit
     (Avx512KernelTests.cs:7-33), Winograd within 1e-4 * max|out| of direct (EngineTests.cs:184-212);
   * the shared transcendental cores against math.erf / math.exp within their published bounds;
-  * planted mistakes in a copy of the restatement fail these checks (mutation guard).
+  * planted mistakes in a copy of the restatement fail these checks (the mutation guard,
+    tests/test_oracle_mutation.py: seven mutants, each caught; the unmutated copy passes).
 """
 import math
 import os
