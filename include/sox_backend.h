@@ -282,8 +282,10 @@ int sox_ctc_argmax(sox_ctc* ctc, sox_session* session, int32_t feature_value, in
  * 1 for a non-finite logit, the reference's "Recognizer output is invalid.") are written when the
  * stream gets there. The column-range partials (column ranges x batch x rows x 12 bytes) go to the
  * GPU's static scratch (sox_scratch, SOX_SCRATCH_BYTES); a larger call returns SOX_E_INVALID.
- * Every call on one GPU shares that scratch: calls that overlap on one GPU (other streams, other
- * threads) race. */
+ * Every call on one GPU shares that scratch: calls are serialised on the host (any thread, any
+ * CtcProjection) and each call's stream waits for the previous call's kernels, so eager calls on
+ * different streams do not race. A call captured into a graph (the stream is capturing) is ordered
+ * by the stream the graph is launched on only: replays must not overlap other users of the scratch. */
 int sox_ctc_argmax_noalloc(sox_ctc* ctc, sox_session* session, int32_t feature_value, int32_t batch, int32_t rows,
                            int32_t* d_indices, float* d_probabilities, int32_t* d_status);
 

@@ -51,6 +51,9 @@ int sox_device_sync(void); /* vkDeviceWaitIdle, Vk.cs:474 */
 
 /* Memory (vkCreateBuffer/AllocateMemory/MapMemory, Vk.cs:401-413): device slabs and pinned staging. */
 int sox_malloc(void** ptr, size_t bytes);
+/* Device (sox_malloc) and pinned host (sox_host_alloc) allocations made since the process started:
+ * the check that an allocation-free entry point made none (no counterpart in the reference). */
+uint64_t sox_alloc_count(void);
 int sox_free(void* ptr);
 int sox_host_alloc(void** ptr, size_t bytes); /* pinned, mapped: the "mapped staging" of VkSession */
 int sox_host_free(void* ptr);
@@ -73,6 +76,10 @@ int sox_launch(void* fn, const uint32_t grid[3], const uint32_t block[3], uint32
 int sox_stream_create(void** stream);
 int sox_stream_destroy(void* stream);
 int sox_stream_sync(void* stream);
+/* hipStreamWaitEvent: later work on `stream` waits for the event's last record. */
+int sox_stream_wait_event(void* stream, void* ev);
+/* Whether `stream` is capturing into a graph (sox_graph_begin). */
+int sox_stream_is_capturing(void* stream, int* capturing);
 
 /* Events (vkCmdWriteTimestamp + vkGetQueryPoolResults, Vk.cs:449-453). */
 int sox_event_create(void** ev);

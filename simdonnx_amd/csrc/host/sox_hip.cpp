@@ -90,9 +90,17 @@ void sox_device_reset_lost(void) { g_lost.store(0); }
 void sox_device_mark_lost(void) { g_lost.store(1); }
 int sox_device_sync(void) { return st(hipDeviceSynchronize()); }
 
-int sox_malloc(void** ptr, size_t bytes) { return st(hipMalloc(ptr, bytes ? bytes : 256)); }
+std::atomic<uint64_t> g_allocs{0};
+int sox_malloc(void** ptr, size_t bytes) {
+    g_allocs++;
+    return st(hipMalloc(ptr, bytes ? bytes : 256));
+}
+uint64_t sox_alloc_count(void) { return g_allocs.load(); }
 int sox_free(void* ptr) { return ptr ? st(hipFree(ptr)) : SOX_OK; }
-int sox_host_alloc(void** ptr, size_t bytes) { return st(hipHostMalloc(ptr, bytes ? bytes : 64, hipHostMallocDefault)); }
+int sox_host_alloc(void** ptr, size_t bytes) {
+    g_allocs++;
+    return st(hipHostMalloc(ptr, bytes ? bytes : 64, hipHostMallocDefault));
+}
 int sox_host_free(void* ptr) { return ptr ? st(hipHostFree(ptr)) : SOX_OK; }
 
 int sox_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream) {
@@ -147,6 +155,13 @@ int sox_launch(void* fn, const uint32_t grid[3], const uint32_t block[3], uint32
 int sox_stream_create(void** stream) { return st(hipStreamCreateWithFlags((hipStream_t*)stream, hipStreamNonBlocking)); }
 int sox_stream_destroy(void* stream) { return st(hipStreamDestroy((hipStream_t)stream)); }
 int sox_stream_sync(void* stream) { return st(hipStreamSynchronize((hipStream_t)stream)); }
+int sox_stream_wait_event(void* stream, void* ev) { return st(hipStreamWaitEvent((hipStream_t)stream, (hipEvent_t)ev, 0)); }
+int sox_stream_is_capturing(void* stream, int* capturing) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const int rc = st(hipStreamIsCapturing((hipStream_t)stream, &cs));
+    *capturing = cs != hipStreamCaptureStatusNone;
+    return rc;
+}
 
 int sox_event_create(void** ev) { return st(hipEventCreate((hipEvent_t*)ev)); }
 int sox_event_destroy(void* ev) { return st(hipEventDestroy((hipEvent_t)ev)); }

@@ -153,6 +153,7 @@ THIN_API = {
     "sox_device_mark_lost": (None, []),
     "sox_device_sync": (c_int32, []),
     "sox_malloc": (c_int32, [ctypes.POINTER(c_void_p), c_size_t]),
+    "sox_alloc_count": (c_uint64, []),
     "sox_free": (c_int32, [c_void_p]),
     "sox_host_alloc": (c_int32, [ctypes.POINTER(c_void_p), c_size_t]),
     "sox_host_free": (c_int32, [c_void_p]),
@@ -167,6 +168,8 @@ THIN_API = {
     "sox_stream_create": (c_int32, [ctypes.POINTER(c_void_p)]),
     "sox_stream_destroy": (c_int32, [c_void_p]),
     "sox_stream_sync": (c_int32, [c_void_p]),
+    "sox_stream_wait_event": (c_int32, [c_void_p, c_void_p]),
+    "sox_stream_is_capturing": (c_int32, [c_void_p, ctypes.POINTER(c_int32)]),
     "sox_event_create": (c_int32, [ctypes.POINTER(c_void_p)]),
     "sox_event_destroy": (c_int32, [c_void_p]),
     "sox_event_record": (c_int32, [c_void_p, c_void_p]),

@@ -36,7 +36,7 @@ class Case:
 
 def lifetimes(plan):
     """[first writer, last reader] node index per buffer, as the lifetime packer counts them
-    (graph inputs from -1 and, with the output, to the end)."""
+    (graph inputs from -1 and, with the output, to the end; an unread value at its writer)."""
     nb = len(plan.buf_offset)
     first, last = [None] * nb, [-1] * nb
     for i in plan.inputs:
@@ -54,6 +54,9 @@ def lifetimes(plan):
     last[plan.values[plan.output].buf] = end
     for i in plan.inputs:
         last[plan.values[i].buf] = end
+    for bi in range(nb):  # a value nothing reads is still live where it is written
+        if first[bi] is not None:
+            last[bi] = max(last[bi], first[bi])
     return first, last
 
 
@@ -190,3 +193,29 @@ SHIFT = {"mlp": 64 * 192}
 def forced(case: Case):
     """The case's plan with the rewritten output planned over the rewrite's input."""
     return place_over(case.plan, case.moved, case.over, SHIFT.get(case.name, 0))
+
+
+def upsample_add_after_fused_write(seed=105, c=64, hw=16, rows=512, k=192, hidden=768):
+    """The FPN Add o = up(u) + conv1x1(xi) runs the conv in the Add's place (plan_upsample_add), so xi
+    must survive until then. Between the conv and the Add a transformer MLP (LayerNorm -> fc1 + GELU ->
+    fc2) runs as one kernel at fc1's place (plan_fused_mlp): fc2 is folded and its output f2 is written
+    by fc1's dispatch. Returns (plan, inputs, xi, f2, the Resize+Add node): the forced plan puts f2 over
+    xi, which the unfused order allows (xi is dead after the conv there) and the fused one must undo by
+    moving f2."""
+    pb = PlanBuilder()
+    x = pb.input((1, c, hw, hw), NHWC, "x")
+    u = pb.input((1, c, hw // 2, hw // 2), NHWC, "u")
+    t = pb.input((rows, k), None, "t")
+    xi = pb.unary("Relu", x, name="xi")
+    a = pb.conv(xi, synth.normal(seed, 1, (c, c, 1, 1), 0.1), synth.uniform(seed, 2, (c,), -0.1, 0.1), name="lat")
+    h = pb.layer_norm(t, 1.0 + synth.uniform(seed, 3, (k,), -0.1, 0.1), synth.uniform(seed, 4, (k,), -0.1, 0.1), 1e-6,
+                      name="ln")
+    f1 = pb.gemm(h, synth.normal(seed, 5, (k, hidden), 0.05), synth.uniform(seed, 6, (hidden,), -0.1, 0.1),
+                 act="gelu", name="fc1")
+    f2 = pb.gemm(f1, synth.normal(seed, 7, (hidden, k), 0.05), synth.uniform(seed, 8, (k,), -0.1, 0.1), name="fc2")
+    o = pb.resize_nearest(u, 2, add=a, name="up")
+    plan = pb.build(o)
+    ins = [synth.normal(seed, 9, (1, hw, hw, c), 1.0), synth.normal(seed, 10, (1, hw // 2, hw // 2, c), 1.0),
+           synth.normal(seed, 11, (rows, k), 1.0)]
+    up = next(i for i, n in enumerate(plan.nodes) if o in n.outs)
+    return plan, ins, xi, f2, up

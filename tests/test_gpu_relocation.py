@@ -69,3 +69,23 @@ def test_relocated_output_read_through_view(hip, case, storage, monkeypatch):
         assert got.tobytes() == unfused.tobytes()
     assert err_unfused <= UNFUSED_TOL[storage]
     assert err_oracle < ORACLE_TOL[storage]
+
+
+@pytest.mark.parametrize("storage", ["f16", "bf16"])
+def test_upsample_add_input_survives_fused_mlp(hip, storage, monkeypatch):
+    """The lateral conv of an FPN Add runs at the Add's place; a fused transformer MLP in between writes
+    fc2's output from fc1's dispatch. With that output planned over the conv's input (forced), the
+    result equals the packer's own plan bit for bit, the unfused Add (SIMDONNX_HIP_NO_UPADD) within the
+    rounding the fusion changes, and the oracle within the 16-bit contract."""
+    plan, ins, xi, f2, up = RC.upsample_add_after_fused_write()
+    forced = RC.place_over(plan, f2, xi)
+    print(f"[gpu] upsample add after fused MLP {storage}", flush=True)
+    got = _run(hip, forced, ins, storage)
+    natural = _run(hip, plan, ins, storage)
+    assert got.tobytes() == natural.tobytes(), f"max diff {np.abs(got - natural).max()}"
+    monkeypatch.setenv("SIMDONNX_HIP_NO_UPADD", "1")
+    unfused = _run(hip, forced, ins, storage)
+    want = run_plan(plan, ins, f16_storage={"f16": True, "bf16": "bf16"}[storage])
+    print(f"[gpu] vs unfused {max_rel(got, unfused):.2e}, vs oracle {max_rel(got, want):.2e}", flush=True)
+    assert max_rel(got, unfused) <= UNFUSED_TOL[storage]
+    assert max_rel(got, want) < ORACLE_TOL[storage]

@@ -170,3 +170,25 @@ def test_host_lowering_under_sanitizers():
     assert r.returncode == 0, out[-6000:]
     for marker in ("AddressSanitizer", "runtime error:", "LeakSanitizer"):
         assert marker not in out, out[-6000:]
+
+
+@pytest.mark.parametrize("storage", ["f16", "bf16"])
+def test_upsample_add_input_survives_fused_writes(offline, storage):
+    """plan_upsample_add runs the lateral conv at the Add's place, so its input must survive what the
+    dispatches in between write, including outputs written by a fused dispatch for a folded node (the
+    transformer MLP writes fc2's output from fc1's place): an fc2 output planned over the conv's input
+    moves to a buffer of its own (tests/relocation_cases.py: upsample_add_after_fused_write)."""
+    plan, ins, xi, f2, up = RC.upsample_add_after_fused_write()
+    p = RC.place_over(plan, f2, xi)
+    assert RC.overlaps(p, f2, xi) and not RC.conflicts(p)
+    g = offline.graph(p, storage)
+    try:
+        labels = [d[0] for d in g.dispatches]
+        assert "mlp" in labels and "nearest" not in labels and labels[-1] == "conv", labels
+        _check_binds(g)
+        (xo, xb), (fo, fb) = g.value_place(xi), g.value_place(f2)
+        assert fo + fb <= xo or xo + xb <= fo, "the fused MLP writes over the lateral conv's input"
+        conv = len(labels) - 1
+        assert (N.SLOT_ARENA, xo) in [(s, o) for s, o, _ in g.binds(conv)]
+    finally:
+        g.release()

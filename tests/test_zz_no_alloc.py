@@ -2,7 +2,9 @@
 one (sox_ctc_argmax) through the C ABI: two calls in a row, the second on a smaller input, give the
 same indices and probabilities bit for bit (same kernels, same column ranges; the partials live in the
 GPU's static scratch instead of a per-object workspace), the status word is cleared by every call,
-and a call whose partials exceed the scratch is refused with an error."""
+and a call whose partials exceed the scratch is refused with an error. The calls make no device or
+pinned allocation (sox_alloc_count unchanged), and a call captured into a HIP graph replays to the
+same bits, three times, with eager work between the replays."""
 import ctypes
 
 import numpy as np
@@ -56,7 +58,10 @@ class DeviceOut:
 
 
 def noalloc(ctc, s, xv, batch, rows, out):
-    return N.backend().sox_ctc_argmax_noalloc(ctc.h, s.h, xv, batch, rows, out.ptrs[0], out.ptrs[1], out.ptrs[2])
+    before = N.thin().sox_alloc_count()
+    rc = N.backend().sox_ctc_argmax_noalloc(ctc.h, s.h, xv, batch, rows, out.ptrs[0], out.ptrs[1], out.ptrs[2])
+    assert N.thin().sox_alloc_count() == before, "the allocation-free entry point allocated"
+    return rc
 
 
 def test_ctc_noalloc_matches_allocating_entry(hip):
@@ -112,3 +117,42 @@ def test_ctc_noalloc_status_and_limit(hip):
         assert b"scratch" in N.backend().sox_last_error()
     outb.free()
     wide.close()
+
+
+def test_ctc_noalloc_under_graph_capture(hip):
+    """The entry point called while the session's stream captures a HIP graph: the graph replays the
+    two passes into the caller's arrays. Three replays, each after the outputs were overwritten and an
+    eager (allocating) call ran, give the eager result bit for bit."""
+    inner, columns, batch, rows = 192, 6625, 8, 80
+    w = f16(synth.normal(53, 2, (inner, columns), 0.1))
+    b = synth.uniform(53, 3, (columns,), -0.5, 0.5)
+    ctc = HipCtcProjection(hip, w, b, inner, columns)
+    x = f16(synth.normal(53, 1, (batch * rows, inner), 1.0))
+    s, xv = features_session(hip, x)
+    out = DeviceOut(batch * rows)
+    T = N.thin()
+    with s:
+        stream = N.backend().sox_session_stream(s.h)
+        want_i, want_p = ctc.argmax(s, xv, batch, rows)
+        print("[gpu] no-alloc ctc under capture", flush=True)
+        N.check(T.sox_graph_begin(stream), "capture")
+        rc = noalloc(ctc, s, xv, batch, rows, out)
+        ex = N.c_void_p()
+        N.check(T.sox_graph_end(stream, ctypes.byref(ex)), "capture end")
+        N.check(rc, "sox_ctc_argmax_noalloc under capture")
+        junk = np.full(batch * rows, -7, np.int32)
+        try:
+            for rep in range(3):
+                for p in out.ptrs[:2]:
+                    N.check(T.sox_memcpy_h2d(p, junk.ctypes.data, junk.nbytes, stream), "overwrite")
+                N.check(T.sox_memcpy_h2d(out.ptrs[2], junk.ctypes.data, 4, stream), "overwrite")
+                ei, ep = ctc.argmax(s, xv, batch, rows)  # eager work between the replays
+                assert np.array_equal(ei, want_i) and np.array_equal(ep, want_p)
+                N.check(T.sox_graph_launch(ex, stream), "replay")
+                idx, prob, status = out.read(stream)
+                assert status == 0, rep
+                assert np.array_equal(idx, want_i) and np.array_equal(prob, want_p), rep
+        finally:
+            T.sox_graph_destroy(ex)
+    out.free()
+    ctc.close()
