@@ -1101,7 +1101,11 @@ extern "C" __global__ void __launch_bounds__(256) sox_unary_f32(sox_unary_args p
 template <typename T, int CV>
 __device__ __forceinline__ void nearest_body(const sox_nearest_args& p) {
     const int cvn = p.c / CV;
-    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    // workgroups numbered XCD-major (when the grid divides by 8): the output rows that read the same
+    // input row, a few workgroups apart, then run on one XCD and find that row in its L2
+    const int G = gridDim.x;
+    const int bid = G % 8 == 0 ? (int)(blockIdx.x % 8) * (G / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+    const long idx = (long)bid * blockDim.x + threadIdx.x;
     const long total = (long)p.n * p.oh * p.ow * cvn;
     if (idx >= total) return;
     const int c0 = (int)(idx % cvn) * CV;

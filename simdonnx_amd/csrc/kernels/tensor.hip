@@ -11,7 +11,14 @@ template <typename T, int CV> struct Vt {
     typedef T V __attribute__((ext_vector_type(CV)));
 };
 
-SOX_DEV long gid() { return (long)blockIdx.x * blockDim.x + threadIdx.x; }
+// The global thread index of a 1-D grid, workgroups numbered XCD-major when the grid divides by 8:
+// consecutive workgroups go to the 8 XCDs in turn, so renumbered, each XCD runs one contiguous range
+// and the output rows that read the same input rows (resize, pooling) find them in its L2.
+SOX_DEV long xcd_block() {
+    const int G = gridDim.x;
+    return G % 8 == 0 ? (long)(blockIdx.x % 8) * (G / 8) + blockIdx.x / 8 : (long)blockIdx.x;
+}
+SOX_DEV long gid() { return xcd_block() * blockDim.x + threadIdx.x; }
 
 // ------------------------------------------------------------------------------------------
 // Bilinear resize (Kernels/Nhwc.cs:773-870): per axis f = (o + 0.5) / scale - 0.5, taps floor(f)
@@ -579,7 +586,7 @@ __device__ __forceinline__ void img2nhwc_body(const sox_img2nhwc_args& p) {
     // flat tensor pixels 2t and 2t + 1 per thread: their 6 values leave as 3 aligned 2-element words
     // (element offset 6t) instead of 6 separate stores; an odd last pixel alone
     const long total = (long)p.oh * p.ow;
-    const long p0 = 2 * ((long)blockIdx.x * blockDim.x + threadIdx.x);
+    const long p0 = 2 * gid();
     if (p0 >= total) return;
     const int ob = p.swap * 2;
     T v[6];
