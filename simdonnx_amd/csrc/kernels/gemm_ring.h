@@ -278,6 +278,7 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
     const bool has_bias = (p.flags & SOX_F_BIAS) != 0 && !(CONV && (p.flags & SOX_F_CONVT)) && !LN;
     const int cblocks = CONV ? (p.ic + BK - 1) / BK : 1;  // channel blocks per tap
     const int nk = CONV ? p.kh * p.kw * cblocks : K / BK;
+    const long img_elems = CONV ? (long)p.ih * p.iw * p.ic : 0;  // conv: elements of one input image
     const bool reflect = (p.flags & SOX_F_REFLECT) != 0;
 
     // XCD-major workgroup number: dispatch id b runs on XCD b % 8, so XCD x gets the contiguous
@@ -298,22 +299,23 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
     // at (wave * IT + i) * CH + 16 l, i.e. row r = that offset / ROWB, slot (offset % ROWB) / 16, which
     // holds global chunk slot ^ swz(r). Rows past M / N re-read the last row (never stored).
     const bool a_lane = lane * 16 < CH_A, b_lane = lane * 16 < CH_B;
-    int a_chunk[A_IT], b_chunk[B_IT];  // global chunk (k / 8 within the slice) of each instruction
-    const T* a_src[A_IT];              // dense A: row base + chunk; conv: image base of the row's batch
-    int a_iy0[A_IT], a_ix0[A_IT];      // conv: the row's receptive-field origin
-    int a_off0[A_IT];                  // conv: (iy0 * iw + ix0) * ic, the origin's offset in its image
-    const T* b_src[B_IT];
-    const float* c_src;  // this lane's 4 bias floats (a duplicate A chunk when there is no bias)
-#pragma unroll
-    for (int i = 0; i < A_IT; i++) {
+    // global chunk (k / 8 within the slice) of DMA instruction i, recomputed where it is used (a few
+    // VALU per slice in conv mode; held across the K loop it would take a register per instruction)
+    auto a_chunk = [&](int i) __attribute__((always_inline)) {
         const int off = (wave * A_IT + i) * CH_A + lane * 16, r = off / ROWB;
-        a_chunk[i] = ((off % ROWB) / 16) ^ swz<CPR>(r);
-    }
-#pragma unroll
-    for (int i = 0; i < B_IT; i++) {
+        return ((off % ROWB) / 16) ^ swz<CPR>(r);
+    };
+    auto b_chunk = [&](int i) __attribute__((always_inline)) {
         const int off = (wave * B_IT + i) * CH_B + lane * 16, r = off / ROWB;
-        b_chunk[i] = ((off % ROWB) / 16) ^ swz<CPR>(r);
-    }
+        return ((off % ROWB) / 16) ^ swz<CPR>(r);
+    };
+    const T* a_src[A_IT];              // dense A: row base + chunk
+    const T* a_img[A_IT];              // conv: the base of the row's image in the batch
+    unsigned a_yx[A_IT];               // conv: the row's receptive-field origin, (iy0, ix0) + 2^15 in 16 bits each
+    int a_off0[A_IT];                  // conv: (iy0 * iw + ix0) * ic, the origin's offset in its image
+    const T* b_src[B_IT];              // dense: W row base + chunk
+    int b_o[B_IT];                     // conv: the same as an element offset from W
+    const float* c_src;  // this lane's 4 bias floats (a duplicate A chunk when there is no bias)
     auto set_sources = [&](int t) __attribute__((always_inline)) {
         int bm, bn;
         tile_origin(t, bm, bn);
@@ -326,18 +328,21 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
                 const int m = min(bm + r, M - 1);
                 const int ohw = p.oh * p.ow, b = m / ohw, rem = m - b * ohw;
                 const int oy = rem / p.ow, ox = rem - oy * p.ow;
-                a_iy0[i] = oy * p.sh - p.pt;
-                a_ix0[i] = ox * p.sw - p.pl;
-                a_off0[i] = (a_iy0[i] * p.iw + a_ix0[i]) * p.ic;
-                a_src[i] = A + (long)b * p.ih * p.iw * p.ic;
+                const int iy0 = oy * p.sh - p.pt, ix0 = ox * p.sw - p.pl;  // |.| < 2^15 (the launcher checks)
+                a_yx[i] = ((unsigned)(iy0 + 32768) << 16) | (unsigned)(ix0 + 32768);
+                a_off0[i] = (iy0 * p.iw + ix0) * p.ic;
+                a_img[i] = A + (long)b * img_elems;
             } else {
-                a_src[i] = A + (long)min(bm + r, M - 1) * p.lda + a_chunk[i] * 8;
+                a_src[i] = A + (long)min(bm + r, M - 1) * p.lda + a_chunk(i) * 8;
             }
         }
 #pragma unroll
         for (int i = 0; i < B_IT; i++) {
             const int r = ((wave * B_IT + i) * CH_B + lane * 16) / ROWB;
-            b_src[i] = W + (long)min(bn + r, N - 1) * p.kpad + b_chunk[i] * 8;
+            if constexpr (CONV)
+                b_o[i] = min(bn + r, N - 1) * p.kpad + b_chunk(i) * 8;  // W < 2^31 elements (the launcher checks)
+            else
+                b_src[i] = W + (long)min(bn + r, N - 1) * p.kpad + b_chunk(i) * 8;
         }
     };
     // ring slice gs = (index in this workgroup's tile list) * nk + k-slice. Slices past the end are
@@ -360,8 +365,8 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
             const int tap_off = (ky * p.iw + kx) * p.ic;
 #pragma unroll
             for (int i = 0; i < A_IT; i++) {
-                const int ch = c0 + a_chunk[i] * 8;
-                const int iy = a_iy0[i] + ky, ix = a_ix0[i] + kx;
+                const int ch = c0 + a_chunk(i) * 8;
+                const int iy = (int)(a_yx[i] >> 16) - 32768 + ky, ix = (int)(a_yx[i] & 0xffffu) - 32768 + kx;
                 bool ok = (unsigned)iy < (unsigned)p.ih && (unsigned)ix < (unsigned)p.iw;
                 int off = a_off0[i] + tap_off + ch;
                 if (reflect) {  // uniform; folds once: the launcher only routes pads < the image size here
@@ -371,12 +376,12 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
                     ok = true;
                 }
                 ok = ok && ch < p.ic;
-                q.a[i] = ok ? a_src[i] + off : Z;  // one image < 2^31 elements
+                q.a[i] = ok ? a_img[i] + off : Z;  // one image < 2^31 elements
             }
 #pragma unroll
             for (int i = 0; i < B_IT; i++) {
-                const int ch = c0 + b_chunk[i] * 8;
-                q.b[i] = ch < p.ic ? b_src[i] + tap * p.ic + c0 : Z;  // b_src includes the chunk
+                const int ch = c0 + b_chunk(i) * 8;
+                q.b[i] = ch < p.ic ? W + b_o[i] + tap * p.ic + c0 : Z;  // b_o includes the chunk
             }
         } else {
             const int k0 = kt * BK;

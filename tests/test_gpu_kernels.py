@@ -833,7 +833,8 @@ def test_gemm_pp_matches_ring_bitwise(hip, m, n, act, bias, storage, monkeypatch
     assert max_rel(got, want) < (2e-3 if storage == "f16" else 8e-3)
 
 
-@pytest.mark.parametrize("kernel", ["", "sox_conv_f16_256x128_w8k64s2"], ids=["default", "w8-256x128"])
+@pytest.mark.parametrize("kernel", ["", "sox_conv_f16_256x128_w8k64s2", "sox_conv_f16_256x256_w8k64s2"],
+                         ids=["default", "w8-256x128", "w8-256x256"])
 @pytest.mark.parametrize("storage", ["f16", "bf16"])
 def test_conv_large_channels(hip, storage, kernel, monkeypatch):
     """The large implicit-GEMM conv the bench times (3x3 s1 p1 + bias + ReLU, 256 -> 256 channels on
@@ -852,3 +853,26 @@ def test_conv_large_channels(hip, storage, kernel, monkeypatch):
     got = run(hip, plan, ins, storage)
     want = O.conv(x, wt, b, stride=(1, 1), pads=(1, 1, 1, 1), act="relu")
     assert max_rel(got, want) < (TOL[True] if storage == "f16" else 4e-3)
+
+
+@pytest.mark.parametrize("storage", ["f16", "bf16"])
+@pytest.mark.parametrize("shape", [(1, 48, 40), (2, 33, 31)], ids=["48x40", "2x33x31-ragged"])
+def test_conv_256x256_tile_matches_256x128(hip, storage, shape, monkeypatch):
+    """The 256 x 256 conv tile (8 waves of 128 x 64, stores from registers) and the 256 x 128 one (LDS-
+    staged stores) run the same k-steps in the same order from the same bias: the outputs are equal bit
+    for bit, on whole and ragged row tiles."""
+    from oracle.interp import _bf16
+    n, h, w = shape
+    cv = f16 if storage == "f16" else _bf16
+    x = cv(synth.normal(65, 3, (n, h, w, 256), 1.0))
+    wt = cv(synth.he_normal(65, 1, (256, 256, 3, 3)))
+    b = synth.uniform(65, 2, (256,), -0.1, 0.1)
+    plan, ins = conv_plan(x, wt, b, None, (1, 1), (1, 1, 1, 1), "relu", 0, 0.0)
+    outs = []
+    for k in ("sox_conv_f16_256x256_w8k64s2", "sox_conv_f16_256x128_w8k64s2"):
+        monkeypatch.setenv("SIMDONNX_HIP_CONV", k)
+        g = hip.graph(plan, storage)
+        assert g.kernels == [k.replace("_f16_", f"_{storage}_")], g.kernels
+        g.release()
+        outs.append(run(hip, plan, ins, storage))
+    assert outs[0].tobytes() == outs[1].tobytes(), f"max diff {np.abs(outs[0] - outs[1]).max()}"
