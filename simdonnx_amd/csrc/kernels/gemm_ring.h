@@ -230,7 +230,7 @@ constexpr int dma_chunk(int share) {
 // when BK does not divide ic) and zero-padding taps are fetched from p.zeros; ic % 8 == 0. Rows past
 // M re-read row M - 1 (never stored).
 template <typename T, int BM, int BN, int BK, int WM, int WN, int STAGES, int NW, int GM, bool CONV = false,
-          bool EPI_LDS = false, bool LN = false>
+          bool EPI_LDS = false, bool LN = false, int CPARTS = 0>
 __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
     typedef vec_t<T, 8> T8;
     typedef vec_t<T, 2> T2;
@@ -355,34 +355,52 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
         const T* b[B_IT];
         const float* c;
     };
+    // conv: the slice's tap (ky, kx), its offset in an image and the first channel c0 (uniform). The
+    // K loop walks channel blocks outermost and taps innermost: a tile's kh * kw consecutive slices
+    // read shifted windows of the same BK channels of the same input rows, which stay in L2 between
+    // them (taps outermost, every tile re-read all ic channels of its rows once per tap, and the rows
+    // of an XCD's tiles in flight outgrew its L2)
+    struct Tap {
+        int tap, c0, ky, kx, off;
+    };
+    auto slice_tap = [&](int gs) __attribute__((always_inline)) {
+        Tap t;
+        const int kt = gs % nk, taps = p.kh * p.kw, cb = kt / taps;
+        t.tap = kt - cb * taps;
+        t.c0 = cb * BK;
+        t.ky = t.tap / p.kw;
+        t.kx = t.tap - t.ky * p.kw;
+        t.off = (t.ky * p.iw + t.kx) * p.ic;
+        return t;
+    };
+    // conv DMA source of A instruction i / B instruction i for a slice
+    auto conv_a = [&](int i, const Tap& t) __attribute__((always_inline)) {
+        const int ch = t.c0 + a_chunk(i) * 8;
+        const int iy = (int)(a_yx[i] >> 16) - 32768 + t.ky, ix = (int)(a_yx[i] & 0xffffu) - 32768 + t.kx;
+        bool ok = (unsigned)iy < (unsigned)p.ih && (unsigned)ix < (unsigned)p.iw;
+        int off = a_off0[i] + t.off + ch;
+        if (reflect) {  // uniform; folds once: the launcher only routes pads < the image size here
+            const int ry = iy < 0 ? -iy : iy >= p.ih ? 2 * p.ih - 2 - iy : iy;
+            const int rx = ix < 0 ? -ix : ix >= p.iw ? 2 * p.iw - 2 - ix : ix;
+            off = (ry * p.iw + rx) * p.ic + ch;
+            ok = true;
+        }
+        ok = ok && ch < p.ic;
+        return ok ? a_img[i] + off : Z;  // one image < 2^31 elements
+    };
+    auto conv_b = [&](int i, const Tap& t) __attribute__((always_inline)) {
+        const int ch = t.c0 + b_chunk(i) * 8;
+        return ch < p.ic ? W + b_o[i] + t.tap * p.ic + t.c0 : Z;  // b_o includes the chunk
+    };
     auto prep = [&](int gs, Src& q) __attribute__((always_inline)) {
         const int kt = gs % nk;
         if (kt == 0 && gs < total) set_sources(vid + (gs / nk) * G);
         if constexpr (CONV) {
-            // uniform: the slice's tap (ky, kx) and first channel c0
-            const int tap = kt / cblocks, c0 = (kt - tap * cblocks) * BK;
-            const int ky = tap / p.kw, kx = tap - ky * p.kw;
-            const int tap_off = (ky * p.iw + kx) * p.ic;
+            const Tap t = slice_tap(gs);
 #pragma unroll
-            for (int i = 0; i < A_IT; i++) {
-                const int ch = c0 + a_chunk(i) * 8;
-                const int iy = (int)(a_yx[i] >> 16) - 32768 + ky, ix = (int)(a_yx[i] & 0xffffu) - 32768 + kx;
-                bool ok = (unsigned)iy < (unsigned)p.ih && (unsigned)ix < (unsigned)p.iw;
-                int off = a_off0[i] + tap_off + ch;
-                if (reflect) {  // uniform; folds once: the launcher only routes pads < the image size here
-                    const int ry = iy < 0 ? -iy : iy >= p.ih ? 2 * p.ih - 2 - iy : iy;
-                    const int rx = ix < 0 ? -ix : ix >= p.iw ? 2 * p.iw - 2 - ix : ix;
-                    off = (ry * p.iw + rx) * p.ic + ch;
-                    ok = true;
-                }
-                ok = ok && ch < p.ic;
-                q.a[i] = ok ? a_img[i] + off : Z;  // one image < 2^31 elements
-            }
+            for (int i = 0; i < A_IT; i++) q.a[i] = conv_a(i, t);
 #pragma unroll
-            for (int i = 0; i < B_IT; i++) {
-                const int ch = c0 + b_chunk(i) * 8;
-                q.b[i] = ch < p.ic ? W + b_o[i] + tap * p.ic + c0 : Z;  // b_o includes the chunk
-            }
+            for (int i = 0; i < B_IT; i++) q.b[i] = conv_b(i, t);
         } else {
             const int k0 = kt * BK;
 #pragma unroll
@@ -418,8 +436,8 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
     // slice's vmcnt wait (one part per k-step over all four k-steps left the last part too little time).
     // Every part of slice g + STAGES - 1 is out before the vmcnt wait of slice g, so the waits count the
     // same loads as before.
-    constexpr bool SPREAD = !CONV && KS >= 2;
-    constexpr int NPARTS = 2;
+    constexpr bool SPREAD = (!CONV || CPARTS > 1) && KS >= 2;
+    constexpr int NPARTS = !SPREAD ? 1 : CONV ? (CPARTS < KS ? CPARTS : KS) : 2;
     constexpr int PER = (LOADS + NPARTS - 1) / NPARTS;  // DMA instructions per part
     auto fire_part = [&](int gs, auto pp) __attribute__((always_inline)) {
         constexpr int p0 = decltype(pp)::value * PER;
@@ -427,15 +445,18 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
             if (gs % nk == 0 && gs < total) set_sources(vid + (gs / nk) * G);
         }
         const int k0 = (gs % nk) * BK;
+        Tap t{};
+        if constexpr (CONV) t = slice_tap(gs);  // recomputed per part: scalar work, no registers held
         unsigned char* st = smem + (gs % STAGES) * STAGE_BYTES;
         static_for<p0, (p0 + PER < LOADS ? p0 + PER : LOADS)>([&](auto xx) {
             constexpr int x = decltype(xx)::value;
             if constexpr (x < A_IT) {
-                if (a_lane) __builtin_amdgcn_global_load_lds(a_src[x] + k0, LDS_PTR(st + (wave * A_IT + x) * CH_A), 16, 0, 0);
+                const T* src = CONV ? conv_a(x, t) : a_src[x] + k0;
+                if (a_lane) __builtin_amdgcn_global_load_lds(src, LDS_PTR(st + (wave * A_IT + x) * CH_A), 16, 0, 0);
             } else if constexpr (x < A_IT + B_IT) {
+                const T* src = CONV ? conv_b(x - A_IT, t) : b_src[x - A_IT] + k0;
                 if (b_lane)
-                    __builtin_amdgcn_global_load_lds(b_src[x - A_IT] + k0, LDS_PTR(st + A_BYTES + (wave * B_IT + x - A_IT) * CH_B),
-                                                     16, 0, 0);
+                    __builtin_amdgcn_global_load_lds(src, LDS_PTR(st + A_BYTES + (wave * B_IT + x - A_IT) * CH_B), 16, 0, 0);
             } else {
                 if (lane < BIAS_LANES)
                     __builtin_amdgcn_global_load_lds(c_src, LDS_PTR(st + A_BYTES + B_BYTES + wave * BIAS_LANES * 16), 16, 0, 0);
@@ -648,4 +669,9 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
 #define SOX_CONV_E(NAME, T, BM, BN, BK, WM, WN, ST, NW, OCC, GM)                                    \
     extern "C" __global__ void __launch_bounds__(64 * NW, OCC) NAME(sox_igemm_args p) {           \
         gemm_body<T, BM, BN, BK, WM, WN, ST, NW, GM, true, true>(p);                              \
+    }
+// conv mode with the slice's DMA issued in PARTS parts (the dense Gemm issues it in two)
+#define SOX_CONV_P(NAME, T, BM, BN, BK, WM, WN, ST, NW, OCC, GM, PARTS)                             \
+    extern "C" __global__ void __launch_bounds__(64 * NW, OCC) NAME(sox_igemm_args p) {           \
+        gemm_body<T, BM, BN, BK, WM, WN, ST, NW, GM, true, false, false, PARTS>(p);               \
     }
