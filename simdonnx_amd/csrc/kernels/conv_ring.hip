@@ -16,5 +16,6 @@ SOX_CONV(sox_conv_f16_128x64_k64s5, half_t, 128, 64, 64, 64, 32, 5, 4, 1, 4)
 SOX_CONV_E(sox_conv_f16_256x128_w8k64s2, half_t, 256, 128, 64, 64, 64, 2, 8, 1, 4)
 // 256 output channels: the whole N in one tile (fewer DMA and LDS bytes per MFMA than 256 x 128); its
 // LDS-staged epilogue would not fit beside the two 64 KiB stages, so it stores from registers. Each
-// slice's DMA goes out in two parts (after the barrier and after the first k-step's MFMAs)
-SOX_CONV_P(sox_conv_f16_256x256_w8k64s2, half_t, 256, 256, 64, 128, 64, 2, 8, 1, 4, 2)
+// slice's DMA goes out in two parts (after the barrier and after the first k-step's MFMAs); its DMA
+// rows hold 32-bit input offsets (the launcher routes inputs of fewer than 2^31 elements only)
+SOX_CONV_L(sox_conv_f16_256x256_w8k64s2, half_t, 256, 256, 64, 128, 64, 2, 8, 1, 4, 2)

@@ -13,4 +13,4 @@ SOX_CONV(sox_conv_bf16_64x64_k64s8, bf16_t, 64, 64, 64, 32, 32, 8, 4, 1, 4)
 SOX_CONV(sox_conv_bf16_128x64_k64s5, bf16_t, 128, 64, 64, 64, 32, 5, 4, 1, 4)
 // large convs (many output pixels, K >= 1024): the headline Gemm's 8-wave tilings, LDS-staged epilogue
 SOX_CONV_E(sox_conv_bf16_256x128_w8k64s2, bf16_t, 256, 128, 64, 64, 64, 2, 8, 1, 4)
-SOX_CONV_P(sox_conv_bf16_256x256_w8k64s2, bf16_t, 256, 256, 64, 128, 64, 2, 8, 1, 4, 2)
+SOX_CONV_L(sox_conv_bf16_256x256_w8k64s2, bf16_t, 256, 256, 64, 128, 64, 2, 8, 1, 4, 2)

@@ -856,18 +856,21 @@ def test_conv_large_channels(hip, storage, kernel, monkeypatch):
 
 
 @pytest.mark.parametrize("storage", ["f16", "bf16"])
-@pytest.mark.parametrize("shape", [(1, 48, 40), (2, 33, 31)], ids=["48x40", "2x33x31-ragged"])
-def test_conv_256x256_tile_matches_256x128(hip, storage, shape, monkeypatch):
-    """The 256 x 256 conv tile (8 waves of 128 x 64, stores from registers) and the 256 x 128 one (LDS-
-    staged stores) run the same k-steps in the same order from the same bias: the outputs are equal bit
-    for bit, on whole and ragged row tiles."""
+@pytest.mark.parametrize("shape,mode", [((1, 48, 40), 0), ((2, 33, 31), 0), ((2, 33, 31), 1)],
+                         ids=["48x40", "2x33x31-ragged", "2x33x31-reflect"])
+def test_conv_256x256_tile_matches_256x128(hip, storage, shape, mode, monkeypatch):
+    """The 256 x 256 conv tile (8 waves of 128 x 64, 32-bit input offsets, 16-byte stores from
+    registers) and the 256 x 128 one (image-base pointers, LDS-staged stores) run the same k-steps in
+    the same order from the same bias: the outputs are equal bit for bit, on whole and ragged row
+    tiles, with zero and reflect padding (the second image's reflected rows find their image's base
+    from the 32-bit offset); the reflect case also against the oracle."""
     from oracle.interp import _bf16
     n, h, w = shape
     cv = f16 if storage == "f16" else _bf16
     x = cv(synth.normal(65, 3, (n, h, w, 256), 1.0))
     wt = cv(synth.he_normal(65, 1, (256, 256, 3, 3)))
     b = synth.uniform(65, 2, (256,), -0.1, 0.1)
-    plan, ins = conv_plan(x, wt, b, None, (1, 1), (1, 1, 1, 1), "relu", 0, 0.0)
+    plan, ins = conv_plan(x, wt, b, None, (1, 1), (1, 1, 1, 1), "relu", mode, 0.0)
     outs = []
     for k in ("sox_conv_f16_256x256_w8k64s2", "sox_conv_f16_256x128_w8k64s2"):
         monkeypatch.setenv("SIMDONNX_HIP_CONV", k)
@@ -876,3 +879,6 @@ def test_conv_256x256_tile_matches_256x128(hip, storage, shape, monkeypatch):
         g.release()
         outs.append(run(hip, plan, ins, storage))
     assert outs[0].tobytes() == outs[1].tobytes(), f"max diff {np.abs(outs[0] - outs[1]).max()}"
+    if mode:
+        want = O.conv(x, wt, b, stride=(1, 1), pads=(1, 1, 1, 1), act="relu", pad_mode=mode)
+        assert max_rel(outs[0], want) < (TOL[True] if storage == "f16" else 4e-3)
