@@ -263,7 +263,9 @@ def bench_conv_large(steps: int, storage="f16"):
     with HipInferenceSession(g) as s:
         s.set_input(synth.normal(64, 3, (n, h, w, c), 1.0))
         s.run()
-        s.time(100)
+        warm_ms = s.time(100)
+        while warm_ms < MIN_WARM_MS:  # past the clock transient of a cold start (as the headline leg)
+            warm_ms += s.time(100)
         ms = s.time(steps) / steps
     g.release()
     flops = 2 * n * h * w * c * c * 9
