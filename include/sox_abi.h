@@ -129,6 +129,26 @@ typedef struct sox_convt_args {
     int32_t flags;
 } sox_convt_args;
 
+/*
+ * Two chained stride-2 2x2 ConvTransposes run as one kernel (the DB head's probability map: ConvT
+ * ic -> oc1 + bias + act1, then ConvT oc1 -> 1 + bias + act2; the reference dispatches convt.comp
+ * for each, Backends/Vulkan/VkGraph.cs:918-926). Per input pixel the first one's 4 x oc1 outputs
+ * stay on chip (rounded to the storage type as the unfused path stores them) and the second one's
+ * 16 outputs are written:
+ * y[n][4 ih][4 iw][1]. w1 is the first ConvT as [tap * oc1 + o][kpad] (its Gemm packing), w2 the
+ * second as [tap][oc1]. ic <= 32, ic % 8 == 0; oc1 % 8 == 0, oc1 <= 32.
+ */
+typedef struct sox_convt2_args {
+    const void* x;
+    const void* w1;
+    const float* b1; /* [oc1] or null */
+    const void* w2;
+    const float* b2; /* [1] or null */
+    void* y;
+    int32_t n, ih, iw, ic, oc1, kpad;
+    int32_t act1, act2;
+} sox_convt2_args;
+
 /* Per-channel mean partials over pixel chunks (gap_part.comp): part[n][chunk][c] (fp32). */
 typedef struct sox_gap_args {
     const void* x;

@@ -882,3 +882,49 @@ def test_conv_256x256_tile_matches_256x128(hip, storage, shape, mode, monkeypatc
     if mode:
         want = O.conv(x, wt, b, stride=(1, 1), pads=(1, 1, 1, 1), act="relu", pad_mode=mode)
         assert max_rel(outs[0], want) < (TOL[True] if storage == "f16" else 4e-3)
+
+
+# (batch, ic, oc1, h, w, bn): two chained 2x2 ConvTransposes, the second to one channel (the DB head's
+# probability map); bn: an unfolded BatchNorm + ReLU between them (folded into the first), else ReLU on
+# the first. Ragged pixel counts leave partial 128-pixel blocks.
+CONVT_CHAIN = [(1, 24, 24, 60, 60, True), (2, 16, 8, 9, 13, False), (1, 32, 32, 17, 11, True), (1, 8, 16, 5, 7, False)]
+
+
+@pytest.mark.parametrize("storage", ["f16", "bf16"])
+@pytest.mark.parametrize("case", CONVT_CHAIN, ids=lambda c: "x".join(str(v) for v in c[:5]) + ("-bn" if c[5] else ""))
+def test_convt_chain_matches_unfused(hip, storage, case, monkeypatch):
+    """The fused pair (sox_convt2_*) against the two separate ConvTranspose dispatches bit for bit (the
+    first as the same matrix product from zero with its bias after, rounded to the storage type; the
+    second in sox_convt_one_*'s order), and against the fp32 oracle of the chain."""
+    from oracle.interp import _bf16
+    n, ic, oc1, h, w, bn = case
+    cv = f16 if storage == "f16" else _bf16
+    x = cv(synth.uniform(66, 1, (n, h, w, ic), -1, 1))
+    w1 = cv(synth.normal(66, 2, (ic, oc1, 2, 2), 0.3))
+    b1 = synth.uniform(66, 3, (oc1,), -0.2, 0.2)
+    w2 = cv(synth.normal(66, 4, (oc1, 1, 2, 2), 0.3))
+    b2 = synth.uniform(66, 5, (1,), -0.2, 0.2)
+    s_, t_ = synth.uniform(66, 6, (oc1, 1, 1), 0.5, 1.5), synth.uniform(66, 7, (oc1, 1, 1), -0.3, 0.3)
+    pb = PlanBuilder()
+    xv = pb.input((n, ic, h, w), NHWC, "x")
+    hv = pb.conv_transpose(xv, w1, b1, act="none" if bn else "relu", name="convt1")
+    if bn:
+        hv = pb.ew(hv, pb.const(s_, "bn_scale"), 2, name="bn_mul")
+        hv = pb.ew(hv, pb.const(t_, "bn_shift"), 0, act="relu", name="bn_add")
+    y = pb.conv_transpose(hv, w2, b2, act="sigmoid", name="convt2")
+    plan = pb.build(y)
+    g = hip.graph(plan, storage)
+    assert g.kernels == [f"sox_convt2_{storage}_n{oc1 // 8}"], g.kernels
+    g.release()
+    got = run(hip, plan, [x], storage)
+    monkeypatch.setenv("SIMDONNX_HIP_NO_CONVT_CHAIN", "1")
+    g = hip.graph(plan, storage)
+    assert len(g.kernels) == 2 and g.kernels[1] == f"sox_convt_one_{storage}", g.kernels
+    g.release()
+    unfused = run(hip, plan, [x], storage)
+    assert got.shape == (n, 4 * h, 4 * w, 1)
+    assert got.tobytes() == unfused.tobytes(), f"max diff {np.abs(got - unfused).max()}"
+    ref = O.conv_transpose(x, w1, b1)
+    ref = np.maximum(ref * s_.reshape(-1) + t_.reshape(-1), 0.0) if bn else np.maximum(ref, 0.0)
+    want = O.conv_transpose(ref, w2, b2, act="sigmoid")
+    assert max_rel(got, want) < (5e-3 if storage == "f16" else 2e-2)

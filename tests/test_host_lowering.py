@@ -95,7 +95,7 @@ def test_se_in_depthwise_lowers_without_device(offline, name, storage, monkeypat
         labels = [d[0] for d in g.dispatches]
         assert labels.count("depthwise_se") == 9 and "se_gate" not in labels and "gap_part" not in labels, labels
         if storage != "f32":
-            assert len(labels) == {"mobilenetv3": 33, "dbnet": 44}[name], labels
+            assert len(labels) == {"mobilenetv3": 33, "dbnet": 43}[name], labels
         _check_binds(g)
         syncs = [(off, size) for i in range(len(labels)) for slot, off, size in g.binds(i) if slot == N.SLOT_SYNC]
         assert len(syncs) == 9 and len({off for off, _ in syncs}) == 9
