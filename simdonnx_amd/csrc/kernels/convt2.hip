@@ -53,7 +53,7 @@ __device__ __forceinline__ void convt2_body(const sox_convt2_args& p) {
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int o = (c0 + r) % OC1;
-                h[r] = (T)sox_act(acc[4 * q + r] + (p.b1 ? p.b1[o] : 0.0f), p.act1);
+                h[r] = (T)fp32_value(sox_act(acc[4 * q + r] + (p.b1 ? p.b1[o] : 0.0f), p.act1));
             }
             *(T4*)(hrow + c0) = h;
         }
@@ -88,8 +88,8 @@ __device__ __forceinline__ void convt2_body(const sox_convt2_args& p) {
 #pragma unroll
         for (int dy2 = 0; dy2 < 2; dy2++) {
             T2 v;
-            v[0] = (T)sox_act(acc[2 * dy2], p.act2);
-            v[1] = (T)sox_act(acc[2 * dy2 + 1], p.act2);
+            v[0] = (T)fp32_value(sox_act(acc[2 * dy2], p.act2));
+            v[1] = (T)fp32_value(sox_act(acc[2 * dy2 + 1], p.act2));
             *(T2*)((T*)p.y + ((long)b * OH + Y + dy2) * OW + X0) = v;
         }
     }

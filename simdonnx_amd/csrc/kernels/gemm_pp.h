@@ -205,6 +205,7 @@ __device__ __forceinline__ void gemm_pp_body(const sox_igemm_args& p) {
             pv[e % 4] = ACT == SOX_ACT_GELU ? gelu_fast_hi(x, pa[e % 4], pl[e % 4])
                         : ACT == SOX_ACT_RELU ? __builtin_amdgcn_fmed3f(x, 0.0f, __builtin_inff()) : x;
             if constexpr (e % 4 == 3) {
+                fp32_rounded(pv);
                 const T4 hv = __builtin_convertvector(pv, T4);
                 *(T4*)(stg + l32 * g.ch * 16 + ((c ^ (l32 % g.ch)) << 4) + hl * 8) = hv;
             }

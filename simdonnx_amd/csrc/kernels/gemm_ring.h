@@ -98,7 +98,7 @@ SOX_DEV void store_tile(T* __restrict__ Y, const T* __restrict__ R, int ldy, int
                             T4 h;
                             static_for<0, 4>([&](auto ee) {
                                 constexpr int e = decltype(ee)::value;
-                                h[e] = (T)fin(acc[j][i][4 * q + e] + (ct->bias ? ct->bias[o + e] : 0.0f));
+                                h[e] = (T)fp32_value(fin(acc[j][i][4 * q + e] + (ct->bias ? ct->bias[o + e] : 0.0f)));
                             });
                             *(T4*)(Y + (base + (long)dy * ow + dx) * ct->oc + o) = h;
                         }
@@ -108,7 +108,7 @@ SOX_DEV void store_tile(T* __restrict__ Y, const T* __restrict__ R, int ldy, int
                             if (n + e < N) {
                                 const int t = (n + e) / ct->oc, o = n + e - t * ct->oc, dy = t / ct->kw, dx = t - dy * ct->kw;
                                 Y[(base + (long)dy * ow + dx) * ct->oc + o] =
-                                    (T)fin(acc[j][i][4 * q + e] + (ct->bias ? ct->bias[o] : 0.0f));
+                                    (T)fp32_value(fin(acc[j][i][4 * q + e] + (ct->bias ? ct->bias[o] : 0.0f)));
                             }
                         });
                     }
@@ -134,8 +134,8 @@ SOX_DEV void store_tile(T* __restrict__ Y, const T* __restrict__ R, int ldy, int
                 T4 h0, h1;
                 static_for<0, 4>([&](auto ee) {
                     constexpr int e = decltype(ee)::value;
-                    h0[e] = (T)fin(acc[j][i][4 * q0 + e]);
-                    h1[e] = (T)fin(acc[j][i][4 * q1 + e]);
+                    h0[e] = (T)fp32_value(fin(acc[j][i][4 * q0 + e]));
+                    h1[e] = (T)fp32_value(fin(acc[j][i][4 * q1 + e]));
                 });
                 const U2 d0 = __builtin_bit_cast(U2, h0), d1 = __builtin_bit_cast(U2, h1);
                 // lanes 0-31 keep their dword of group q0 and receive lane + 32's; lanes 32-63 receive
@@ -188,7 +188,7 @@ SOX_DEV void store_tile(T* __restrict__ Y, const T* __restrict__ R, int ldy, int
                 constexpr int e = decltype(ee)::value;
                 float v = acc[j][i][4 * q + e];
                 if (R) v += (float)rv[q][e];
-                h[e] = (T)(ACT == SOX_ACT_GELU ? gelu_fast(v) : ACT >= 0 ? sox_act(v, ACT) : act_fast(v, act));
+                h[e] = (T)fp32_value(ACT == SOX_ACT_GELU ? gelu_fast(v) : ACT >= 0 ? sox_act(v, ACT) : act_fast(v, act));
             });
             if (m < M && n < N) {
                 T* yp = Y + (long)m * ldy + n;
@@ -227,7 +227,8 @@ SOX_DEV void store_tile_lds(T* __restrict__ Y, int ldy, int M, int N, int m0, in
             float4v f;
             static_for<0, 4>([&](auto ee) { f[decltype(ee)::value] = fin(acc[j][i][4 * q + decltype(ee)::value]); });
             // a vector conversion: two v_cvt_pk_f16_f32 / v_cvt_pk_bf16_f32 (round to nearest even)
-            // instead of four conversions and the packing moves
+            // instead of four conversions and the packing moves, from the values rounded to fp32
+            fp32_rounded(f);
             const T4 h = __builtin_convertvector(f, T4);
             *(T4*)(stg + l32 * CH * 16 + ((c ^ (l32 % CH)) << 4) + hl * 8) = h;
         });

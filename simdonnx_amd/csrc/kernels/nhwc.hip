@@ -603,11 +603,11 @@ __device__ __forceinline__ void convt_one_body(const sox_convt_args& p) {
         if (p.kw == 2) {
             typedef typename VecT<T, 2>::Vec Vec2;
             Vec2 v;
-            v[0] = (T)sox_act(acc[2 * dy], act);
-            v[1] = (T)sox_act(acc[2 * dy + 1], act);
+            v[0] = (T)fp32_value(sox_act(acc[2 * dy], act));
+            v[1] = (T)fp32_value(sox_act(acc[2 * dy + 1], act));
             *(Vec2*)out = v;
         } else {
-            for (int dx = 0; dx < p.kw; dx++) out[dx] = (T)sox_act(acc[dy * p.kw + dx], act);
+            for (int dx = 0; dx < p.kw; dx++) out[dx] = (T)fp32_value(sox_act(acc[dy * p.kw + dx], act));
         }
     }
 }

@@ -118,6 +118,10 @@ SOX_DEV float gelu_fast(float x) {
 // compiler may fold the last fma or add and the conversion into one mixed-precision op
 // (v_fma_mixlo_f16) that rounds once, where the unfused kernels round to fp32 and then to 16 bits.
 SOX_DEV void fp32_rounded(float4v& v) { asm volatile("" : "+v"(v)); }
+SOX_DEV float fp32_value(float v) {  // the same for one value: (T)fp32_value(f) rounds f to fp32 first
+    asm volatile("" : "+v"(v));
+    return v;
+}
 
 // The split transformer MLP's outputs, four columns: act(b2 + part[0] + .. + part[parts - 1] (+ res)),
 // summed in part order in fp32. sox_mlp_sum_* and the fused qkv-attention's row load both finish the
