@@ -258,9 +258,10 @@ constexpr int dma_chunk(int share) {
 
 // CONV = false: A is a dense [M][lda] matrix (Gemm). CONV = true: A is the implicit im2col matrix of
 // an NHWC image, A[m][k] = x[b][oy*sh - pt + ky][ox*sw - pl + kx][c] for m = (b, oy, ox) and
-// k = (ky*kw + kx)*ic + c (tap-major, the packed weights' order). The K loop walks taps x channel
-// blocks of BK, so a slice never straddles a tap: its tap is uniform (scalar math) and a lane's source
-// is its row's offset + the tap's offset + its channel. Channels past ic (the last block of a tap
+// k = (ky*kw + kx)*ic + c (tap-major, the packed weights' order). The K loop walks channel blocks of
+// BK x taps (taps innermost; any order of the slices gives the same sum set, and this one keeps a
+// block's rows in L2 across its taps), so a slice never straddles a tap: its tap is uniform (scalar
+// math) and a lane's source is its row's offset + the tap's offset + its channel. Channels past ic (the last block of a tap
 // when BK does not divide ic) and zero-padding taps are fetched from p.zeros; ic % 8 == 0. Rows past
 // M re-read row M - 1 (never stored).
 template <typename T, int BM, int BN, int BK, int WM, int WN, int STAGES, int NW, int GM, bool CONV = false,
