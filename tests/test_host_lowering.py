@@ -192,3 +192,28 @@ def test_upsample_add_input_survives_fused_writes(offline, storage):
         assert (N.SLOT_ARENA, xo) in [(s, o) for s, o, _ in g.binds(conv)]
     finally:
         g.release()
+
+
+def _conv3x3_256(n, h, w):
+    import numpy as np
+    from simdonnx_amd.plan import NHWC, PlanBuilder
+    pb = PlanBuilder()
+    x = pb.input((n, 256, h, w), NHWC, "x")
+    y = pb.conv(x, np.zeros((256, 256, 3, 3), np.float32), np.zeros(256, np.float32), pad=1, act="relu", name="c")
+    return pb.build(y)
+
+
+def test_large_conv_tile_takes_inputs_under_2_pow_31_elements(offline, monkeypatch):
+    """The 256x256 conv tile keeps one 32-bit offset into the whole input per DMA row: a large conv takes
+    it below 2^31 input elements and the 256x128 tile (64-bit image bases) from there; forcing the
+    256x256 tile onto a larger input is refused at graph creation, not run."""
+    g = offline.graph(_conv3x3_256(2, 256, 256), "f16")
+    assert g.kernels == ["sox_conv_f16_256x256_w8k64s2"], g.kernels
+    g.release()
+    big = _conv3x3_256(1, 1024, 8448)  # 2^31 + 2^26 input elements
+    g = offline.graph(big, "f16")
+    assert g.kernels == ["sox_conv_f16_256x128_w8k64s2"], g.kernels
+    g.release()
+    monkeypatch.setenv("SIMDONNX_HIP_CONV", "sox_conv_f16_256x256_w8k64s2")
+    with pytest.raises(N.NotSupportedError):
+        offline.graph(big, "f16")
