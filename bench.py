@@ -19,6 +19,9 @@ Also reported on the same line:
   detector / detector_fp32 / recognizer / recognizer_bf16 / mobilenetv3
                 ms per image of the whole networks (HIP-graph replay), per-kernel-class roofline
   conv3x3       the fp32 Conv3x3 + bias + ReLU 1x64x64x64 kernel (us, TFLOP/s)
+  conv_large_f16 / conv_large_bf16
+                the Conv3x3 + bias + ReLU over 8x128x128, 256 -> 256 channels (154.6 GFLOP) on the LDS-DMA
+                ring in fp16 / bf16 storage, against the dense MFMA peak
   ops           the kernels of the rest of the ExecOp surface (resize, pad, transpose, slice, unary,
                 depth-space, pools, MatMul) at detector / recognizer sizes, GB/s vs the HBM peak
   hbm_kernels   the convnets' bandwidth-bound kernels (depthwise 5x5 s1 / 3x3 s2, the SE passes, nearest,
@@ -768,7 +771,7 @@ def main():
                          "may hold the GPU before the child would start)")
     ap.add_argument("--no-replay", action="store_true",
                     help="launch network dispatches one by one instead of replaying a HIP graph (profiler runs)")
-    ap.add_argument("--only", choices=["gemm", "gemm_bf16", "mfma_peak", "lds_peak", "vendor_gemm", "conv_large", "conv", "detector", "detector_fp32", "recognizer",
+    ap.add_argument("--only", choices=["gemm", "gemm_bf16", "mfma_peak", "lds_peak", "vendor_gemm", "conv_large", "conv_large_bf16", "conv", "detector", "detector_fp32", "recognizer",
                                        "recognizer_bf16", "mobilenetv3", "copy", "ops", "hbm_kernels",
                                        "recognizer_ctc", "image", "runner"],
                     help="run one workload only (profiling runs); prints its own JSON line")
@@ -783,6 +786,7 @@ def main():
               "mfma_peak": lambda: bench_mfma_peak(), "lds_peak": lambda: bench_lds_peak(),
               "vendor_gemm": lambda: bench_vendor_gemm(),
               "conv_large": lambda: bench_conv_large(args.steps),
+              "conv_large_bf16": lambda: bench_conv_large(args.steps, "bf16"),
               "copy": lambda: bench_copy(args.steps),
               "ops": lambda: {"ops": bench_ops(args.steps)},
               "hbm_kernels": lambda: {"hbm_kernels": bench_hbm_kernels(args.steps)},
@@ -863,6 +867,11 @@ def main():
         log(f"large conv: {out['conv_large_f16']['tflop_s']} TFLOP/s")
     except Exception as e:
         out["conv_large_f16"] = {"error": repr(e)}
+    try:
+        out["conv_large_bf16"] = bench_conv_large(50, "bf16")
+        log(f"large conv bf16: {out['conv_large_bf16']['tflop_s']} TFLOP/s")
+    except Exception as e:
+        out["conv_large_bf16"] = {"error": repr(e)}
     try:
         out["conv3x3_bias_relu_fp32"] = bench_conv(200)
     except Exception as e:
