@@ -280,6 +280,9 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
     constexpr int CH_A = dma_chunk(A_BYTES / NW), A_IT = A_BYTES / NW / CH_A;
     constexpr int CH_B = dma_chunk(B_BYTES / NW), B_IT = B_BYTES / NW / CH_B;
     constexpr int LOADS = A_IT + B_IT + 1;      // + the bias DMA
+    // two stages: the K loop waits for every load in flight (vmcnt 0), so slices need not carry the
+    // same number of loads and the bias DMA goes out with a tile's first slice only
+    constexpr bool BIAS_ONCE = STAGES == 2;
     constexpr int TI = WM / 32, TJ = WN / 32;   // 32x32 MFMA blocks: m (columns) x n (rows)
     constexpr int WAVES_N = BN / WN;
     static_assert(CPR == 4 || CPR == 8, "BK = 32 or 64");
@@ -461,9 +464,9 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
         for (int i = 0; i < B_IT; i++)
             if (b_lane)
                 __builtin_amdgcn_global_load_lds(q.b[i], LDS_PTR(st + A_BYTES + (wave * B_IT + i) * CH_B), 16, 0, 0);
-        // the tile's bias rides along with every slice (same bytes each time) so every slice has the
-        // same load count; the accumulators of a new tile start from it
-        if (lane < BIAS_LANES)
+        // the tile's bias rides along with its first slice (with every slice when the in-loop waits
+        // count loads: more than two stages); the accumulators of a new tile start from it
+        if (lane < BIAS_LANES && (!BIAS_ONCE || gs % nk == 0))
             __builtin_amdgcn_global_load_lds(q.c, LDS_PTR(st + A_BYTES + B_BYTES + wave * BIAS_LANES * 16), 16, 0, 0);
     };
     auto issue = [&](int gs) __attribute__((always_inline)) {
@@ -500,7 +503,7 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
                 if (b_lane)
                     __builtin_amdgcn_global_load_lds(src, LDS_PTR(st + A_BYTES + (wave * B_IT + x - A_IT) * CH_B), 16, 0, 0);
             } else {
-                if (lane < BIAS_LANES)
+                if (lane < BIAS_LANES && (!BIAS_ONCE || gs % nk == 0))
                     __builtin_amdgcn_global_load_lds(c_src, LDS_PTR(st + A_BYTES + B_BYTES + wave * BIAS_LANES * 16), 16, 0, 0);
             }
         });
@@ -622,7 +625,8 @@ __device__ __forceinline__ void gemm_body(const sox_igemm_args& p) {
 
 #pragma unroll
     for (int s = 0; s < STAGES; s++) issue(s);
-    wait_vmcnt<(STAGES - 1) * LOADS>();  // slice 0
+    // slice 0 (loads complete in order; slice 1 carries LOADS - 1 of them when it does not start a tile)
+    wait_vmcnt<(STAGES - 1) * LOADS - (BIAS_ONCE ? 1 : 0)>();
     __builtin_amdgcn_s_barrier();
     init_acc(0);
     read_step(0, 0, fa0, fb0);
