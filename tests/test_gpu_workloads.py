@@ -139,6 +139,24 @@ def test_detector_replay_is_bitwise_stable(hip):
             assert np.array_equal(s.run(), direct)
 
 
+@pytest.mark.parametrize("storage", ["f16", "bf16"])
+def test_detector_head_convt_pair_matches_unfused(hip, storage, monkeypatch):
+    """The full 960 x 960 detector with its head's two ConvTransposes in one kernel (sox_convt2_*) equals
+    the detector with them as two dispatches, bit for bit: 61 against 62 dispatches."""
+    plan, ins = graphs.dbnet()
+    g = hip.graph(plan, storage)
+    assert g.kernels[-1] == f"sox_convt2_{storage}_n3" and len(g.dispatches) == 61, g.kernels[-3:]
+    g.release()
+    fused = run_gpu(hip, plan, ins, storage)
+    monkeypatch.setenv("SIMDONNX_HIP_NO_CONVT_CHAIN", "1")
+    g = hip.graph(plan, storage)
+    assert g.kernels[-1] == f"sox_convt_one_{storage}" and len(g.dispatches) == 62, g.kernels[-3:]
+    g.release()
+    unfused = run_gpu(hip, plan, ins, storage)
+    assert fused.shape == (1, 960, 960, 1)
+    assert fused.tobytes() == unfused.tobytes(), f"max diff {np.abs(fused - unfused).max()}"
+
+
 @pytest.mark.parametrize("split", ["0", "1"], ids=["whole", "split"])
 @pytest.mark.parametrize("rows,dim,hidden,residual", [(2560, 192, 768, True), (333, 128, 512, True), (70, 64, 256, False)])
 def test_fused_mlp_matches_unfused_and_oracle(hip, rows, dim, hidden, residual, split, monkeypatch):
