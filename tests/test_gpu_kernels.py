@@ -856,21 +856,26 @@ def test_conv_large_channels(hip, storage, kernel, monkeypatch):
 
 
 @pytest.mark.parametrize("storage", ["f16", "bf16"])
-@pytest.mark.parametrize("shape,mode", [((1, 48, 40), 0), ((2, 33, 31), 0), ((2, 33, 31), 1)],
-                         ids=["48x40", "2x33x31-ragged", "2x33x31-reflect"])
-def test_conv_256x256_tile_matches_256x128(hip, storage, shape, mode, monkeypatch):
+@pytest.mark.parametrize("shape,mode,act,res", [((1, 48, 40), 0, "relu", False), ((2, 33, 31), 0, "relu", False),
+                                                ((2, 33, 31), 1, "relu", False), ((1, 48, 40), 0, "gelu", False),
+                                                ((2, 33, 31), 0, "relu", True)],
+                         ids=["48x40", "2x33x31-ragged", "2x33x31-reflect", "48x40-gelu", "2x33x31-residual"])
+def test_conv_256x256_tile_matches_256x128(hip, storage, shape, mode, act, res, monkeypatch):
     """The 256 x 256 conv tile (8 waves of 128 x 64, 32-bit input offsets, 16-byte stores from
-    registers) and the 256 x 128 one (image-base pointers, LDS-staged stores) run the same k-steps in
-    the same order from the same bias: the outputs are equal bit for bit, on whole and ragged row
-    tiles, with zero and reflect padding (the second image's reflected rows find their image's base
-    from the 32-bit offset); the reflect case also against the oracle."""
+    registers; 8-byte stores with a residual) and the 256 x 128 one (image-base pointers, LDS-staged
+    stores; register stores with a residual) run the same k-steps in the same order from the same bias
+    and round the activation to fp32 before the 16-bit conversion: the outputs are equal bit for bit,
+    on whole and ragged row tiles, with zero and reflect padding (the second image's reflected rows find
+    their image's base from the 32-bit offset), GELU, and a fused residual Add; the reflect case also
+    against the oracle."""
     from oracle.interp import _bf16
     n, h, w = shape
     cv = f16 if storage == "f16" else _bf16
     x = cv(synth.normal(65, 3, (n, h, w, 256), 1.0))
     wt = cv(synth.he_normal(65, 1, (256, 256, 3, 3)))
     b = synth.uniform(65, 2, (256,), -0.1, 0.1)
-    plan, ins = conv_plan(x, wt, b, None, (1, 1), (1, 1, 1, 1), "relu", mode, 0.0)
+    add = cv(synth.uniform(65, 4, (n, h, w, 256), -1, 1)) if res else None
+    plan, ins = conv_plan(x, wt, b, add, (1, 1), (1, 1, 1, 1), act, mode, 0.0)
     outs = []
     for k in ("sox_conv_f16_256x256_w8k64s2", "sox_conv_f16_256x128_w8k64s2"):
         monkeypatch.setenv("SIMDONNX_HIP_CONV", k)
