@@ -224,10 +224,10 @@ extern "C" __global__ void __launch_bounds__(256) sox_dw_bf16_v5(sox_dw_args p) 
 extern "C" __global__ void __launch_bounds__(256) sox_dw_f32_v3(sox_dw_args p) { dw_body_k<float, 4, 3>(p); }
 extern "C" __global__ void __launch_bounds__(256) sox_dw_f32_v5(sox_dw_args p) { dw_body_k<float, 4, 5>(p); }
 // Depthwise K x K, stride S, over LDS tiles (any storage type). A workgroup owns an output tile of
-// 8 x 8 pixels of 64 channels (8 vectors of 8): it stages the tile's input halo
-// ((8 - 1) S + K rows x (TW - 1) S + K columns, 8-channel vectors, constant-0 or reflected
+// TH x 8 pixels (TH = 8, or 4 for small maps) of 64 channels (8 vectors of 8): it stages the tile's
+// input halo ((TH - 1) S + K rows x (8 - 1) S + K columns, 8-channel vectors, constant-0 or reflected
 // padding, channels past c as zeros) and the 64 channels' K x K weights in LDS in one round trip,
-// then each thread computes one channel vector of NP = 2 horizontally adjacent pixels, tap row
+// then each thread computes one channel vector of NP = TH / 4 horizontally adjacent pixels, tap row
 // by tap row, keeping the row's input vectors in registers: every input byte is read from memory
 // once per tile instead of once per tap (K^2 times), and the weights once per workgroup.
 // Accumulation per pixel is bias, then the taps in row-major order (one fma each), as dw_body.
@@ -235,8 +235,9 @@ extern "C" __global__ void __launch_bounds__(256) sox_dw_f32_v5(sox_dw_args p) {
 // hit different banks.
 // GAP (p.gap): the channel sums of the tile's stored outputs (after rounding to T), over the
 // thread's pixels and then the tile's 32 pixel lanes in a fixed order, to part[b][tile][c].
-template <typename T, int K, int S> struct DwtShape {
-    static constexpr int TH = 8, TW = 8, NP = TW / 4;                   // tile; pixels per thread
+template <typename T, int K, int S, int TH_ = 8> struct DwtShape {
+    // tile: TH_ (8 or 4) rows x 8 columns; the 32 pixel lanes take NP pixels of one row each
+    static constexpr int TH = TH_, TW = 8, NP = TH * TW / 32;
     static constexpr int HH = (TH - 1) * S + K, HW = (TW - 1) * S + K;  // halo
     static constexpr int VB = 8 * sizeof(T), PB = 8 * VB;              // bytes of a channel vector, a pixel
     static constexpr int RP = ((HW * PB / 128) | 1) * 128;              // halo row pitch: an odd number of 128 B
@@ -260,9 +261,9 @@ __device__ __forceinline__ DwtCoords dwt_coords() {
     return DwtCoords{rest % tiles, v % groups, rest / tiles};
 }
 
-template <typename T, int K, int S, bool GAP, bool COH = false>
+template <typename T, int K, int S, bool GAP, bool COH = false, int TH_ = 8>
 __device__ __forceinline__ void dwt_body(const sox_dwt_args& p, unsigned char* lds) {
-    typedef DwtShape<T, K, S> D;
+    typedef DwtShape<T, K, S, TH_> D;
     constexpr int TH = D::TH, TW = D::TW, NP = D::NP, HH = D::HH, HW = D::HW, VB = D::VB, PB = D::PB, RP = D::RP;
     constexpr int XR = (NP - 1) * S + K;  // input vectors of one tap row
     typedef vec_t<T, 8> T8;
@@ -287,7 +288,7 @@ __device__ __forceinline__ void dwt_body(const sox_dwt_args& p, unsigned char* l
     float bv[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) bv[e] = hb ? p.bias[c0 + e] : 0.0f;
-    const int orow = pl & 7, ocol = (pl >> 3) * NP;  // thread pixel lanes: row, first of NP columns
+    const int orow = pl % TH, ocol = (pl / TH) * NP;  // thread pixel lanes: row, first of NP columns
     const int oy = ty0 + orow;
     T8 rv[NP];
 #pragma unroll
@@ -417,6 +418,30 @@ SOX_DWT(f32, float, 3, 1)
 SOX_DWT(f32, float, 3, 2)
 SOX_DWT(f32, float, 5, 1)
 SOX_DWT(f32, float, 5, 2)
+
+// 4 x 8 tiles (one pixel per thread): twice the workgroups of the 8 x 8 form, for maps too small to
+// fill the GPU with 8 x 8 tiles (the 40 x 40 / 20 x 20 levels of MobileNetV3-small at 640, the 60 x 60 /
+// 30 x 30 ones of the detector)
+#define SOX_DWT_H4(TY, T, K, S)                                                                                \
+    extern "C" __global__ void __launch_bounds__(256) sox_dwt_##TY##_k##K##s##S##_h4(sox_dwt_args p) {     \
+        __shared__ __attribute__((aligned(16))) unsigned char lds[DwtShape<T, K, S, 4>::LDS];               \
+        if (p.gap)                                                                                             \
+            dwt_body<T, K, S, true, false, 4>(p, lds);                                                         \
+        else                                                                                                   \
+            dwt_body<T, K, S, false, false, 4>(p, lds);                                                        \
+    }
+SOX_DWT_H4(f16, half_t, 3, 1)
+SOX_DWT_H4(f16, half_t, 3, 2)
+SOX_DWT_H4(f16, half_t, 5, 1)
+SOX_DWT_H4(f16, half_t, 5, 2)
+SOX_DWT_H4(bf16, bf16_t, 3, 1)
+SOX_DWT_H4(bf16, bf16_t, 3, 2)
+SOX_DWT_H4(bf16, bf16_t, 5, 1)
+SOX_DWT_H4(bf16, bf16_t, 5, 2)
+SOX_DWT_H4(f32, float, 3, 1)
+SOX_DWT_H4(f32, float, 3, 2)
+SOX_DWT_H4(f32, float, 5, 1)
+SOX_DWT_H4(f32, float, 5, 2)
 
 
 extern "C" __global__ void __launch_bounds__(256) sox_dw_f16_v(sox_dw_args p) { dw_body<half_t, 8>(p); }

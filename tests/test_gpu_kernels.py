@@ -124,11 +124,14 @@ DW_TILE_CASES = [  # (c, k, s, h, w, pad_mode, act, residual)
     (16, 3, 2, 33, 17, 1, "relu", False), (576, 5, 1, 30, 30, 0, "hardswish", True), (120, 5, 2, 9, 23, 1, "swish", False)]
 
 
+@pytest.mark.parametrize("rows", [8, 4], ids=["8x8", "4x8"])
 @pytest.mark.parametrize("storage", ["f16", "bf16", "f32"])
 @pytest.mark.parametrize("case", DW_TILE_CASES, ids=[f"c{c[0]}k{c[1]}s{c[2]}_{c[3]}x{c[4]}" for c in DW_TILE_CASES])
-def test_depthwise_tiles_match_per_pixel_kernel(hip, case, storage, monkeypatch):
-    """The LDS-tile depthwise kernels (sox_dwt_*: channel tails, reflect padding, residual, ragged
-    tiles) give the per-pixel kernel's bits (same fma order per output) and meet the oracle."""
+def test_depthwise_tiles_match_per_pixel_kernel(hip, case, storage, rows, monkeypatch):
+    """The LDS-tile depthwise kernels (sox_dwt_*: 8 x 8 and 4 x 8 tiles, channel tails, reflect
+    padding, residual, ragged tiles) give the per-pixel kernel's bits (same fma order per output) and
+    meet the oracle."""
+    monkeypatch.setenv("SIMDONNX_HIP_DWT_ROWS", str(rows))
     c, k, s, h, w, mode, act, res = case
     from oracle.interp import _bf16
     rnd = {"f16": f16, "bf16": _bf16, "f32": lambda a: a}[storage]
@@ -139,7 +142,7 @@ def test_depthwise_tiles_match_per_pixel_kernel(hip, case, storage, monkeypatch)
     add = rnd(synth.uniform(41, 4, (1, oh, ow, c), -1, 1)) if res else None
     plan, ins = conv_plan(x, wt, b, add, (s, s), (k // 2,) * 4, act, mode, 0.0, group=c)
     g = hip.graph(plan, storage)
-    assert g.kernels == [f"sox_dwt_{storage}_k{k}s{s}"], g.kernels
+    assert g.kernels == [f"sox_dwt_{storage}_k{k}s{s}" + ("_h4" if rows == 4 else "")], g.kernels
     g.release()
     tiled = run(hip, plan, ins, storage)
     monkeypatch.setenv("SIMDONNX_HIP_DW_DIRECT", "1")

@@ -80,6 +80,7 @@ def test_se_in_depthwise_launch_matches_separate_passes(hip, case, storage, monk
     replays = _runs(g, x, 3, replay=True)
     g.release()
     monkeypatch.delenv("SIMDONNX_HIP_SE_IN_DW")
+    monkeypatch.setenv("SIMDONNX_HIP_DWT_ROWS", "8")  # the fused gate's tiling: the same GAP partial sums
     g2 = hip.graph(plan, storage)
     labels2 = [d[0] for d in g2.dispatches]
     assert "depthwise_se" not in labels2 and "se_gate" in labels2, labels2
