@@ -20,8 +20,9 @@ Also reported on the same line:
                 ms per image of the whole networks (HIP-graph replay), per-kernel-class roofline
   conv3x3       the fp32 Conv3x3 + bias + ReLU 1x64x64x64 kernel (us, TFLOP/s)
   conv_large_f16 / conv_large_bf16
-                the Conv3x3 + bias + ReLU over 8x128x128, 256 -> 256 channels (154.6 GFLOP) on the LDS-DMA
-                ring in fp16 / bf16 storage, against the dense MFMA peak
+                the Conv3x3 + bias + ReLU over 8x128x128, 256 -> 256 channels (154.6 GFLOP) on the halo
+                tile (input halos in LDS, weights through an LDS-DMA ring) in fp16 / bf16 storage, against
+                the dense MFMA peak
   ops           the kernels of the rest of the ExecOp surface (resize, pad, transpose, slice, unary,
                 depth-space, pools, MatMul) at detector / recognizer sizes, GB/s vs the HBM peak
   hbm_kernels   the convnets' bandwidth-bound kernels (depthwise 5x5 s1 / 3x3 s2, the SE passes, nearest,
@@ -250,8 +251,9 @@ def bench_lds_peak(iters: int = 2000, reps: int = 10):
 
 
 def bench_conv_large(steps: int, storage="f16"):
-    """A large implicit-GEMM conv on the LDS-DMA ring: Conv3x3 s1 p1 + bias + ReLU, NHWC, 8x128x128,
-    256 -> 256 channels (154.6 GFLOP), 16-bit storage, against the dense MFMA peak."""
+    """A large conv: Conv3x3 s1 p1 + bias + ReLU, NHWC, 8x128x128, 256 -> 256 channels (154.6 GFLOP),
+    16-bit storage, against the dense MFMA peak (the backend's choice, reported in `kernels`: the halo
+    tile, or the implicit-GEMM ring under SIMDONNX_HIP_NO_H256)."""
     from simdonnx_amd import synth
     from simdonnx_amd.backend import HipBackend, HipInferenceSession
     from simdonnx_amd.plan import NHWC, PlanBuilder

@@ -840,9 +840,9 @@ def test_gemm_pp_matches_ring_bitwise(hip, m, n, act, bias, storage, monkeypatch
                          ids=["default", "w8-256x128", "w8-256x256"])
 @pytest.mark.parametrize("storage", ["f16", "bf16"])
 def test_conv_large_channels(hip, storage, kernel, monkeypatch):
-    """The large implicit-GEMM conv the bench times (3x3 s1 p1 + bias + ReLU, 256 -> 256 channels on
-    the LDS-DMA ring), at batch 1 and 48x40 so the oracle stays quick; also forced onto the 8-wave
-    tiling the bench's 8x128x128 size selects."""
+    """The large conv of the bench (3x3 s1 p1 + bias + ReLU, 256 -> 256 channels), at batch 1 and 48x40
+    so the oracle stays quick, on the default route and forced onto the ring's 8-wave tilings (the
+    bench's 8x128x128 size takes the halo tile, tested by test_conv_halo_tile_matches_ring)."""
     if kernel:
         monkeypatch.setenv("SIMDONNX_HIP_CONV", kernel)
     from oracle.interp import _bf16
@@ -890,6 +890,39 @@ def test_conv_256x256_tile_matches_256x128(hip, storage, shape, mode, act, res, 
     if mode:
         want = O.conv(x, wt, b, stride=(1, 1), pads=(1, 1, 1, 1), act="relu", pad_mode=mode)
         assert max_rel(outs[0], want) < (TOL[True] if storage == "f16" else 4e-3)
+
+
+# (batch, h, w, ic, oc, act, residual): 3x3 convs on the halo tile (sox_conv_*_h256): ragged row tiles
+# (h % 8 != 0), one and four 64-channel blocks, two 256-channel blocks of output (grid.y = 2), GELU and
+# a fused residual (8-byte stores), several tiles per workgroup
+H256_CASES = [(2, 33, 64, 256, 256, "relu", False), (1, 16, 32, 64, 256, "gelu", False),
+              (1, 19, 96, 128, 512, "relu", False), (2, 24, 32, 192, 256, "none", True)]
+
+
+@pytest.mark.parametrize("storage", ["f16", "bf16"])
+@pytest.mark.parametrize("case", H256_CASES, ids=lambda c: "x".join(str(v) for v in c[:5]) + f"-{c[5]}" + ("-res" if c[6] else ""))
+def test_conv_halo_tile_matches_ring(hip, storage, case, monkeypatch):
+    """The halo-tile large conv (8 x 32 pixels x 256 channels per workgroup, input halos in LDS) adds
+    each output's channel blocks, taps and k-steps in the implicit-GEMM ring's order from the same
+    bias, so it equals the 256 x 128 ring tile bit for bit, and meets the oracle."""
+    from oracle.interp import _bf16
+    n, h, w, ic, oc, act, res = case
+    cv = f16 if storage == "f16" else _bf16
+    x = cv(synth.normal(66, 3, (n, h, w, ic), 1.0))
+    wt = cv(synth.he_normal(66, 1, (oc, ic, 3, 3)))
+    b = synth.uniform(66, 2, (oc,), -0.1, 0.1)
+    add = cv(synth.uniform(66, 4, (n, h, w, oc), -1, 1)) if res else None
+    plan, ins = conv_plan(x, wt, b, add, (1, 1), (1, 1, 1, 1), act, 0, 0.0)
+    outs = []
+    for k in ("sox_conv_f16_h256", "sox_conv_f16_256x128_w8k64s2"):
+        monkeypatch.setenv("SIMDONNX_HIP_CONV", k)
+        g = hip.graph(plan, storage)
+        assert g.kernels == [k.replace("_f16_", f"_{storage}_")], g.kernels
+        g.release()
+        outs.append(run(hip, plan, ins, storage))
+    assert outs[0].tobytes() == outs[1].tobytes(), f"max diff {np.abs(outs[0] - outs[1]).max()}"
+    want = O.conv(x, wt, b, add, stride=(1, 1), pads=(1, 1, 1, 1), act=act)
+    assert max_rel(outs[0], want) < (TOL[True] if storage == "f16" else 4e-3)
 
 
 # (batch, ic, oc1, h, w, bn): two chained 2x2 ConvTransposes, the second to one channel (the DB head's

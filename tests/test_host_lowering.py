@@ -203,10 +203,32 @@ def _conv3x3_256(n, h, w):
     return pb.build(y)
 
 
+def test_large_conv_takes_the_halo_tile(offline, monkeypatch):
+    """A large 3x3 stride-1 conv over 256 channels takes the halo tile (sox_conv_*_h256) when its rows are
+    whole 32-pixel blocks, the ring otherwise or under SIMDONNX_HIP_NO_H256; forcing the halo tile onto a
+    conv it does not take is refused at graph creation."""
+    for storage in ("f16", "bf16"):
+        g = offline.graph(_conv3x3_256(2, 256, 256), storage)
+        assert g.kernels == [f"sox_conv_{storage}_h256"], g.kernels
+        g.release()
+    g = offline.graph(_conv3x3_256(2, 256, 264), "f16")  # 264 = 8.25 blocks of 32 pixels
+    assert g.kernels == ["sox_conv_f16_256x256_w8k64s2"], g.kernels
+    g.release()
+    monkeypatch.setenv("SIMDONNX_HIP_NO_H256", "1")
+    g = offline.graph(_conv3x3_256(2, 256, 256), "f16")
+    assert g.kernels == ["sox_conv_f16_256x256_w8k64s2"], g.kernels
+    g.release()
+    monkeypatch.delenv("SIMDONNX_HIP_NO_H256")
+    monkeypatch.setenv("SIMDONNX_HIP_CONV", "sox_conv_f16_h256")
+    with pytest.raises(N.NotSupportedError):
+        offline.graph(_conv3x3_256(2, 256, 264), "f16")
+
+
 def test_large_conv_tile_takes_inputs_under_2_pow_31_elements(offline, monkeypatch):
     """The 256x256 conv tile keeps one 32-bit offset into the whole input per DMA row: a large conv takes
     it below 2^31 input elements and the 256x128 tile (64-bit image bases) from there; forcing the
     256x256 tile onto a larger input is refused at graph creation, not run."""
+    monkeypatch.setenv("SIMDONNX_HIP_NO_H256", "1")  # the ring's choice
     g = offline.graph(_conv3x3_256(2, 256, 256), "f16")
     assert g.kernels == ["sox_conv_f16_256x256_w8k64s2"], g.kernels
     g.release()
