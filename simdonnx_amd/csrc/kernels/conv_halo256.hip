@@ -46,7 +46,7 @@ __device__ __forceinline__ void conv_h256_body(const sox_igemm_args& p) {
 
     const int N = p.n, ic = p.ic, ih = p.ih, iw = p.iw, oh = p.oh, ow = p.ow;
     const int n0 = blockIdx.y * 256;
-    const int tiles_x = ow / TW, tiles_y = (oh + TH - 1) / TH, per_img = tiles_x * tiles_y;
+    const int tiles_x = (ow + TW - 1) / TW, tiles_y = (oh + TH - 1) / TH, per_img = tiles_x * tiles_y;
     const int ntiles = (p.m / (oh * ow)) * per_img;
     const int ncb = ic / 64, nk = ncb * 9;
     const T* __restrict__ X = (const T*)p.x;
@@ -138,20 +138,23 @@ __device__ __forceinline__ void conv_h256_body(const sox_igemm_args& p) {
         });
     };
 
-    // tile k's outputs: activation (+ residual) and stores from the accumulators, rows past oh skipped
+    // tile k's outputs: activation (+ residual) and stores from the accumulators; rows past oh are
+    // skipped, and in the last column tile of a row whose width is not a multiple of 32 the pixels past
+    // ow (lanes l32 >= ow - ox0: their m would run into the next row) by a row-local bound on m
     auto epilogue = [&](int k) __attribute__((always_inline)) {
         int b, oy0, ox0;
         origin(k, b, oy0, ox0);
+        const int valid = min(TW, ow - ox0);
         static_for<0, 4>([&](auto rr) {
             constexpr int pr = decltype(rr)::value;
             const int oy = oy0 + 4 * ph + pr;
             if (oy < oh) {
-                const int m0 = (b * oh + oy) * ow + ox0, nw = n0 + oq * 64;
+                const int m0 = (b * oh + oy) * ow + ox0, mb = m0 + valid, nw = n0 + oq * 64;
                 switch (act) {
-                    case SOX_ACT_NONE: store_tile<T, SOX_ACT_NONE, 2, 1, false, true>(Y, R, p.ldy, p.m, N, m0, nw, acc[pr]); break;
-                    case SOX_ACT_RELU: store_tile<T, SOX_ACT_RELU, 2, 1, false, true>(Y, R, p.ldy, p.m, N, m0, nw, acc[pr]); break;
-                    case SOX_ACT_GELU: store_tile<T, SOX_ACT_GELU, 2, 1, false, true>(Y, R, p.ldy, p.m, N, m0, nw, acc[pr]); break;
-                    default: store_tile<T, -1, 2, 1, false, true>(Y, R, p.ldy, p.m, N, m0, nw, acc[pr], act); break;
+                    case SOX_ACT_NONE: store_tile<T, SOX_ACT_NONE, 2, 1, false, true>(Y, R, p.ldy, mb, N, m0, nw, acc[pr]); break;
+                    case SOX_ACT_RELU: store_tile<T, SOX_ACT_RELU, 2, 1, false, true>(Y, R, p.ldy, mb, N, m0, nw, acc[pr]); break;
+                    case SOX_ACT_GELU: store_tile<T, SOX_ACT_GELU, 2, 1, false, true>(Y, R, p.ldy, mb, N, m0, nw, acc[pr]); break;
+                    default: store_tile<T, -1, 2, 1, false, true>(Y, R, p.ldy, mb, N, m0, nw, acc[pr], act); break;
                 }
             }
         });

@@ -893,10 +893,11 @@ def test_conv_256x256_tile_matches_256x128(hip, storage, shape, mode, act, res, 
 
 
 # (batch, h, w, ic, oc, act, residual): 3x3 convs on the halo tile (sox_conv_*_h256): ragged row tiles
-# (h % 8 != 0), one and four 64-channel blocks, two 256-channel blocks of output (grid.y = 2), GELU and
-# a fused residual (8-byte stores), several tiles per workgroup
+# (h % 8 != 0), partial column tiles (w % 32 != 0), one and four 64-channel blocks, two 256-channel
+# blocks of output (grid.y = 2), GELU and a fused residual (8-byte stores), several tiles per workgroup
 H256_CASES = [(2, 33, 64, 256, 256, "relu", False), (1, 16, 32, 64, 256, "gelu", False),
-              (1, 19, 96, 128, 512, "relu", False), (2, 24, 32, 192, 256, "none", True)]
+              (1, 19, 96, 128, 512, "relu", False), (2, 24, 32, 192, 256, "none", True),
+              (2, 17, 40, 128, 256, "relu", False), (1, 9, 71, 64, 256, "gelu", True)]
 
 
 @pytest.mark.parametrize("storage", ["f16", "bf16"])

@@ -194,26 +194,25 @@ def test_upsample_add_input_survives_fused_writes(offline, storage):
         g.release()
 
 
-def _conv3x3_256(n, h, w):
+def _conv3x3_256(n, h, w, stride=1):
     import numpy as np
     from simdonnx_amd.plan import NHWC, PlanBuilder
     pb = PlanBuilder()
     x = pb.input((n, 256, h, w), NHWC, "x")
-    y = pb.conv(x, np.zeros((256, 256, 3, 3), np.float32), np.zeros(256, np.float32), pad=1, act="relu", name="c")
+    y = pb.conv(x, np.zeros((256, 256, 3, 3), np.float32), np.zeros(256, np.float32), stride=stride, pad=1, act="relu",
+                name="c")
     return pb.build(y)
 
 
 def test_large_conv_takes_the_halo_tile(offline, monkeypatch):
-    """A large 3x3 stride-1 conv over 256 channels takes the halo tile (sox_conv_*_h256) when its rows are
-    whole 32-pixel blocks, the ring otherwise or under SIMDONNX_HIP_NO_H256; forcing the halo tile onto a
-    conv it does not take is refused at graph creation."""
+    """A large 3x3 stride-1 conv over 256 channels takes the halo tile (sox_conv_*_h256), also with a
+    partial last tile per row (264 = 8.25 tiles of 32 pixels), and the ring under SIMDONNX_HIP_NO_H256;
+    forcing the halo tile onto a conv it does not take (stride 2) is refused at graph creation."""
     for storage in ("f16", "bf16"):
-        g = offline.graph(_conv3x3_256(2, 256, 256), storage)
-        assert g.kernels == [f"sox_conv_{storage}_h256"], g.kernels
-        g.release()
-    g = offline.graph(_conv3x3_256(2, 256, 264), "f16")  # 264 = 8.25 blocks of 32 pixels
-    assert g.kernels == ["sox_conv_f16_256x256_w8k64s2"], g.kernels
-    g.release()
+        for w in (256, 264):
+            g = offline.graph(_conv3x3_256(2, 256, w), storage)
+            assert g.kernels == [f"sox_conv_{storage}_h256"], g.kernels
+            g.release()
     monkeypatch.setenv("SIMDONNX_HIP_NO_H256", "1")
     g = offline.graph(_conv3x3_256(2, 256, 256), "f16")
     assert g.kernels == ["sox_conv_f16_256x256_w8k64s2"], g.kernels
@@ -221,7 +220,7 @@ def test_large_conv_takes_the_halo_tile(offline, monkeypatch):
     monkeypatch.delenv("SIMDONNX_HIP_NO_H256")
     monkeypatch.setenv("SIMDONNX_HIP_CONV", "sox_conv_f16_h256")
     with pytest.raises(N.NotSupportedError):
-        offline.graph(_conv3x3_256(2, 256, 264), "f16")
+        offline.graph(_conv3x3_256(2, 256, 256, stride=2), "f16")
 
 
 def test_large_conv_tile_takes_inputs_under_2_pow_31_elements(offline, monkeypatch):
